@@ -1,0 +1,126 @@
+/*
+ * tabby_sampler -- C ABI of the MI355X (gfx950) token sampler.
+ *
+ * For each row of logits it computes, in one stream-ordered launch sequence:
+ *   maxLogit, sumExp = sum exp(x - maxLogit) over the whole row, the exact top-k
+ *   (value descending, ties to the lower index), and then sampleFromTopK's temperature /
+ *   top-p / categorical draw from a caller-supplied uniform.
+ *
+ * It replaces, in the reference (xOAviOx/tabby):
+ *   - ForwardPass.encodeSampling            src/engine/forward.ts:522-601   (GPU head)
+ *   - the sample-block readback + decode    src/engine/forward.ts:142-157, 442-451
+ *   - sampleFromTopK                        src/engine/sampler.ts:147-212   (CPU tail)
+ * composed as the worker does (src/worker/inference.worker.ts:162-168), for many rows at once.
+ *
+ * Conventions: plain C types only; every function returns a tabby_status; device pointers
+ * are owned by the caller, scratch is owned by the handle; one handle per host thread and
+ * stream (calls on one handle must not overlap). tabby_last_error() gives the message of
+ * the calling thread's most recent failure.
+ */
+#ifndef TABBY_SAMPLER_H
+#define TABBY_SAMPLER_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define TABBY_API __attribute__((visibility("default")))
+#else
+#define TABBY_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  TABBY_OK = 0,
+  TABBY_EINVAL = 1,    /* bad argument; e.g. topK outside [0, k_max] (forward.ts:348-351) */
+  TABBY_EHIP = 2,      /* HIP runtime / launch failure */
+  TABBY_EEMPTY = 3,    /* empty candidate pool (sampler.ts:153) */
+  TABBY_EDOMAIN = 4,   /* row outside the contract: NaN, +inf, or every entry -inf */
+  TABBY_ECAPACITY = 5  /* request exceeds what the handle was created for */
+} tabby_status;
+
+typedef enum { TABBY_F32 = 0, TABBY_F16 = 1 } tabby_dtype;
+
+/* Per-row sampling parameters: SamplingParams (sampler.ts:83-98) plus the uniform that
+ * SeededRandom.next() (sampler.ts:112-118) would return for this row. All f64, as JS
+ * numbers are: 0.9 as f32 is not 0.9, and a mulberry32 draw has 32 significant bits. */
+typedef struct {
+  double temperature; /* <= 0: greedy, the uniform is not used (sampler.ts:159-167) */
+  double top_p;       /* >= 1: no nucleus cut (sampler.ts:177) */
+  double uniform;     /* in [0, 1) */
+  int32_t top_k;      /* 1..k_max candidates; 0 = the whole vocabulary */
+  int32_t reserved;   /* must be 0 */
+} tabby_row_params;
+
+/* Per-row result: SampleOutcome (sampler.ts:121-135) plus the TopKResult header
+ * (forward.ts:93-103). */
+typedef struct {
+  int32_t id;            /* chosen token id */
+  uint32_t considered;   /* consideredCount: candidates that survived top-p */
+  double probability;    /* exp(l - maxLogit) / sumExp of the chosen id */
+  double pool_mass;      /* full-vocabulary mass of the k candidates */
+  float max_logit;       /* largest logit of the row */
+  int32_t pool_exhausted;/* 1 when poolMass < topP (top-p clipped by k) */
+  double sum_exp;        /* sum over the row of exp(x - maxLogit) */
+  int32_t status;        /* tabby_status of this row */
+  int32_t topk_count;    /* entries written to the row's top-k output, if requested */
+} tabby_row_result;
+
+typedef struct tabby_sampler tabby_sampler;
+
+/* Allocates the scratch a ForwardPass allocates for sampling (forward.ts:243-248), sized
+ * for up to rows_max rows of up to vocab_max entries and top_k up to k_max (<= 1024).
+ * `device` is a HIP device ordinal. */
+TABBY_API int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_t k_max,
+                         tabby_sampler **out);
+
+/* Frees the handle's scratch (ForwardPass.destroy, forward.ts:309-315). NULL is a no-op. */
+TABBY_API int tabby_sampler_destroy(tabby_sampler *sampler);
+
+/*
+ * Device-resident form: logits_dev is [rows, vocab] row-major of `dtype`; params_dev and
+ * results_dev have `rows` entries in device memory. If topk_cap > 0, topk_ids_dev and
+ * topk_logits_dev ([rows, topk_cap]) receive each row's candidates, highest first (the
+ * TopKResult ids/logits, forward.ts:93-103). Asynchronous on `stream` (a hipStream_t, NULL
+ * for the default stream). Parameters are validated on the device: a bad row gets a
+ * nonzero status and the other rows are still sampled.
+ * `flags`: TABBY_FLAG_FULL_VOCAB must be set if any row may have top_k = 0 (or >= vocab).
+ */
+#define TABBY_FLAG_FULL_VOCAB 1u
+TABBY_API int tabby_sampler_sample_device(tabby_sampler *sampler, const void *logits_dev, int32_t dtype,
+                                int32_t rows, int32_t vocab, const tabby_row_params *params_dev,
+                                tabby_row_result *results_dev, int32_t *topk_ids_dev,
+                                float *topk_logits_dev, int32_t topk_cap, uint32_t flags,
+                                void *stream);
+
+/*
+ * Host-parameter form, the decode-loop entry (forward.ts:430-451 + inference.worker.ts:162-168):
+ * params_host are validated before any GPU work (TABBY_EINVAL with the reference's
+ * "topK must be between 0 and <k_max>, got <k>" message), uploaded, sampled, and
+ * results_host (and the optional top-k arrays, host memory) are filled when it returns.
+ * Returns the first nonzero row status, if any.
+ */
+TABBY_API int tabby_sampler_sample(tabby_sampler *sampler, const void *logits_dev, int32_t dtype,
+                         int32_t rows, int32_t vocab, const tabby_row_params *params_host,
+                         tabby_row_result *results_host, int32_t *topk_ids_host,
+                         float *topk_logits_host, int32_t topk_cap, void *stream);
+
+/* Message of the calling thread's last failure ("" if none). */
+TABBY_API const char *tabby_last_error(void);
+
+/* Library version string. */
+TABBY_API const char *tabby_version(void);
+
+/*
+ * Diagnostic: y[i] = exp(x[i]) over device arrays with the device's f64 exp, the fdlibm
+ * method that V8's Math.exp uses (the exp of sampler.ts:156,170). For parity tests.
+ */
+TABBY_API int tabby_debug_exp(const double *x_dev, double *y_dev, int64_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TABBY_SAMPLER_H */

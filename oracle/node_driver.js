@@ -1,0 +1,124 @@
+'use strict';
+/*
+ * Command-line driver for the Node restatement -- TEST INFRASTRUCTURE ONLY.
+ *
+ *   node node_driver.js exp IN.f64 OUT.f64          Math.exp over a file of f64
+ *   node node_driver.js mulberry SEED N OUT.f64     N draws of SeededRandom(SEED)
+ *   node node_driver.js sample SPEC.json            rows of an f32 file through sampleRow
+ *   node node_driver.js bench SPEC.json             time sampleRow (single thread, or
+ *                                                   worker_threads when spec.threads > 1)
+ *
+ * SPEC.json: {logits: path (f32, row-major), rows, vocab, topK[], temperature[], topP[],
+ *             uniform[], out: path (JSON outcomes), threads, seconds}
+ */
+const fs = require('fs');
+const os = require('os');
+const path = require('path');
+const oracle = require('./sampler_oracle.js');
+
+function readF64(file) {
+  const buf = fs.readFileSync(file);
+  return new Float64Array(buf.buffer, buf.byteOffset, buf.byteLength / 8);
+}
+
+function writeF64(file, arr) {
+  fs.writeFileSync(file, Buffer.from(arr.buffer, arr.byteOffset, arr.byteLength));
+}
+
+function readRows(spec) {
+  const buf = fs.readFileSync(spec.logits);
+  const all = new Float32Array(buf.buffer, buf.byteOffset, buf.byteLength / 4);
+  const rows = [];
+  for (let r = 0; r < spec.rows; r++) rows.push(all.subarray(r * spec.vocab, (r + 1) * spec.vocab));
+  return rows;
+}
+
+function paramsOf(spec, r) {
+  return { temperature: spec.temperature[r], topK: spec.topK[r], topP: spec.topP[r], seed: 0 };
+}
+
+function runRows(spec, rows, first, count) {
+  const out = [];
+  for (let i = 0; i < count; i++) {
+    const r = (first + i) % spec.rows;
+    out.push(oracle.sampleRow(rows[r], paramsOf(spec, r), spec.uniform[r]));
+  }
+  return out;
+}
+
+function benchSingle(spec, rows) {
+  // Rows are cycled until the time budget is spent; inputs were generated outside.
+  const budgetMs = 1000 * (spec.seconds || 10);
+  const started = process.hrtime.bigint();
+  let done = 0;
+  for (;;) {
+    runRows(spec, rows, done, 1);
+    done++;
+    const elapsedMs = Number(process.hrtime.bigint() - started) / 1e6;
+    if (elapsedMs >= budgetMs || (spec.maxRows && done >= spec.maxRows)) {
+      return { rows: done, seconds: elapsedMs / 1000 };
+    }
+  }
+}
+
+function main() {
+  const cmd = process.argv[2];
+  if (cmd === 'exp') {
+    const x = readF64(process.argv[3]);
+    const y = new Float64Array(x.length);
+    for (let i = 0; i < x.length; i++) y[i] = Math.exp(x[i]);
+    writeF64(process.argv[4], y);
+  } else if (cmd === 'mulberry') {
+    const rng = new oracle.SeededRandom(Number(process.argv[3]));
+    const n = Number(process.argv[4]);
+    const y = new Float64Array(n);
+    for (let i = 0; i < n; i++) y[i] = rng.next();
+    writeF64(process.argv[5], y);
+  } else if (cmd === 'sample') {
+    const spec = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
+    const rows = readRows(spec);
+    fs.writeFileSync(spec.out, JSON.stringify(runRows(spec, rows, 0, spec.rows)));
+  } else if (cmd === 'bench') {
+    const spec = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
+    const threads = spec.threads || 1;
+    if (threads <= 1) {
+      const rows = readRows(spec);
+      const r = benchSingle(spec, rows);
+      process.stdout.write(JSON.stringify({
+        rows: r.rows, seconds: r.seconds, rowsPerSec: r.rows / r.seconds, threads: 1,
+        node: process.version, cpu: os.cpus()[0].model,
+      }) + '\n');
+      return;
+    }
+    const { Worker } = require('worker_threads');
+    const results = [];
+    let pending = threads;
+    const started = process.hrtime.bigint();
+    for (let t = 0; t < threads; t++) {
+      const w = new Worker(path.join(__dirname, 'node_driver.js'), {
+        argv: ['worker'], workerData: spec,
+      });
+      w.on('message', (m) => {
+        results.push(m);
+        if (--pending === 0) {
+          const wall = Number(process.hrtime.bigint() - started) / 1e9;
+          const rows = results.reduce((a, b) => a + b.rows, 0);
+          process.stdout.write(JSON.stringify({
+            rows, seconds: wall, rowsPerSec: results.reduce((a, b) => a + b.rows / b.seconds, 0),
+            threads, node: process.version, cpu: os.cpus()[0].model,
+          }) + '\n');
+        }
+      });
+      w.on('error', (e) => { process.stderr.write(String(e) + '\n'); process.exit(1); });
+    }
+  } else if (cmd === 'worker') {
+    const { parentPort, workerData } = require('worker_threads');
+    const rows = readRows(workerData);
+    parentPort.postMessage(benchSingle(workerData, rows));
+  } else {
+    process.stderr.write('usage: node node_driver.js exp|mulberry|sample|bench ...\n');
+    process.exit(2);
+  }
+}
+
+main();

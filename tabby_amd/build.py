@@ -1,0 +1,90 @@
+"""Builds the native parts of tabby_amd in-tree.
+
+* ``tabby_amd/lib/libtabby_sampler.so`` -- the HIP kernels and the C ABI of
+  ``include/tabby_sampler.h``, compiled for gfx950 with hipcc.
+* ``tabby_amd/node/build/tabby_sampler.node`` -- the N-API addon that exposes the C ABI to
+  Node (g++ against ``/usr/include/node``), when the Node headers are present.
+
+Run ``python -m tabby_amd.build``. Both outputs are rebuilt on every call.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+LIB_DIR = os.path.join(PKG, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libtabby_sampler.so")
+NODE_DIR = os.path.join(PKG, "node")
+NODE_ADDON = os.path.join(NODE_DIR, "build", "tabby_sampler.node")
+NODE_INCLUDE = "/usr/include/node"
+ARCH = os.environ.get("TABBY_OFFLOAD_ARCH", "gfx950")
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-fvisibility=hidden",
+    # f64 tail: every operation rounds once, in source order (V8 evaluates JS that way).
+    "-ffp-contract=off",
+    # Packed FP32 instructions are kept out of all device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+]
+
+
+def _hipcc() -> str:
+    for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found; the sampler library cannot be built")
+
+
+def build_library(verbose: bool = False) -> str:
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-o", tmp, os.path.join(CSRC, "tabby_sampler.hip")]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr[-6000:]}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def build_node_addon(verbose: bool = False) -> str | None:
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        return None
+    os.makedirs(os.path.dirname(NODE_ADDON), exist_ok=True)
+    tmp = NODE_ADDON + ".tmp"
+    cmd = [
+        shutil.which("g++") or "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+        f"-I{NODE_INCLUDE}", f"-I{INCLUDE}", "-o", tmp, os.path.join(NODE_DIR, "addon.cc"),
+        f"-L{LIB_DIR}", "-ltabby_sampler", "-Wl,-rpath,$ORIGIN/../../lib",
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ (node addon) failed ({r.returncode}):\n{r.stderr[-6000:]}")
+    os.replace(tmp, NODE_ADDON)
+    return NODE_ADDON
+
+
+def build(verbose: bool = False) -> None:
+    build_library(verbose)
+    if os.path.exists(os.path.join(NODE_DIR, "addon.cc")):
+        build_node_addon(verbose)
+
+
+if __name__ == "__main__":
+    build(verbose="-q" not in sys.argv)
+    print("built", LIB_PATH)

@@ -1,0 +1,181 @@
+// Workgroup-level building blocks for the sampler kernels: reductions, scans, the
+// radix select over 64-bit composites, and an LDS bitonic sort.
+//
+// Workgroups are kBlock = 256 lanes = 4 wave64s. Cross-lane steps inside a wave use
+// __shfl_xor / __shfl_up; the cross-wave step goes through a few words of LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tabby {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / 64;
+constexpr int kBins = 2048;  // 11-bit radix digits
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// LDS words the helpers below communicate through. One per workgroup.
+struct BlockScratch {
+  float f[kWaves];
+  double d[kWaves];
+  uint32_t u[kWaves];
+  uint32_t bin, above, count, slot;
+};
+
+__device__ __forceinline__ float block_max(float v, BlockScratch &s) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  __syncthreads();
+  if (lane_id() == 0) s.f[wave_id()] = v;
+  __syncthreads();
+  float r = s.f[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) r = fmaxf(r, s.f[i]);
+  return r;
+}
+
+// Fixed reduction tree, so the result is bit-identical from run to run.
+__device__ __forceinline__ double block_sum(double v, BlockScratch &s) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  __syncthreads();
+  if (lane_id() == 0) s.d[wave_id()] = v;
+  __syncthreads();
+  double r = s.d[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) r += s.d[i];
+  return r;
+}
+
+// Exclusive prefix sum in thread order; *total receives the workgroup sum.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, BlockScratch &s,
+                                                         uint32_t *total) {
+  const int lane = lane_id();
+  uint32_t inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_up(inc, o);
+    if (lane >= o) inc += t;
+  }
+  __syncthreads();
+  if (lane == 63) s.u[wave_id()] = inc;
+  __syncthreads();
+  uint32_t base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    const uint32_t w = s.u[i];
+    base += (i < wave_id()) ? w : 0u;
+    tot += w;
+  }
+  *total = tot;
+  return base + inc - v;
+}
+
+// Given a filled histogram, find the bin b holding the need-th largest element counted
+// from the top: above(b) < need <= above(b) + hist[b]. Thread t owns the PER bins just
+// below kBins - t*PER, so thread order is descending bin order. Publishes b, above(b) and
+// hist[b] in s.bin / s.above / s.count.
+__device__ __forceinline__ void find_bin(const uint32_t *hist, uint32_t need, BlockScratch &s) {
+  constexpr int PER = kBins / kBlock;
+  const int top = kBins - 1 - (int)threadIdx.x * PER;
+  uint32_t c[PER];
+  uint32_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    c[i] = hist[top - i];
+    sum += c[i];
+  }
+  uint32_t total;
+  const uint32_t before = block_exclusive_scan(sum, s, &total);
+  if (before < need && need <= before + sum) {
+    uint32_t acc = before;
+    bool found = false;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (!found && need <= acc + c[i]) {
+        s.bin = (uint32_t)(top - i);
+        s.above = acc;
+        s.count = c[i];
+        found = true;
+      }
+      acc += c[i];
+    }
+  }
+  __syncthreads();
+}
+
+// Radix select on 64-bit composites: finds the threshold such that exactly `need` of the
+// elements visited by for_each satisfy (v >> shift) >= (prefix >> shift). Digits are
+// 11/11/10 bits of the value key, then 11/11/10 bits of the ~index word; a pass that leaves
+// the threshold bin exactly full ends the search early, so index digits are only visited
+// when values tie across the threshold. Requires 1 <= need <= number of elements.
+struct SelectResult {
+  uint64_t prefix;
+  int shift;
+};
+
+__device__ __forceinline__ int digit_shift(int pass) {
+  return pass == 0 ? 53 : pass == 1 ? 42 : pass == 2 ? 32 : pass == 3 ? 21 : pass == 4 ? 10 : 0;
+}
+
+template <class ForEach>
+__device__ SelectResult radix_select(ForEach for_each, uint32_t need, uint32_t *hist,
+                                     BlockScratch &s) {
+  uint64_t prefix = 0;
+  int done = 64;
+  for (int pass = 0; pass < 6; ++pass) {
+    const int shift = digit_shift(pass);
+    const uint32_t dmask = (pass == 2 || pass == 5) ? 0x3ffu : 0x7ffu;
+    for (int i = threadIdx.x; i < kBins; i += kBlock) hist[i] = 0u;
+    __syncthreads();
+    const bool first = pass == 0;
+    const int cmp_shift = first ? 0 : done;
+    const uint64_t want = first ? 0 : (prefix >> cmp_shift);
+    for_each([&](uint64_t v) {
+      if (first || (v >> cmp_shift) == want) atomicAdd(&hist[(uint32_t)(v >> shift) & dmask], 1u);
+    });
+    __syncthreads();
+    find_bin(hist, need, s);
+    const uint32_t b = s.bin, above = s.above, count = s.count;
+    __syncthreads();
+    prefix |= (uint64_t)b << shift;
+    need -= above;
+    done = shift;
+    if (count == need) break;
+  }
+  return {prefix, done};
+}
+
+__device__ __forceinline__ bool selected(uint64_t v, SelectResult r) {
+  return (v >> r.shift) >= (r.prefix >> r.shift);
+}
+
+// In-place descending bitonic sort of a[0..n), n a power of two, by the whole workgroup.
+__device__ __forceinline__ void bitonic_sort_desc(uint64_t *a, int n) {
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < (n >> 1); i += kBlock) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t x = a[lo], y = a[hi];
+        if ((x < y) == desc) {
+          a[lo] = y;
+          a[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__host__ __device__ __forceinline__ int next_pow2(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+}  // namespace tabby

@@ -1,0 +1,298 @@
+"""Python host side of the MI355X sampler, over the C ABI of ``include/tabby_sampler.h``.
+
+The names mirror the reference's sampling surface so a caller of the reference finds the
+same things:
+
+* ``SeededRandom``      -- mulberry32, src/engine/sampler.ts:105-119 (host RNG; it only
+                           produces each row's uniform)
+* ``SamplingParams`` / ``DEFAULT_SAMPLING`` -- src/engine/sampler.ts:83-98
+* ``SampleOutcome``     -- src/engine/sampler.ts:121-135
+* ``TopKResult``        -- src/engine/forward.ts:93-103
+* ``sample(logits, params, rng)`` -- the composition encodeSampling (forward.ts:522-601)
+  -> readback -> sampleFromTopK (sampler.ts:147-212) that the worker performs
+  (src/worker/inference.worker.ts:162-168), done on the GPU.
+
+Device memory and streams come from torch (``torch.cuda``); every sampling computation runs
+in ``libtabby_sampler.so``. There is no CPU fallback: without the built library, importing
+the binding raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence, Union
+
+import numpy as np
+
+from .build import LIB_PATH
+
+TABBY_OK, TABBY_EINVAL, TABBY_EHIP, TABBY_EEMPTY, TABBY_EDOMAIN, TABBY_ECAPACITY = range(6)
+TABBY_F32, TABBY_F16 = 0, 1
+TABBY_FLAG_FULL_VOCAB = 1
+
+PARAMS_DTYPE = np.dtype([
+    ("temperature", "<f8"), ("top_p", "<f8"), ("uniform", "<f8"),
+    ("top_k", "<i4"), ("reserved", "<i4"),
+])
+RESULT_DTYPE = np.dtype([
+    ("id", "<i4"), ("considered", "<u4"), ("probability", "<f8"), ("pool_mass", "<f8"),
+    ("max_logit", "<f4"), ("pool_exhausted", "<i4"), ("sum_exp", "<f8"), ("status", "<i4"),
+    ("topk_count", "<i4"),
+])
+assert PARAMS_DTYPE.itemsize == 32 and RESULT_DTYPE.itemsize == 48
+
+EXPORTED_SYMBOLS = (
+    "tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
+    "tabby_sampler_sample", "tabby_last_error", "tabby_version", "tabby_debug_exp",
+)
+
+
+class SamplingError(RuntimeError):
+    """A nonzero tabby_status; ``status`` holds the code."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Loads the C ABI library. Raises if it has not been built (no fallback exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing; build it with `python -m tabby_amd.build`")
+    L = ctypes.CDLL(path)
+    vp, i32, u32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32, ctypes.c_int64
+    L.tabby_sampler_create.argtypes = [ctypes.c_int, i32, i32, i32, ctypes.POINTER(vp)]
+    L.tabby_sampler_destroy.argtypes = [vp]
+    L.tabby_sampler_sample_device.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, vp, i32, u32, vp]
+    L.tabby_sampler_sample.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, vp, i32, vp]
+    L.tabby_last_error.restype = ctypes.c_char_p
+    L.tabby_version.restype = ctypes.c_char_p
+    L.tabby_debug_exp.argtypes = [vp, vp, i64, vp]
+    for name in ("tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
+                 "tabby_sampler_sample", "tabby_debug_exp"):
+        getattr(L, name).restype = ctypes.c_int
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != TABBY_OK:
+        msg = load_library().tabby_last_error().decode("utf-8", "replace")
+        raise SamplingError(rc, msg)
+
+
+# ---------------------------------------------------------------------------------------
+# The reference's value types.
+# ---------------------------------------------------------------------------------------
+
+class SeededRandom:
+    """mulberry32 (src/engine/sampler.ts:105-119): u32 arithmetic, 32-bit uniforms."""
+
+    def __init__(self, seed: int):
+        self.state = seed & 0xFFFFFFFF
+
+    def next(self) -> float:
+        s = (self.state + 0x6D2B79F5) & 0xFFFFFFFF
+        self.state = s
+        t = ((s ^ (s >> 15)) * (s | 1)) & 0xFFFFFFFF
+        t ^= (t + (((t ^ (t >> 7)) * (t | 61)) & 0xFFFFFFFF)) & 0xFFFFFFFF
+        return ((t ^ (t >> 14)) & 0xFFFFFFFF) / 4294967296.0
+
+
+@dataclass
+class SamplingParams:
+    """src/engine/sampler.ts:83-91. topK = 0 means the whole vocabulary here."""
+
+    temperature: float
+    topK: int
+    topP: float
+    seed: int = 0
+
+
+DEFAULT_SAMPLING = SamplingParams(temperature=0.7, topK=40, topP=0.9, seed=0)
+
+
+@dataclass
+class SampleOutcome:
+    """src/engine/sampler.ts:121-135."""
+
+    id: int
+    probability: float
+    consideredCount: int
+    poolMass: float
+    poolExhausted: bool
+
+
+@dataclass
+class TopKResult:
+    """src/engine/forward.ts:93-103 (sumExp is carried in f64)."""
+
+    maxLogit: float
+    sumExp: float
+    ids: List[int] = field(default_factory=list)
+    logits: List[float] = field(default_factory=list)
+
+
+def outcome_of(rec) -> SampleOutcome:
+    return SampleOutcome(id=int(rec["id"]), probability=float(rec["probability"]),
+                         consideredCount=int(rec["considered"]), poolMass=float(rec["pool_mass"]),
+                         poolExhausted=bool(rec["pool_exhausted"]))
+
+
+def make_params(params: Union[SamplingParams, Sequence[SamplingParams]], rows: int,
+                rng: Union[SeededRandom, Sequence[float], np.ndarray, float, None]) -> np.ndarray:
+    """Packs per-row params. A SeededRandom is advanced once per row with temperature > 0,
+    in row order, as the reference advances it once per non-greedy token (sampler.ts:194)."""
+    if isinstance(params, SamplingParams):
+        params = [params] * rows
+    if len(params) != rows:
+        raise ValueError(f"expected {rows} SamplingParams, got {len(params)}")
+    out = np.zeros(rows, dtype=PARAMS_DTYPE)
+    explicit = None
+    if rng is not None and not isinstance(rng, SeededRandom):
+        explicit = np.broadcast_to(np.asarray(rng, dtype=np.float64), (rows,))
+    for r, p in enumerate(params):
+        out[r]["temperature"] = p.temperature
+        out[r]["top_p"] = p.topP
+        out[r]["top_k"] = p.topK
+        if explicit is not None:
+            out[r]["uniform"] = explicit[r]
+        elif isinstance(rng, SeededRandom) and p.temperature > 0:
+            out[r]["uniform"] = rng.next()
+    return out
+
+
+# ---------------------------------------------------------------------------------------
+# The sampler handle.
+# ---------------------------------------------------------------------------------------
+
+def _dtype_code(t) -> int:
+    import torch
+    if t.dtype == torch.float32:
+        return TABBY_F32
+    if t.dtype == torch.float16:
+        return TABBY_F16
+    raise TypeError(f"logits must be float32 or float16, got {t.dtype}")
+
+
+class GpuSampler:
+    """Owns the device scratch for sampling up to rows_max rows of up to vocab_max logits
+    with top_k up to k_max (the sampling part of ForwardPass, forward.ts:243-248)."""
+
+    def __init__(self, vocab_max: int, rows_max: int = 1, k_max: int = 64, device: int = 0):
+        self._lib = load_library()
+        h = ctypes.c_void_p()
+        _check(self._lib.tabby_sampler_create(device, vocab_max, rows_max, k_max, ctypes.byref(h)))
+        self._h = h
+        self.vocab_max, self.rows_max, self.k_max, self.device = vocab_max, rows_max, k_max, device
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            self._lib.tabby_sampler_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @staticmethod
+    def _stream(stream):
+        import torch
+        if stream is None:
+            stream = torch.cuda.current_stream()
+        return ctypes.c_void_p(stream.cuda_stream)
+
+    def sample_params(self, logits, params: np.ndarray, topk_cap: int = 0, stream=None):
+        """Host-parameter entry (tabby_sampler_sample). ``logits`` is a CUDA tensor [V] or
+        [R, V]; returns (results structured array, topk ids, topk logits)."""
+        if not logits.is_cuda:
+            raise ValueError("logits must be a device (cuda) tensor")
+        x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+        if not x.is_contiguous():
+            raise ValueError("logits must be contiguous")
+        rows, vocab = int(x.shape[0]), int(x.shape[1])
+        params = np.ascontiguousarray(params, dtype=PARAMS_DTYPE)
+        if params.shape != (rows,):
+            raise ValueError(f"params must have shape ({rows},), got {params.shape}")
+        results = np.zeros(rows, dtype=RESULT_DTYPE)
+        ids = np.zeros((rows, max(topk_cap, 0)), dtype=np.int32)
+        vals = np.zeros((rows, max(topk_cap, 0)), dtype=np.float32)
+        _check(self._lib.tabby_sampler_sample(
+            self._h, ctypes.c_void_p(x.data_ptr()), _dtype_code(x), rows, vocab,
+            params.ctypes.data, results.ctypes.data,
+            ids.ctypes.data if topk_cap > 0 else None, vals.ctypes.data if topk_cap > 0 else None,
+            topk_cap, self._stream(stream)))
+        return results, ids, vals
+
+    def sample_device(self, logits, params_dev, results_dev, topk_ids=None, topk_logits=None,
+                      flags: int = 0, stream=None) -> None:
+        """Device-resident entry (tabby_sampler_sample_device); asynchronous. ``params_dev``
+        and ``results_dev`` are uint8 CUDA tensors holding PARAMS_DTYPE / RESULT_DTYPE rows."""
+        x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+        rows, vocab = int(x.shape[0]), int(x.shape[1])
+        cap = int(topk_ids.shape[-1]) if topk_ids is not None else 0
+        _check(self._lib.tabby_sampler_sample_device(
+            self._h, ctypes.c_void_p(x.data_ptr()), _dtype_code(x), rows, vocab,
+            ctypes.c_void_p(params_dev.data_ptr()), ctypes.c_void_p(results_dev.data_ptr()),
+            ctypes.c_void_p(topk_ids.data_ptr()) if cap else None,
+            ctypes.c_void_p(topk_logits.data_ptr()) if cap else None, cap, flags,
+            self._stream(stream)))
+
+    def sample(self, logits, params: SamplingParams, rng) -> SampleOutcome:
+        """One row: sample(logits, {temperature, topK, topP}, rng) -> SampleOutcome."""
+        res, _, _ = self.sample_params(logits, make_params(params, 1, rng))
+        return outcome_of(res[0])
+
+    def sample_batch(self, logits, params, rng) -> List[SampleOutcome]:
+        rows = int(logits.shape[0])
+        res, _, _ = self.sample_params(logits, make_params(params, rows, rng))
+        return [outcome_of(r) for r in res]
+
+    def top_k(self, logits, k: int) -> TopKResult:
+        """The GPU half alone (encodeSampling's TopKResult) for one row."""
+        p = make_params(SamplingParams(temperature=0.0, topK=k, topP=1.0), 1, 0.0)
+        vocab = int(logits.shape[-1])
+        cap = vocab if k <= 0 else min(k, vocab)
+        res, ids, vals = self.sample_params(logits, p, topk_cap=cap)
+        n = int(res[0]["topk_count"])
+        return TopKResult(maxLogit=float(res[0]["max_logit"]), sumExp=float(res[0]["sum_exp"]),
+                          ids=[int(v) for v in ids[0, :n]], logits=[float(v) for v in vals[0, :n]])
+
+
+_default: Optional[GpuSampler] = None
+
+
+def sample(logits, params: SamplingParams, rng) -> SampleOutcome:
+    """Module-level drop-in: one row, a cached handle grown to fit."""
+    global _default
+    vocab = int(logits.shape[-1])
+    k = max(params.topK, 1)
+    if _default is None or _default.vocab_max < vocab or _default.k_max < min(k, 1024):
+        if _default is not None:
+            _default.close()
+        _default = GpuSampler(vocab_max=vocab, rows_max=1, k_max=max(64, min(k, 1024)))
+    return _default.sample(logits, params, rng)
+
+
+def device_exp(x) -> "object":
+    """The device f64 exp over a CUDA float64 tensor (diagnostic)."""
+    import torch
+    y = torch.empty_like(x)
+    _check(load_library().tabby_debug_exp(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()),
+                                          x.numel(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    return y

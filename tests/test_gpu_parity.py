@@ -1,0 +1,160 @@
+"""GPU parity: libtabby_sampler.so (through its C ABI) against the CPU oracle on identical
+seeded logits and uniforms. Ids, candidate sets and counts must be bit-exact; the f64
+probabilities within 1e-5 relative (the tolerance of BASELINE.json's north_star)."""
+import numpy as np
+import pytest
+
+from tabby_amd import sampler as S
+from tabby_amd import synth
+
+from parity import compare, params_of, run_gpu, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(name, stats):
+    print(f"[parity] {name}: {stats}", flush=True)
+
+
+@pytest.mark.parametrize("greedy", [False, True])
+def test_config1_single_row_49152(oracle, greedy):
+    w = synth.config(1)
+    if greedy:
+        w.temperature[:] = 0.0
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=40)
+    _log(f"config1 greedy={greedy}", compare(w, res, ids, vals, run_oracle(oracle, w, 40), 40))
+
+
+def test_config2_single_row_151936_spiky(oracle):
+    w = synth.config(2)
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=50)
+    _log("config2", compare(w, res, ids, vals, run_oracle(oracle, w, 50), 50))
+
+
+def test_config3_batch_256(oracle):
+    w = synth.config(3)
+    res, ids, vals = run_gpu(w, k_max=128, topk_cap=100)
+    _log("config3", compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100))
+
+
+def test_config5_ties_neg_inf_k1024(oracle):
+    w = synth.config(5, rows=128)
+    res, ids, vals = run_gpu(w, k_max=1024, topk_cap=1024)
+    _log("config5[128 rows]", compare(w, res, ids, vals, run_oracle(oracle, w, 1024), 1024))
+
+
+def test_f16_input_finite_k(oracle):
+    w = synth.config(4, rows=16)
+    w.top_k[:] = np.array([1, 20, 50, 100] * 4, np.int32)
+    w.temperature[:] = 0.3
+    res, ids, vals = run_gpu(w, k_max=128, topk_cap=100)
+    _log("f16 finite k", compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100))
+
+
+@pytest.mark.parametrize("vocab", [1, 3, 64, 203, 1000, 4097, 16385, 49153])
+def test_awkward_vocab_sizes(oracle, vocab):
+    # Non-multiples of 4 take the scalar-load path; sizes straddle the slice lengths.
+    w = synth.random_workload(rows=6, vocab=vocab, seed=vocab, k_choices=(1, 5, 40, 64))
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=64)
+    _log(f"vocab {vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
+def test_ties_and_neg_inf(oracle):
+    w = synth.random_workload(rows=32, vocab=20000, seed=7, ties=True, neg_inf_frac=0.5,
+                              k_choices=(1, 7, 64, 256))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=256)
+    _log("ties+neg_inf", compare(w, res, ids, vals, run_oracle(oracle, w, 256), 256))
+
+
+def test_all_equal_row_takes_lowest_ids(oracle):
+    w = synth.random_workload(rows=2, vocab=5000, seed=3, k_choices=(64,))
+    w.logits[:] = 1.5
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=64)
+    assert np.array_equal(ids[0], np.arange(64)) and np.array_equal(ids[1], np.arange(64))
+    compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64)
+
+
+def test_signed_zero_ties(oracle):
+    w = synth.random_workload(rows=4, vocab=3000, seed=11, k_choices=(50,))
+    w.logits[:] = -1.0
+    w.logits[:, ::3] = 0.0
+    w.logits[:, 1::3] = -0.0  # equal to +0 for the comparator: order by id
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=50)
+    compare(w, res, ids, vals, run_oracle(oracle, w, 50), 50)
+
+
+def test_k_at_least_vocab_takes_whole_row(oracle):
+    w = synth.random_workload(rows=4, vocab=100, seed=5, k_choices=(100, 200, 0))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=100)
+    compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100)
+
+
+def test_repeatable_bit_for_bit():
+    w = synth.config(3, rows=32)
+    a = run_gpu(w, k_max=128, topk_cap=100)
+    b = run_gpu(w, k_max=128, topk_cap=100)
+    assert a[0].tobytes() == b[0].tobytes()
+    assert np.array_equal(a[1], b[1]) and np.array_equal(a[2].view(np.uint32), b[2].view(np.uint32))
+
+
+def test_reuse_handle_across_calls(oracle):
+    # The arrival counters reset themselves; a second call on the same handle must agree.
+    w = synth.random_workload(rows=8, vocab=30000, seed=21)
+    with S.GpuSampler(vocab_max=30000, rows_max=8, k_max=64) as g:
+        first = run_gpu(w, sampler=g, topk_cap=64)
+        second = run_gpu(w, sampler=g, topk_cap=64)
+    assert first[0].tobytes() == second[0].tobytes()
+    compare(w, *first, run_oracle(oracle, w, 64), 64)
+
+
+def test_rejects_topk_above_capacity():
+    import torch
+    x = torch.zeros(1, 1000, device="cuda")
+    with S.GpuSampler(vocab_max=1000, rows_max=1, k_max=64) as g:
+        p = S.make_params(S.SamplingParams(0.7, 65, 0.9), 1, 0.5)
+        with pytest.raises(S.SamplingError, match="topK"):
+            g.sample_params(x, p)
+
+
+@pytest.mark.parametrize("fill", ["all_neg_inf", "nan", "pos_inf"])
+def test_rows_outside_contract_report_edomain(fill):
+    import torch
+    x = torch.randn(3, 2000, device="cuda")
+    if fill == "all_neg_inf":
+        x[1] = float("-inf")
+    elif fill == "nan":
+        x[1, 17] = float("nan")
+    else:
+        x[1, 17] = float("inf")
+    with S.GpuSampler(vocab_max=2000, rows_max=3, k_max=64) as g:
+        p = S.make_params(S.SamplingParams(0.7, 40, 0.9), 3, 0.25)
+        with pytest.raises(S.SamplingError) as e:
+            g.sample_params(x, p)
+        assert e.value.status == S.TABBY_EDOMAIN
+        # The other rows are still sampled: run the device form and look at statuses.
+        pd = torch.from_numpy(p.view(np.uint8).copy()).cuda()
+        rd = torch.zeros(3 * S.RESULT_DTYPE.itemsize, dtype=torch.uint8, device="cuda")
+        g.sample_device(x, pd, rd)
+        res = rd.cpu().numpy().view(S.RESULT_DTYPE)
+        assert list(res["status"]) == [0, S.TABBY_EDOMAIN, 0]
+
+
+def test_device_exp_matches_oracle_exp(oracle):
+    import torch
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.uniform(-60, 1, 400_000), rng.uniform(-750, 712, 100_000),
+                        np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, 709.78, -745.2])])
+    y = S.device_exp(torch.from_numpy(x).cuda()).cpu().numpy()
+    expected = oracle.exp_array(x)
+    bad = np.nonzero(y.view(np.uint64) != expected.view(np.uint64))[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first at x={x[bad[0]]!r}"
+
+
+def test_module_level_sample_matches_oracle(oracle):
+    import torch
+    w = synth.config(1)
+    rng = S.SeededRandom(42)
+    out = S.sample(torch.from_numpy(w.logits[0]).cuda(), S.SamplingParams(0.7, 40, 0.9), rng)
+    u = S.SeededRandom(42).next()
+    o = oracle.sample_row(w.logits[0], 40, 0.7, 0.9, u)
+    assert out.id == o["id"] and out.consideredCount == o["considered"]
