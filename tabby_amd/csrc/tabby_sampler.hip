@@ -30,16 +30,13 @@
 
 #include "block_ops.h"
 #include "device_math.h"
+#include "wave_ops.h"
 #include "tabby_sampler.h"
 
 namespace tabby {
 
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr int kMaxSplits = kBlock;  // one merge lane per slice
-constexpr int kSliceElemsSmall = 16;
-constexpr int kSliceElemsLarge = 64;
-constexpr int kMinSliceLen = kSliceElemsSmall * kBlock;
-constexpr int kMaxSliceLen = kSliceElemsLarge * kBlock;
 constexpr int kKcapSmall = 256;
 constexpr int kKcapLarge = 1024;
 
@@ -63,13 +60,13 @@ struct Workspace {
   uint32_t *head_arrivals;  // [rows_cap] arrival counters of the head kernel
   uint32_t *head_count;     // [rows_cap] head sizes
   SliceStat *stats;         // [rows_cap * kMaxSplits]
-  uint64_t *cands;          // [rows_cap * kMaxSplits * cand_stride]
+  uint64_t *cands;          // [rows_cap * row_cand_stride]
   RowState *row_state;      // [rows_cap]
   uint64_t *head;           // [head_rows * head_stride] (whole-vocabulary rows only)
   uint64_t *head_sorted;    // [head_rows * head_stride]
   double *head_exact;       // [head_rows * head_stride]
   double *head_w;           // [head_rows * head_stride]
-  int32_t cand_stride;
+  int64_t row_cand_stride;  // composites per row in cands
   int32_t head_stride;
 };
 
@@ -146,62 +143,14 @@ __device__ __forceinline__ bool params_valid(const tabby_row_params &p, int k_ma
          !(p.uniform >= 1.0) && p.uniform == p.uniform;
 }
 
-// ---------------------------------------------------------------------------------------
-// Slice stage, shared by both kernels: load ELEMS elements per lane, return them as keys.
-// ---------------------------------------------------------------------------------------
-template <typename In, int VEC, int ELEMS>
-__device__ __forceinline__ void load_slice(const In *src, int n, float (&x)[ELEMS]) {
-  constexpr int ITEMS = ELEMS / VEC;
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    const int le = (j * kBlock + (int)threadIdx.x) * VEC;
-    const bool valid = le < n;
-    // Lanes past the end read the slice's last vector (always in bounds) and discard it.
-    float v[VEC];
-    Loader<In, VEC>::load(src + (valid ? le : n - VEC), v);
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) x[j * VEC + c] = valid ? v[c] : -INFINITY;
-  }
-}
-
-template <int VEC>
-__device__ __forceinline__ uint32_t elem_index(int begin, int e) {
-  // Element e of this lane's registers sits at row index begin + (j*kBlock + lane)*VEC + c.
-  const int j = e / VEC, c = e % VEC;
-  return (uint32_t)(begin + (j * kBlock + (int)threadIdx.x) * VEC + c);
-}
-
-// ---------------------------------------------------------------------------------------
-// LDS layout of the sampling kernel. The histogram and the tail arrays are never live at
-// the same time, so they share storage.
-// ---------------------------------------------------------------------------------------
-template <int KCAP>
-struct SampleSmem {
-  BlockScratch bs;
-  int32_t is_last;
-  float row_max;
-  double sum_exp;
-  double pool_mass;
-  double scaled_total;
-  double slice_term[kMaxSplits];
-  uint64_t sorted[KCAP];
-  union {
-    uint32_t hist[kBins];
-    struct {
-      double exact[KCAP];
-      double w[KCAP];
-    } tail;
-  } u;
-};
-
 // sampleFromTopK (src/engine/sampler.ts:147-212) over the `count` sorted candidates in
 // sm.sorted, f64 throughout, with the reference's order of operations: the per-element
 // terms are independent and computed by all lanes; every sum is a sequential left-to-right
 // f64 sum on lane 0. The running sums of the draw (sampler.ts:195-203) are the same
 // numbers as the top-p cumulative sums (sampler.ts:178-185), and `total` (:191-192) is the
 // last of them, so lane 0 computes that sequence once and keeps it.
-template <int KCAP, typename In>
-__device__ void finish_row(SampleSmem<KCAP> &sm, const Launch &L, int row, const In *row_src,
+template <int KCAP, typename In, class Smem>
+__device__ void finish_row(Smem &sm, const Launch &L, int row, const In *row_src,
                            int count, float max_logit, double sum_exp,
                            const tabby_row_params &P) {
   const double T = P.temperature;
@@ -278,6 +227,125 @@ __device__ void finish_row(SampleSmem<KCAP> &sm, const Launch &L, int row, const
   }
 }
 
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const long long b = __double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(b >> 32), lane);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// sampleFromTopK (src/engine/sampler.ts:147-212) for a pool of at most 64*R candidates, by
+// one wave, in registers: element i of the pool is register i/64 of lane i%64. The
+// per-element terms are computed lane-parallel; each sum is sequential in index order,
+// lane by lane through readlane, as the reference's left-to-right reduce. The running sums
+// of the draw equal the top-p cumulative sums, so they are kept (writelane) from the
+// top-p scan (each lane keeps its own element's) and the draw is a ballot over
+// "target < running".
+template <int R, typename In>
+__device__ void wave_finish(const uint64_t *pool_in, int count, const Launch &L, int row,
+                            const In *row_src, float max_logit, double sum_exp,
+                            const tabby_row_params &P) {
+  const int lane = wave_lane();
+  uint64_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + lane;
+    v[r] = i < count ? pool_in[i] : 0ull;
+  }
+  wave_sort_desc<R>(v);
+  const double T = P.temperature;
+  double exact[R], w[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    exact[r] = 0.0;
+    w[r] = 0.0;
+    if (r * kWaveSize + lane < count) {
+      const double d = (double)value_of(composite_key(v[r])) - (double)max_logit;
+      exact[r] = fdlibm_exp(d) / sum_exp;
+      if (T > 0.0) w[r] = fdlibm_exp(d / T);
+    }
+  }
+  double pool = 0.0, scaled = 0.0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int m = min(kWaveSize, count - r * kWaveSize);
+    for (int j = 0; j < m; ++j) {
+      pool += readlane_f64(exact[r], j);
+      scaled += readlane_f64(w[r], j);
+    }
+  }
+  tabby_row_result res;
+  res.max_logit = max_logit;
+  res.sum_exp = sum_exp;
+  res.pool_mass = pool;
+  res.status = TABBY_OK;
+  res.topk_count = min(count, L.topk_cap);
+  int chosen = 0;
+  if (T <= 0.0) {
+    res.considered = 1;
+    res.pool_exhausted = 0;
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[r] = w[r] / scaled;
+    const double top_p = P.top_p;
+    double c = 0.0, running[R];
+    int cut = count;
+    bool cut_found = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      running[r] = 0.0;
+      const int m = min(kWaveSize, count - r * kWaveSize);
+      for (int j = 0; j < m && !cut_found; ++j) {
+        c += readlane_f64(w[r], j);
+        running[r] = lane == j ? c : running[r];
+        if (top_p < 1.0 && c >= top_p) {
+          cut = r * kWaveSize + j + 1;
+          cut_found = true;
+        }
+      }
+    }
+    const double target = P.uniform * c;  // c is the running sum at cut - 1: the reference's total
+    chosen = cut - 1;
+    bool done = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = r * kWaveSize + lane;
+      const uint64_t hit = __ballot(i < cut && target < running[r]);
+      if (!done && hit) {
+        chosen = r * kWaveSize + __ffsll((unsigned long long)hit) - 1;
+        done = true;
+      }
+    }
+    res.considered = (uint32_t)cut;
+    res.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
+  }
+  // The chosen candidate's id and probability live in lane chosen%64, register chosen/64.
+  uint64_t cv = 0;
+  double cp = 0.0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r == chosen / kWaveSize) {
+      cv = (uint64_t)__builtin_amdgcn_readlane((int)v[r], chosen % kWaveSize) |
+           ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v[r] >> 32), chosen % kWaveSize) << 32);
+      cp = readlane_f64(exact[r], chosen % kWaveSize);
+    }
+  }
+  res.id = (int32_t)composite_index(cv);
+  res.probability = cp;
+  if (lane == 0) L.results[row] = res;
+  if (L.topk_cap > 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = r * kWaveSize + lane;
+      if (i < count && i < L.topk_cap) {
+        const uint32_t idx = composite_index(v[r]);
+        L.topk_ids[(size_t)row * L.topk_cap + i] = (int32_t)idx;
+        L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(L.vocab - 1)));
+      }
+    }
+  }
+}
+
 __device__ __forceinline__ void write_status(const Launch &L, int row, int32_t status, float mx,
                                              double se) {
   tabby_row_result r;
@@ -290,11 +358,98 @@ __device__ __forceinline__ void write_status(const Launch &L, int row, int32_t s
 }
 
 // ---------------------------------------------------------------------------------------
-// The sampling kernel.
+// Kernel 1 (slices): grid = rows x splits; each workgroup streams one slice of a row from
+// HBM exactly once, in chunks of 16 elements per lane (4096 per workgroup) with the next
+// chunk's loads in flight while the current one is processed. Per lane it keeps an online
+// max and an f64 sum of exp(x - max). It also collects the slice's candidates: every
+// element >= theta, where theta is the kk-th largest lane maximum (or, for kk > 256, vector
+// maximum) of the first chunk -- a lower bound on the slice's kk-th largest value, since at
+// least kk distinct elements reach it. Candidates go to an LDS list with one atomic per
+// wave; a list that would overflow is flushed to the slice's region of global memory. The
+// exact selection happens once per row, in the merge.
+//
+// There is no cross-workgroup communication: the merge is the next kernel on the stream,
+// so the kernel boundary orders these writes before its reads (an agent-scope fence per
+// workgroup costs an L2 writeback + invalidate each, measured slower than the whole read).
 // ---------------------------------------------------------------------------------------
-template <typename In, int VEC, int ELEMS, int KCAP>
-__global__ __launch_bounds__(kBlock) void sample_kernel(Launch L, Workspace W) {
-  __shared__ SampleSmem<KCAP> sm;
+constexpr int kChunkPerLane = 16;
+constexpr int kChunk = kChunkPerLane * kBlock;
+constexpr int kListCap = kChunk;  // a whole chunk always fits after a flush
+
+struct SliceSmem {
+  BlockScratch bs;
+  uint32_t list_count;  // appended to with atomics during a chunk
+  uint32_t committed;   // list_count as of the last chunk boundary (stable between barriers)
+  uint32_t flushed;     // candidates already written to global memory
+  uint32_t wave_count[2][kWaves];  // by chunk parity: chunk c+1 writes while c is read
+  float theta;
+  union {
+    uint32_t hist[kBins];      // only for the first chunk's theta, before any append
+    uint64_t list[kListCap];
+  };
+};
+
+// theta from a selection threshold key, clamped to [-inf, +inf]: an early-exit prefix can
+// fall below the key of -inf (or above +inf), where keys decode to NaN.
+__device__ __forceinline__ float theta_of(uint64_t prefix) {
+  const uint32_t k = (uint32_t)(prefix >> 32);
+  return value_of(min(max(k, kNegInfKey), 0xff800000u));
+}
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Raw loads of chunk `chunk` (no masking, so nothing consumes them until the next
+// iteration and they stay in flight). Lanes past the end reread the slice's last vector.
+template <typename In, int VEC>
+__device__ __forceinline__ void load_chunk(const In *src, int n, int chunk, float (&x)[kChunkPerLane]) {
+  constexpr int ITEMS = kChunkPerLane / VEC;
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const int le = chunk * kChunk + (j * kBlock + (int)threadIdx.x) * VEC;
+    float v[VEC];
+    Loader<In, VEC>::load(src + min(le, n - VEC), v);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) x[j * VEC + c] = v[c];
+  }
+}
+
+// Padding lanes of chunk `chunk` become -inf, which no statistic or candidate test admits.
+template <int VEC>
+__device__ __forceinline__ void mask_chunk(int n, int chunk, float (&x)[kChunkPerLane]) {
+  constexpr int ITEMS = kChunkPerLane / VEC;
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const bool valid = chunk * kChunk + (j * kBlock + (int)threadIdx.x) * VEC < n;
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) x[j * VEC + c] = valid ? x[j * VEC + c] : -INFINITY;
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ int chunk_local(int chunk, int e) {
+  // Slice-local index of register element e of this lane in chunk `chunk`.
+  return chunk * kChunk + ((e / VEC) * kBlock + (int)threadIdx.x) * VEC + e % VEC;
+}
+
+// Copies the LDS list to the slice's global region and empties it. Whole workgroup.
+__device__ __forceinline__ void flush_list(SliceSmem &sm, uint64_t *region, uint32_t count) {
+  const uint32_t at = sm.flushed;
+  for (uint32_t i = threadIdx.x; i < count; i += kBlock) region[at + i] = sm.list[i];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    sm.flushed = at + count;
+    sm.list_count = 0u;
+    sm.committed = 0u;
+  }
+  __syncthreads();
+}
+
+template <typename In, int VEC>
+__global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
+  constexpr int ITEMS = kChunkPerLane / VEC;
+  __shared__ SliceSmem sm;
 
   const int splits = L.splits;
   const int row = (int)blockIdx.x / splits;
@@ -302,111 +457,476 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(Launch L, Workspace W) {
   const int V = L.vocab;
   const int begin = slice * L.slice_len;
   const int n = min(L.slice_len, V - begin);
+  const int nchunks = (n + kChunk - 1) / kChunk;
   const tabby_row_params P = L.params[row];
   const bool valid_params = params_valid(P, L.k_max);
   const int keff = effective_k(P, V);
   const bool finite = valid_params && keff <= L.kcap;
   const int kk = finite ? min(keff, n) : 0;
-  const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V;
+  const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
+  // The slice's candidate region: room for every element of the slice.
+  uint64_t *region = W.cands + (size_t)row * W.row_cand_stride + (size_t)begin;
 
-  // 1. One pass over HBM into registers.
-  float x[ELEMS];
-  load_slice<In, VEC, ELEMS>(row_src + begin, n, x);
-
-  // 2. Lane max and lane sum of exp(x - lane max); then the slice's.
-  float mt = x[0];
-#pragma unroll
-  for (int e = 1; e < ELEMS; ++e) mt = fmaxf(mt, x[e]);
-  float st = 0.0f;
-  if (mt != -INFINITY) {
-    const float ml = mt * kLog2e;
-#pragma unroll
-    for (int e = 0; e < ELEMS; ++e) st += __builtin_amdgcn_exp2f(fmaf(x[e], kLog2e, -ml));
+  if (threadIdx.x == 0) {
+    sm.list_count = 0u;
+    sm.committed = 0u;
+    sm.flushed = 0u;
+    sm.theta = -INFINITY;
   }
-  const float ms = block_max(mt, sm.bs);
-  const double term = (mt == -INFINITY) ? 0.0
-                                        : (double)st * (double)__builtin_amdgcn_exp2f((mt - ms) * kLog2e);
-  const double ss = block_sum(term, sm.bs);
+  __syncthreads();
+  float lane_max = -INFINITY;
+  double lane_sum = 0.0;  // sum of exp(x - lane_max) over this lane's elements so far
 
-  // 3. Keys in place of the values.
-  uint32_t key[ELEMS];
-#pragma unroll
-  for (int e = 0; e < ELEMS; ++e) key[e] = key_of(x[e]);
+  float x[kChunkPerLane], y[kChunkPerLane];
+  load_chunk<In, VEC>(src, n, 0, x);
+  for (int c = 0; c < nchunks; ++c) {
+    load_chunk<In, VEC>(src, n, min(c + 1, nchunks - 1), y);  // in flight during this chunk
+    mask_chunk<VEC>(n, c, x);
 
-  // 4. This slice's top-kk composites, unordered, into the row's candidate area.
-  uint64_t *out = W.cands + ((size_t)row * kMaxSplits + slice) * W.cand_stride;
-  if (kk > 0) {
-    if (kk >= n) {
+    // Online max / sum-exp for this lane.
+    float cm = x[0];
 #pragma unroll
-      for (int e = 0; e < ELEMS; ++e) {
-        const uint32_t idx = elem_index<VEC>(begin, e);
-        const int local = (int)idx - begin;
-        if (local < n) out[local] = composite(key[e], idx);
-      }
-    } else {
-      auto regs = [&](auto &&f) {
+    for (int e = 1; e < kChunkPerLane; ++e) cm = fmaxf(cm, x[e]);
+    const float nm = fmaxf(lane_max, cm);
+    if (nm != -INFINITY) {
+      const float ml = nm * kLog2e;
+      float part = 0.0f;
 #pragma unroll
-        for (int e = 0; e < ELEMS; ++e) f(composite(key[e], elem_index<VEC>(begin, e)));
-      };
-      const SelectResult r = radix_select(regs, (uint32_t)kk, sm.u.hist, sm.bs);
-      if (threadIdx.x == 0) sm.bs.slot = 0;
-      __syncthreads();
+      for (int e = 0; e < kChunkPerLane; ++e) part += __builtin_amdgcn_exp2f(fmaf(x[e], kLog2e, -ml));
+      const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f((lane_max - nm) * kLog2e);
+      lane_sum = lane_sum * rescale + (double)part;
+      lane_max = nm;
+    }
+
+    if (kk > 0) {
+      if (c == 0 && kk < n) {
+        // theta from the first chunk's lane or vector maxima.
+        if (kk <= kBlock) {
+          auto lanes = [&](auto &&f) { f(composite(key_of(cm), threadIdx.x)); };
+          const SelectResult r = radix_select(lanes, (uint32_t)kk, sm.hist, sm.bs);
+          if (threadIdx.x == 0) sm.theta = theta_of(r.prefix);
+        } else if (kk <= kBlock * ITEMS) {
+          auto vecs = [&](auto &&f) {
 #pragma unroll
-      for (int e = 0; e < ELEMS; ++e) {
-        const uint64_t v = composite(key[e], elem_index<VEC>(begin, e));
-        if (selected(v, r)) {
-          const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
-          if (at < (uint32_t)kk) out[at] = v;  // exactly kk are selected; the bound is a guard
+            for (int j = 0; j < ITEMS; ++j) {
+              float m = x[j * VEC];
+#pragma unroll
+              for (int q = 1; q < VEC; ++q) m = fmaxf(m, x[j * VEC + q]);
+              f(composite(key_of(m), (uint32_t)(j * kBlock + (int)threadIdx.x)));
+            }
+          };
+          const SelectResult r = radix_select(vecs, (uint32_t)kk, sm.hist, sm.bs);
+          if (threadIdx.x == 0) sm.theta = theta_of(r.prefix);
         }
+        __syncthreads();
+      }
+      const float theta = sm.theta;
+      const bool check_index = !(theta > -INFINITY);
+      // Count first, so that a list that would overflow is flushed before the appends.
+      uint32_t mine = 0;
+#pragma unroll
+      for (int e = 0; e < kChunkPerLane; ++e)
+        mine += (x[e] >= theta && (!check_index || chunk_local<VEC>(c, e) < n)) ? 1u : 0u;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mine += __shfl_xor(mine, o);
+      if (lane_id() == 0) sm.wave_count[c & 1][wave_id()] = mine;
+      __syncthreads();
+      uint32_t incoming = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) incoming += sm.wave_count[c & 1][w];
+      const uint32_t have = sm.committed;
+      if (incoming > 0) {
+        if (have + incoming > (uint32_t)kListCap) flush_list(sm, region, have);
+#pragma unroll
+        for (int e = 0; e < kChunkPerLane; ++e) {
+          const int local = chunk_local<VEC>(c, e);
+          const bool take = x[e] >= theta && (!check_index || local < n);
+          const uint64_t mask = __ballot(take);
+          if (mask) {
+            uint32_t base = 0;
+            if (lane_id() == 0) base = atomicAdd(&sm.list_count, (uint32_t)__popcll(mask));
+            base = __shfl(base, 0);
+            const uint32_t at = base + lanes_below(mask);
+            // A chunk holds at most kChunk == kListCap candidates; the bound is a guard.
+            if (take && at < (uint32_t)kListCap) sm.list[at] = composite(key_of(x[e]), (uint32_t)(begin + local));
+          }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) sm.committed = sm.list_count;  // read after the next barrier
       }
     }
+#pragma unroll
+    for (int e = 0; e < kChunkPerLane; ++e) x[e] = y[e];
+  }
+
+  // Slice statistics (their barriers also publish `committed`).
+  const float ms = block_max(lane_max, sm.bs);
+  const double term = lane_max == -INFINITY
+                          ? 0.0
+                          : lane_sum * (double)__builtin_amdgcn_exp2f((lane_max - ms) * kLog2e);
+  const double ss = block_sum(term, sm.bs);
+  uint32_t total = 0;
+  if (kk > 0) {
+    const uint32_t have = sm.committed;
+    total = sm.flushed + have;
+    const uint32_t at = sm.flushed;
+    for (uint32_t i = threadIdx.x; i < have; i += kBlock) region[at + i] = sm.list[i];
   }
   if (threadIdx.x == 0) {
     SliceStat st_out;
     st_out.max = ms;
-    st_out.count = (uint32_t)kk;
+    st_out.count = total;
     st_out.sum = ss;
     W.stats[(size_t)row * kMaxSplits + slice] = st_out;
   }
+}
 
-  // 5. Arrival: the last workgroup of the row merges.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = atomicAdd(&W.arrivals[row], 1u);
-    sm.is_last = prev == (uint32_t)(splits - 1);
+// ---------------------------------------------------------------------------------------
+// Kernel 1 for pools of at most 256 (wave_kernel): grid = rows x splits, one wave per
+// workgroup, so nothing in it waits at a barrier. Each wave streams its slice of a row from
+// HBM exactly once, 1024 elements (16 per lane) per chunk, with the next chunk's loads in
+// flight while the current one is processed; keeps the lane max and f64 sum-exp online; and
+// keeps in a wave-private LDS list every element >= theta, where theta never exceeds the
+// kk-th largest value seen so far. theta starts at the kk-th largest lane maximum of the
+// first chunk (kk <= 64). Whenever the list fills up it is pruned: its keys are binned by
+// distance below the list's largest key (256 bins, width chosen from the key range), theta
+// rises to the lower edge of the bin that holds the kk-th largest entry, and the entries
+// below are dropped -- a few instructions per entry, no sort. (A bin can only fail to
+// shrink the list under massive ties; then the list is sorted in registers and cut to kk.)
+// The list, unsorted, goes to the slice's candidate region; the merge selects exactly.
+// ---------------------------------------------------------------------------------------
+constexpr int kWChunkPerLane = 16;
+constexpr int kWChunk = kWaveSize * kWChunkPerLane;
+constexpr int kWListCap = 512;
+constexpr int kWaveKcap = 256;
+constexpr int kPruneBins = 256;
+
+template <typename In, int VEC>
+__device__ __forceinline__ void wave_load(const In *src, int n, int chunk, float (&x)[kWChunkPerLane]) {
+  constexpr int ITEMS = kWChunkPerLane / VEC;
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const int le = chunk * kWChunk + (j * kWaveSize + wave_lane()) * VEC;
+    float v[VEC];
+    Loader<In, VEC>::load(src + min(le, n - VEC), v);  // past the end: reread, masked later
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) x[j * VEC + c] = v[c];
   }
-  __syncthreads();
-  if (!sm.is_last) return;
-  __threadfence();
+}
 
-  // 6. Row max and sum-exp from the slice statistics, in slice order.
+template <int VEC>
+__device__ __forceinline__ int wave_local(int chunk, int e) {
+  return chunk * kWChunk + ((e / VEC) * kWaveSize + wave_lane()) * VEC + e % VEC;
+}
+
+// Sorts list[0..count) descending in registers (count <= 64*R) and leaves its top `keep`
+// at list[0..keep).
+template <int R>
+__device__ __forceinline__ void wave_sort_list(uint64_t *list, int count, int keep) {
+  uint64_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + wave_lane();
+    v[r] = i < count ? list[i] : 0ull;
+  }
+  wave_sort_desc<R>(v);
+  wave_lds_sync();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + wave_lane();
+    if (i < keep) list[i] = v[r];
+  }
+  wave_lds_sync();
+}
+
+struct WaveSmem {
+  uint64_t list[kWListCap];
+  uint32_t hist[kPruneBins];
+};
+
+// Drops from the wave's list every entry that cannot be among its top kk, raising
+// *theta_key (and the returned count); see wave_kernel. count <= kWListCap, kk <= count.
+__device__ __noinline__ int wave_prune(WaveSmem &sm, int count, int kk, uint32_t *theta_key) {
+  constexpr int R = kWListCap / kWaveSize;
+  const int lane = wave_lane();
+  wave_lds_sync();
+  uint32_t k[R];
+  uint32_t kmax = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + lane;
+    k[r] = i < count ? composite_key(sm.list[i]) : 0u;
+    kmax = max(kmax, k[r]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+  const uint32_t floor_key = *theta_key;
+  const uint32_t range = kmax - min(floor_key, kmax);
+  const int bits = range == 0 ? 0 : 32 - __clz((int)range);
+  const int shift = bits > 8 ? bits - 8 : 0;  // (kmax - key) >> shift < 256 for key >= floor
+#pragma unroll
+  for (int i = lane; i < kPruneBins; i += kWaveSize) sm.hist[i] = 0u;
+  wave_lds_sync();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + lane;
+    if (i < count) atomicAdd(&sm.hist[min((kmax - k[r]) >> shift, (uint32_t)(kPruneBins - 1))], 1u);
+  }
+  wave_lds_sync();
+  // Bin holding the kk-th largest: lanes own 4 bins each, in order from the top.
+  uint32_t h[4], sum = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    h[q] = sm.hist[lane * 4 + q];
+    sum += h[q];
+  }
+  uint32_t inc = sum;
+#pragma unroll
+  for (int o = 1; o < kWaveSize; o <<= 1) {
+    const uint32_t t = __shfl_up(inc, o);
+    if (lane >= o) inc += t;
+  }
+  const uint64_t reached = __ballot(inc >= (uint32_t)kk);
+  const int owner = __ffsll((unsigned long long)reached) - 1;  // kk <= count: some lane reaches it
+  int bin = 0;
+  if (lane == owner) {
+    uint32_t acc = inc - sum;
+    bin = lane * 4 + 3;
+#pragma unroll
+    for (int q = 3; q >= 0; --q)
+      if (acc + h[0] + (q >= 1 ? h[1] : 0) + (q >= 2 ? h[2] : 0) + (q >= 3 ? h[3] : 0) >= (uint32_t)kk) bin = lane * 4 + q;
+  }
+  bin = __shfl(bin, owner);
+  // Smallest key in the bin; everything at or above it is kept.
+  const uint32_t drop = ((uint32_t)bin + 1u) << shift;
+  uint32_t tk = kmax - min(drop, kmax) + 1u;
+  tk = max(tk, floor_key);
+  int kept = 0;
+  uint64_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + lane;
+    v[r] = i < count ? sm.list[i] : 0ull;
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + lane;
+    const bool keep = i < count && k[r] >= tk;
+    const uint64_t m = __ballot(keep);
+    if (keep) sm.list[kept + (int)lanes_below(m)] = v[r];
+    kept += (int)__popcll(m);
+  }
+  wave_lds_sync();
+  if (kept > kWListCap - kWaveSize) {  // massive ties: sort and cut exactly
+    wave_sort_list<R>(sm.list, kept, kk);
+    kept = kk;
+    tk = composite_key(sm.list[kk - 1]);
+  }
+  *theta_key = tk;
+  return kept;
+}
+
+template <typename In, int VEC>
+__global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) {
+  __shared__ WaveSmem sm;
+
+  const int splits = L.splits;
+  const int row = (int)blockIdx.x / splits;
+  const int slice = (int)blockIdx.x - row * splits;
+  const int V = L.vocab;
+  const int begin = slice * L.slice_len;
+  const int n = min(L.slice_len, V - begin);
+  const int nchunks = (n + kWChunk - 1) / kWChunk;
+  const tabby_row_params P = L.params[row];
+  const bool valid_params = params_valid(P, L.k_max);
+  const int keff = effective_k(P, V);
+  const bool finite = valid_params && keff <= L.kcap;
+  const int kk = finite ? min(keff, n) : 0;
+  const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
+  uint64_t *region = W.cands + (size_t)row * W.row_cand_stride + (size_t)begin;
+
+  float lane_max = -INFINITY;
+  double lane_sum = 0.0;       // sum of exp(x - lane_max) over this lane's elements so far
+  int count = 0;               // entries in the list (wave-uniform)
+  uint32_t theta_key = kNegInfKey;
+  float theta = -INFINITY;     // == value_of(theta_key)
+
+  float x[kWChunkPerLane], y[kWChunkPerLane];
+  wave_load<In, VEC>(src, n, 0, x);
+  for (int c = 0; c < nchunks; ++c) {
+    wave_load<In, VEC>(src, n, min(c + 1, nchunks - 1), y);  // in flight during this chunk
+    const bool last = c == nchunks - 1;
+    if (last) {
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e)
+        if (wave_local<VEC>(c, e) >= n) x[e] = -INFINITY;
+    }
+
+    float cm = x[0];
+#pragma unroll
+    for (int e = 1; e < kWChunkPerLane; ++e) cm = fmaxf(cm, x[e]);
+    const float nm = fmaxf(lane_max, cm);
+    if (nm != -INFINITY) {
+      const float ml = nm * kLog2e;
+      float part = 0.0f;
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e) part += __builtin_amdgcn_exp2f(fmaf(x[e], kLog2e, -ml));
+      const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f((lane_max - nm) * kLog2e);
+      lane_sum = lane_sum * rescale + (double)part;
+      lane_max = nm;
+    }
+
+    if (kk > 0) {
+      if (c == 0 && kk < n && kk <= kWaveSize) {
+        uint32_t k1[1] = {key_of(cm)};
+        wave_sort_desc<1>(k1);
+        theta_key = min(max((uint32_t)__shfl((int)k1[0], kk - 1), kNegInfKey), 0xff800000u);
+        theta = value_of(theta_key);
+      }
+      // Padding (-inf) passes only a theta of -inf; only then is the index checked.
+      const bool check = last && !(theta > -INFINITY);
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e) {
+        if (count > kWListCap - kWaveSize) {
+          count = wave_prune(sm, count, kk, &theta_key);
+          theta = value_of(theta_key);
+        }
+        const int local = wave_local<VEC>(c, e);
+        const bool take = x[e] >= theta && (!check || local < n);
+        const uint64_t mask = __ballot(take);
+        if (mask) {
+          if (take) sm.list[count + (int)lanes_below(mask)] = composite(key_of(x[e]), (uint32_t)(begin + local));
+          count += (int)__popcll(mask);
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kWChunkPerLane; ++e) x[e] = y[e];
+  }
+
+  const float ms = wave_max(lane_max);
+  const double term = lane_max == -INFINITY
+                          ? 0.0
+                          : lane_sum * (double)__builtin_amdgcn_exp2f((lane_max - ms) * kLog2e);
+  const double ss = wave_sum(term);
+  if (kk > 0) {
+    if (count > 2 * kk && count >= kk) count = wave_prune(sm, count, kk, &theta_key);
+    wave_lds_sync();
+    for (int i = wave_lane(); i < count; i += kWaveSize) region[i] = sm.list[i];
+  }
+  if (wave_lane() == 0) {
+    SliceStat st_out;
+    st_out.max = ms;
+    st_out.count = (uint32_t)count;
+    st_out.sum = ss;
+    W.stats[(size_t)row * kMaxSplits + slice] = st_out;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Kernel 2 (merge): one workgroup per row. Row max and sum-exp from the slice statistics
+// (in slice order, so the result does not depend on scheduling), the exact top-keff of the
+// slices' candidates, an LDS bitonic sort, and sampleFromTopK.
+// ---------------------------------------------------------------------------------------
+constexpr int kCandLds = 8192;  // candidate lists up to this size are staged in LDS
+
+template <int KCAP>
+struct MergeSmem {
+  BlockScratch bs;
+  float row_max;
+  double sum_exp;
+  double pool_mass;
+  double scaled_total;
+  uint32_t slice_first[kMaxSplits];
+  double slice_term[kMaxSplits];
+  uint64_t sorted[KCAP];
+  uint64_t cand[kCandLds];
+  union {
+    uint32_t hist[kBins];
+    struct {
+      double exact[KCAP];
+      double w[KCAP];
+    } tail;
+  } u;
+};
+
+template <int KCAP, typename In>
+__global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
+  __shared__ MergeSmem<KCAP> sm;
+  const int row = (int)blockIdx.x;
+  const int splits = L.splits;
+  const int V = L.vocab;
+  const tabby_row_params P = L.params[row];
+  const bool valid_params = params_valid(P, L.k_max);
+  const int keff = effective_k(P, V);
+  const bool finite = valid_params && keff <= L.kcap;
+  const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V;
+
+  // 0. Candidate counts per slice (in the statistics) and their offsets; then the
+  //    candidate loads are issued together, ahead of the statistics math.
   const SliceStat *stats = W.stats + (size_t)row * kMaxSplits;
-  float M = -INFINITY;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, stats[s].max);
-  if ((int)threadIdx.x < splits) {
-    const SliceStat st_s = stats[threadIdx.x];
-    sm.slice_term[threadIdx.x] =
-        st_s.max == -INFINITY ? 0.0 : st_s.sum * fdlibm_exp((double)st_s.max - (double)M);
+  SliceStat mine;
+  mine.max = -INFINITY;
+  mine.count = 0u;
+  mine.sum = 0.0;
+  if ((int)threadIdx.x < splits) mine = stats[threadIdx.x];
+  uint32_t total_u;
+  const uint32_t first = block_exclusive_scan(finite ? mine.count : 0u, sm.bs, &total_u);
+  if ((int)threadIdx.x < splits) sm.slice_first[threadIdx.x] = first;
+  __syncthreads();
+  const int C = (int)total_u;
+  const uint64_t *cands = W.cands + (size_t)row * W.row_cand_stride;
+  // Flat candidate i lives in slice s (the last with slice_first[s] <= i), at
+  // cands[s*slice_len + i - slice_first[s]].
+  auto cand_addr = [&](int i) {
+    int lo = 0, hi = splits - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((int)sm.slice_first[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    return cands + (size_t)lo * L.slice_len + (i - (int)sm.slice_first[lo]);
+  };
+  const bool staged = C <= kCandLds;
+  if (staged) {
+    constexpr int B = 8;
+    for (int base = 0; base < C; base += B * kBlock) {
+      uint64_t v[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int i = base + u * kBlock + (int)threadIdx.x;
+        v[u] = i < C ? *cand_addr(i) : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int i = base + u * kBlock + (int)threadIdx.x;
+        if (i < C) sm.cand[i] = v[u];
+      }
+    }
   }
+  if (threadIdx.x == 0) sm.bs.slot = 0u;
+
+  // 1. Row max and sum-exp, in slice order.
+  const float M = block_max(mine.max, sm.bs);
+  if ((int)threadIdx.x < splits)
+    sm.slice_term[threadIdx.x] =
+        mine.max == -INFINITY ? 0.0 : mine.sum * fdlibm_exp((double)mine.max - (double)M);
   __syncthreads();
   if (threadIdx.x == 0) {
     double S = 0.0;
     for (int s = 0; s < splits; ++s) S += sm.slice_term[s];
-    sm.row_max = M;
     sm.sum_exp = S;
   }
   __syncthreads();
-  const float row_max = sm.row_max;
+  const float row_max = M;
   const double sum_exp = sm.sum_exp;
   const bool in_domain = (row_max > -INFINITY) && (row_max < INFINITY) && (sum_exp > 0.0) &&
                          (sum_exp < INFINITY);
-  if (threadIdx.x == 0) W.arrivals[row] = 0u;  // ready for the next launch
 
   if (!valid_params || !in_domain) {
     if (threadIdx.x == 0) {
       write_status(L, row, !valid_params ? TABBY_EINVAL : TABBY_EDOMAIN, row_max, sum_exp);
-      if (!finite) W.row_state[row].status = !valid_params ? TABBY_EINVAL : TABBY_EDOMAIN;
+      W.row_state[row].status = !valid_params ? TABBY_EINVAL : TABBY_EDOMAIN;
     }
     return;
   }
@@ -415,7 +935,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(Launch L, Workspace W) {
     return;
   }
   if (!finite) {
-    // Whole-vocabulary row: hand max / sum-exp / the head threshold to head_kernel.
+    // Whole-vocabulary row: hand max / sum-exp / the head threshold to the head kernels.
     if (threadIdx.x == 0) {
       RowState rs;
       rs.max = row_max;
@@ -428,7 +948,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(Launch L, Workspace W) {
       } else {
         // Smallest key whose scaled logit (l - max)/T in f64 is >= -40. Anything below has
         // exp(.) < 2^-54 and can change neither the scaled total nor a running sum, both of
-        // which are >= their first term when it is added (see finish_head).
+        // which are >= their first term when it is added.
         uint32_t lo = kNegInfKey, hi = top;
         while (hi - lo > 1u) {
           const uint32_t mid = lo + (hi - lo) / 2u;
@@ -443,39 +963,58 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(Launch L, Workspace W) {
     return;
   }
 
-  // 7. Merge the slices' candidates: exact top-keff by radix select, then sort.
-  auto cands = [&](auto &&f) {
-    for (int s = 0; s < splits; ++s) {
-      const int ns = min(L.slice_len, V - s * L.slice_len);
-      const int cs = min(keff, ns);
-      const uint64_t *src = W.cands + ((size_t)row * kMaxSplits + s) * W.cand_stride;
-      for (int i = threadIdx.x; i < cs; i += kBlock) f(src[i]);
+  // 2. The exact top-keff of the row's candidates, sorted. The candidates include every
+  //    element of the row's top-keff (each slice kept all elements >= a lower bound of its
+  //    own kk-th largest value).
+  auto from_lds = [&](auto &&f) {
+    for (int i = threadIdx.x; i < C; i += kBlock) f(sm.cand[i]);
+  };
+  auto from_global = [&](auto &&f) {
+    constexpr int B = 8;  // loads in flight per lane before the first use
+    for (int base = 0; base < C; base += B * kBlock) {
+      uint64_t v[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int i = base + u * kBlock + (int)threadIdx.x;
+        v[u] = i < C ? *cand_addr(i) : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u)
+        if (base + u * kBlock + (int)threadIdx.x < C) f(v[u]);
     }
   };
-  int total_cands = 0;
-  for (int s = 0; s < splits; ++s) total_cands += min(keff, min(L.slice_len, V - s * L.slice_len));
-  if (threadIdx.x == 0) sm.bs.slot = 0;
-  __syncthreads();
-  if (total_cands > keff) {
-    const SelectResult r = radix_select(cands, (uint32_t)keff, sm.u.hist, sm.bs);
-    cands([&](uint64_t v) {
-      if (selected(v, r)) {
+  auto gather = [&](auto &&each) {
+    if (C > keff) {
+      const SelectResult r = radix_select(each, (uint32_t)keff, sm.u.hist, sm.bs);
+      each([&](uint64_t v) {
+        if (selected(v, r)) {
+          const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
+          if (at < (uint32_t)keff) sm.sorted[at] = v;
+        }
+      });
+    } else {
+      each([&](uint64_t v) {
         const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
         if (at < (uint32_t)keff) sm.sorted[at] = v;
-      }
-    });
-  } else {
-    cands([&](uint64_t v) {
-      const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
-      if (at < (uint32_t)keff) sm.sorted[at] = v;
-    });
+      });
+    }
+  };
+  if (staged) gather(from_lds); else gather(from_global);
+  __syncthreads();
+
+  // 3. Sort and sampleFromTopK: by wave 0 in registers for pools up to 256, else by the
+  //    workgroup through LDS.
+  if (keff <= kWaveKcap) {
+    if (wave_id() != 0) return;
+    if (keff <= 64) wave_finish<1, In>(sm.sorted, keff, L, row, row_src, row_max, sum_exp, P);
+    else if (keff <= 128) wave_finish<2, In>(sm.sorted, keff, L, row, row_src, row_max, sum_exp, P);
+    else wave_finish<4, In>(sm.sorted, keff, L, row, row_src, row_max, sum_exp, P);
+    return;
   }
   const int npow = next_pow2(keff);
   for (int i = keff + (int)threadIdx.x; i < npow; i += kBlock) sm.sorted[i] = 0ull;
   __syncthreads();
   bitonic_sort_desc(sm.sorted, npow);
-
-  // 8. sampleFromTopK.
   finish_row<KCAP, In>(sm, L, row, row_src, keff, row_max, sum_exp, P);
 }
 
@@ -530,50 +1069,56 @@ int hip_fail(hipError_t e, const char *what) {
   } while (0)
 
 struct Plan {
-  int elems;
   int slice_len;
   int splits;
   int vec;
 };
 
-// Large slices (64 elements per lane) when the batch alone fills the chip; small ones
-// (16 per lane) for a few rows, to spread a row over more CUs.
-Plan make_plan(int rows, int vocab, int dtype, const void *logits) {
+// Enough slices per row that the batch fills the chip about once: 256 CUs x 5 resident
+// 256-lane workgroups, or x 24 resident one-wave workgroups for the wave kernel. Each
+// slice is at least one chunk long and aligned to the vector loads.
+constexpr int kTargetGroups = 1280;
+constexpr int kTargetWaves = 6144;
+
+Plan make_plan(int rows, int vocab, int dtype, const void *logits, bool wave) {
   Plan p;
-  const int large_splits = (vocab + kMaxSliceLen - 1) / kMaxSliceLen;
-  p.elems = ((int64_t)rows * large_splits >= 512) ? kSliceElemsLarge : kSliceElemsSmall;
-  p.slice_len = p.elems * kBlock;
-  p.splits = (vocab + p.slice_len - 1) / p.slice_len;
   const int vec_elems = dtype == TABBY_F32 ? 4 : 8;
   const bool aligned = ((uintptr_t)logits % 16u) == 0 && vocab % vec_elems == 0;
   p.vec = aligned ? vec_elems : 1;
+  const int chunk = wave ? kWChunk : kChunk;
+  const int target = wave ? kTargetWaves : kTargetGroups;
+  const int most = std::min(kMaxSplits, (vocab + chunk - 1) / chunk);
+  const int want = std::max(1, std::min(most, (target + rows - 1) / rows));
+  const int granule = (wave ? kWaveSize : kBlock) * p.vec;
+  const int per = (vocab + want - 1) / want;
+  p.slice_len = (per + granule - 1) / granule * granule;
+  p.splits = (vocab + p.slice_len - 1) / p.slice_len;
   return p;
 }
 
-template <typename In, int VEC, int ELEMS>
-hipError_t launch_sample(const Launch &L, const Workspace &W, hipStream_t stream) {
-  const dim3 grid((unsigned)(L.rows * L.splits));
-  if (L.kcap <= kKcapSmall) {
-    hipLaunchKernelGGL((sample_kernel<In, VEC, ELEMS, kKcapSmall>), grid, dim3(kBlock), 0, stream, L, W);
+template <typename In, int VEC>
+hipError_t launch_pair(const Launch &L, const Workspace &W, hipStream_t stream) {
+  const dim3 slices((unsigned)(L.rows * L.splits)), rows((unsigned)L.rows);
+  if (L.kcap <= kWaveKcap) {
+    hipLaunchKernelGGL((wave_kernel<In, VEC>), slices, dim3(kWaveSize), 0, stream, L, W);
   } else {
-    hipLaunchKernelGGL((sample_kernel<In, VEC, ELEMS, kKcapLarge>), grid, dim3(kBlock), 0, stream, L, W);
+    hipLaunchKernelGGL((slice_kernel<In, VEC>), slices, dim3(kBlock), 0, stream, L, W);
+  }
+  if (L.kcap <= kKcapSmall) {
+    hipLaunchKernelGGL((merge_kernel<kKcapSmall, In>), rows, dim3(kBlock), 0, stream, L, W);
+  } else {
+    hipLaunchKernelGGL((merge_kernel<kKcapLarge, In>), rows, dim3(kBlock), 0, stream, L, W);
   }
   return hipGetLastError();
 }
 
-template <typename In, int VEC>
-hipError_t dispatch_elems(const Plan &p, const Launch &L, const Workspace &W, hipStream_t s) {
-  if (p.elems == kSliceElemsLarge) return launch_sample<In, VEC, kSliceElemsLarge>(L, W, s);
-  return launch_sample<In, VEC, kSliceElemsSmall>(L, W, s);
-}
-
 hipError_t dispatch(int dtype, const Plan &p, const Launch &L, const Workspace &W, hipStream_t s) {
   if (dtype == TABBY_F32) {
-    if (p.vec == 4) return dispatch_elems<float, 4>(p, L, W, s);
-    return dispatch_elems<float, 1>(p, L, W, s);
+    if (p.vec == 4) return launch_pair<float, 4>(L, W, s);
+    return launch_pair<float, 1>(L, W, s);
   }
-  if (p.vec == 8) return dispatch_elems<uint16_t, 8>(p, L, W, s);
-  return dispatch_elems<uint16_t, 1>(p, L, W, s);
+  if (p.vec == 8) return launch_pair<uint16_t, 8>(L, W, s);
+  return launch_pair<uint16_t, 1>(L, W, s);
 }
 
 int check_common(tabby_sampler *h, const void *logits, int32_t dtype, int32_t rows, int32_t vocab,
@@ -601,8 +1146,8 @@ int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_
                          tabby_sampler **out) {
   if (!out) return fail(TABBY_EINVAL, "out pointer is null");
   *out = nullptr;
-  if (vocab_max < 1 || vocab_max > kMaxSplits * kMinSliceLen)
-    return fail(TABBY_EINVAL, "vocab_max must be between 1 and " + std::to_string(kMaxSplits * kMinSliceLen));
+  if (vocab_max < 1 || vocab_max > kMaxSplits * kChunk)
+    return fail(TABBY_EINVAL, "vocab_max must be between 1 and " + std::to_string(kMaxSplits * kChunk));
   if (rows_max < 1 || rows_max > (1 << 20)) return fail(TABBY_EINVAL, "rows_max must be between 1 and 1048576");
   if (k_max < 1 || k_max > kKcapLarge)
     return fail(TABBY_ECAPACITY, "k_max must be between 1 and " + std::to_string(kKcapLarge));
@@ -613,9 +1158,7 @@ int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_
   h->vocab_max = vocab_max;
   h->rows_max = rows_max;
   h->k_max = k_max;
-  // A slice emits min(keff, n) candidates and keff can reach the kernel's pool capacity
-  // (top_k >= vocab with vocab <= capacity), so the stride is the capacity, not k_max.
-  h->ws.cand_stride = std::min(k_max <= kKcapSmall ? kKcapSmall : kKcapLarge, kMaxSliceLen);
+  h->ws.row_cand_stride = vocab_max;  // each slice may flush up to its own length
 
   const size_t rows = (size_t)rows_max;
   size_t off = 0;
@@ -626,7 +1169,7 @@ int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_
   };
   const size_t o_arr = carve(rows * 4), o_harr = carve(rows * 4), o_hcnt = carve(rows * 4);
   const size_t o_stats = carve(rows * kMaxSplits * sizeof(SliceStat));
-  const size_t o_cands = carve(rows * kMaxSplits * (size_t)h->ws.cand_stride * 8);
+  const size_t o_cands = carve(rows * (size_t)h->ws.row_cand_stride * 8);
   const size_t o_rs = carve(rows * sizeof(RowState));
   const size_t o_par = carve(rows * sizeof(tabby_row_params));
   const size_t o_res = carve(rows * sizeof(tabby_row_result));
@@ -683,7 +1226,8 @@ int tabby_sampler_sample_device(tabby_sampler *h, const void *logits_dev, int32_
   if (flags & TABBY_FLAG_FULL_VOCAB)
     return fail(TABBY_ECAPACITY, "whole-vocabulary pools (top_k = 0) are not available in this build");
 
-  const Plan p = make_plan(rows, vocab, dtype, logits_dev);
+  const int kcap = h->k_max <= kKcapSmall ? kKcapSmall : kKcapLarge;
+  const Plan p = make_plan(rows, vocab, dtype, logits_dev, kcap <= kWaveKcap);
   Launch L;
   L.logits = logits_dev;
   L.params = params_dev;
@@ -696,7 +1240,7 @@ int tabby_sampler_sample_device(tabby_sampler *h, const void *logits_dev, int32_
   L.slice_len = p.slice_len;
   L.topk_cap = topk_cap;
   L.k_max = h->k_max;
-  L.kcap = h->k_max <= kKcapSmall ? kKcapSmall : kKcapLarge;
+  L.kcap = kcap;
   L.head_pass = 0;
   HIP_TRY(hipSetDevice(h->device));
   HIP_TRY(dispatch(dtype, p, L, h->ws, (hipStream_t)stream));
