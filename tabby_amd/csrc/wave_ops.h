@@ -67,4 +67,5 @@ __device__ __forceinline__ void wave_sort_desc(T (&v)[R]) {
   }
 }
 
+
 }  // namespace tabby
