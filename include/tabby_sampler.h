@@ -86,7 +86,9 @@ TABBY_API int tabby_sampler_destroy(tabby_sampler *sampler);
  * TopKResult ids/logits, forward.ts:93-103). Asynchronous on `stream` (a hipStream_t, NULL
  * for the default stream). Parameters are validated on the device: a bad row gets a
  * nonzero status and the other rows are still sampled.
- * `flags`: TABBY_FLAG_FULL_VOCAB must be set if any row may have top_k = 0 (or >= vocab).
+ * `flags`: TABBY_FLAG_FULL_VOCAB must be set if any row may have top_k = 0 (or >= vocab)
+ * with vocab above the pool capacity; such a row's pool is the whole vocabulary, and its
+ * top-k output holds the first min(topk_cap, vocab) entries of it (topk_cap <= k_max).
  */
 #define TABBY_FLAG_FULL_VOCAB 1u
 TABBY_API int tabby_sampler_sample_device(tabby_sampler *sampler, const void *logits_dev, int32_t dtype,

@@ -63,10 +63,10 @@ struct Workspace {
   SliceStat *stats;         // [rows_cap * kMaxSplits]
   uint64_t *cands;          // [rows_cap * row_cand_stride]
   RowState *row_state;      // [rows_cap]
-  uint64_t *head;           // [head_rows * head_stride] (whole-vocabulary rows only)
-  uint64_t *head_sorted;    // [head_rows * head_stride]
-  double *head_exact;       // [head_rows * head_stride]
-  double *head_w;           // [head_rows * head_stride]
+  uint64_t *head;           // [head_rows * head_stride] whole-vocabulary rows: the head
+  uint64_t *head_sorted;    // [head_rows * head_stride] the head, sorted
+  double *head_s;           // [head_rows * head_stride] exp((l - max)/T) in sorted order
+  double *head_c;           // [head_rows * head_stride] running sums of the weights
   int64_t row_cand_stride;  // composites per row in cands
   int32_t head_stride;
 };
@@ -84,7 +84,9 @@ struct Launch {
   int32_t topk_cap;
   int32_t k_max;     // largest top_k the handle accepts
   int32_t kcap;      // largest pool the sampling kernel finishes itself
-  int32_t head_pass; // 1 when head_kernel runs after this launch
+  int32_t head_pass; // 1 when the head kernels run after this launch
+  int32_t h_splits;  // slices per row of the head kernel
+  int32_t h_slice_len;
 };
 
 // ---------------------------------------------------------------------------------------
@@ -149,6 +151,17 @@ __device__ __forceinline__ int32_t effective_k(const tabby_row_params &p, int vo
 __device__ __forceinline__ bool params_valid(const tabby_row_params &p, int k_max) {
   return p.top_k >= 0 && p.top_k <= k_max && p.reserved == 0 && !(p.uniform < 0.0) &&
          !(p.uniform >= 1.0) && p.uniform == p.uniform;
+}
+
+// How many of its largest elements a slice keeps as candidates: the row's pool for a row
+// whose pool fits the kernels (keff <= kcap); for a whole-vocabulary row, the top-k list the
+// caller asked for (topk_cap <= k_max <= kcap), which the merge uses to lower the row's head
+// threshold far enough that the head holds that list.
+__device__ __forceinline__ int slice_keep(bool valid, int keff, int n, int kcap, int head_pass,
+                                          int topk_cap) {
+  if (!valid) return 0;
+  if (keff <= kcap) return min(keff, n);
+  return head_pass ? min(topk_cap, n) : 0;
 }
 
 // sampleFromTopK (src/engine/sampler.ts:147-212) over the `count` sorted candidates in
@@ -469,8 +482,7 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
   const tabby_row_params P = L.params[row];
   const bool valid_params = params_valid(P, L.k_max);
   const int keff = effective_k(P, V);
-  const bool finite = valid_params && keff <= L.kcap;
-  const int kk = finite ? min(keff, n) : 0;
+  const int kk = slice_keep(valid_params, keff, n, L.kcap, L.head_pass, L.topk_cap);
   const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
   // The slice's candidate region: room for every element of the slice.
   uint64_t *region = W.cands + (size_t)row * W.row_cand_stride + (size_t)begin;
@@ -772,8 +784,7 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   const tabby_row_params P = L.params[row];
   const bool valid_params = params_valid(P, L.k_max);
   const int keff = effective_k(P, V);
-  const bool finite = valid_params && keff <= L.kcap;
-  const int kk = finite ? min(keff, n) : 0;
+  const int kk = slice_keep(valid_params, keff, n, L.kcap, L.head_pass, L.topk_cap);
   const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
   uint64_t *region = W.cands + (size_t)row * W.row_cand_stride + (size_t)begin;
   // The row's shared bound applies when this wave selects the row's whole pool.
@@ -930,7 +941,8 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
   mine.sum = 0.0;
   if ((int)threadIdx.x < splits) mine = stats[threadIdx.x];
   uint32_t total_u;
-  const uint32_t first = block_exclusive_scan(finite ? mine.count : 0u, sm.bs, &total_u);
+  const bool collects = valid_params && (finite || L.head_pass);
+  const uint32_t first = block_exclusive_scan(collects ? mine.count : 0u, sm.bs, &total_u);
   if ((int)threadIdx.x < splits) sm.slice_first[threadIdx.x] = first;
   __syncthreads();
   const int C = (int)total_u;
@@ -998,35 +1010,6 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
     if (threadIdx.x == 0) write_status(L, row, TABBY_EINVAL, row_max, sum_exp);
     return;
   }
-  if (!finite) {
-    // Whole-vocabulary row: hand max / sum-exp / the head threshold to the head kernels.
-    if (threadIdx.x == 0) {
-      RowState rs;
-      rs.max = row_max;
-      rs.sum_exp = sum_exp;
-      rs.status = TABBY_OK;
-      rs.pad = 0;
-      const uint32_t top = key_of(row_max);
-      if (P.temperature <= 0.0) {
-        rs.head_key = top;  // greedy needs only the row's maxima
-      } else {
-        // Smallest key whose scaled logit (l - max)/T in f64 is >= -40. Anything below has
-        // exp(.) < 2^-54 and can change neither the scaled total nor a running sum, both of
-        // which are >= their first term when it is added.
-        uint32_t lo = kNegInfKey, hi = top;
-        while (hi - lo > 1u) {
-          const uint32_t mid = lo + (hi - lo) / 2u;
-          const double q = ((double)value_of(mid) - (double)row_max) / P.temperature;
-          if (q >= -40.0) hi = mid; else lo = mid;
-        }
-        rs.head_key = hi;
-      }
-      W.row_state[row] = rs;
-      W.head_count[row] = 0u;
-    }
-    return;
-  }
-
   // 2. The exact top-keff of the row's candidates, sorted. The candidates include every
   //    element of the row's top-keff (each slice kept all elements >= a lower bound of its
   //    own kk-th largest value).
@@ -1051,6 +1034,48 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
         if (base + u * kBlock + (int)threadIdx.x < C && composite_key(v[u]) >= floor_key) f(v[u]);
     }
   };
+  if (!finite) {
+    // Whole-vocabulary row: hand max / sum-exp / the head threshold to the head kernels.
+    // The threshold also covers the caller's top-k list: the candidates hold the row's
+    // top topk_cap elements, and the key of the topk_cap-th largest bounds the head below.
+    uint32_t list_key = 0xffffffffu;
+    const int need = min(L.topk_cap, V);
+    if (need > 0) {
+      if (C > need) {
+        const SelectResult r = staged ? radix_select(from_lds, (uint32_t)need, sm.u.hist, sm.bs)
+                                      : radix_select(from_global, (uint32_t)need, sm.u.hist, sm.bs);
+        // Every selected composite is >= r.prefix, whose low bits below r.shift are zero.
+        list_key = (uint32_t)(r.prefix >> 32);
+      } else {
+        list_key = kNegInfKey;  // fewer candidates than the list: take the whole row
+      }
+    }
+    if (threadIdx.x == 0) {
+      RowState rs;
+      rs.max = row_max;
+      rs.sum_exp = sum_exp;
+      rs.status = TABBY_OK;
+      rs.pad = 0;
+      const uint32_t top = key_of(row_max);
+      uint32_t head_key = top;  // greedy needs only the row's maxima
+      if (P.temperature > 0.0) {
+        // Smallest key whose scaled logit (l - max)/T in f64 is >= -40. Anything below has
+        // exp(.) < 2^-54 and can change neither the scaled total nor a running sum, both of
+        // which are >= their first term when it is added.
+        uint32_t lo = kNegInfKey, hi = top;
+        while (hi - lo > 1u) {
+          const uint32_t mid = lo + (hi - lo) / 2u;
+          const double q = ((double)value_of(mid) - (double)row_max) / P.temperature;
+          if (q >= -40.0) hi = mid; else lo = mid;
+        }
+        head_key = hi;
+      }
+      rs.head_key = min(head_key, list_key);
+      W.row_state[row] = rs;
+      W.head_count[row] = 0u;
+    }
+    return;
+  }
   auto gather = [&](auto &&each) {
     if (C > keff) {
       const SelectResult r = radix_select(each, (uint32_t)keff, sm.u.hist, sm.bs);
@@ -1084,6 +1109,246 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
   __syncthreads();
   bitonic_sort_desc(sm.sorted, npow);
   finish_row<KCAP, In>(sm, L, row, row_src, keff, row_max, sum_exp, P);
+}
+
+// ---------------------------------------------------------------------------------------
+// Whole-vocabulary rows (top_k = 0, or >= vocab beyond the pool capacity). The pool is the
+// entire row sorted, but only its head matters to sampleFromTopK: with the row max M, an
+// element whose (l - M)/T is below -40 has exp(.) < 2^-54, and it is added -- in sorted
+// order, after every larger term -- to the scaled total (>= 1, the max's own term) or to a
+// running weight sum (>= the first weight), so it cannot change either by rounding. The
+// merge computes head_key, the smallest key with (l - M)/T >= -40 in f64 (or the max's key
+// when T <= 0). head_kernel collects the head; head_finish_kernel sorts it and runs the
+// tail. poolMass takes the head's terms plus the rest of sum-exp.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ bool is_head_row(const tabby_row_params &P, const Launch &L) {
+  return params_valid(P, L.k_max) && effective_k(P, L.vocab) > L.kcap;
+}
+
+// Appends the wave's list to the row's head buffer and empties it.
+__device__ __forceinline__ void flush_head(uint64_t *list, int count, uint32_t *head_count, uint64_t *head) {
+  wave_lds_sync();
+  uint32_t base = 0;
+  if (wave_lane() == 0) base = atomicAdd(head_count, (uint32_t)count);
+  base = (uint32_t)__shfl((int)base, 0);
+  for (int i = wave_lane(); i < count; i += kWaveSize) head[base + i] = list[i];
+  wave_lds_sync();
+}
+
+template <typename In, int VEC>
+__global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) {
+  __shared__ uint64_t list[kWListCap];
+  const int splits = L.h_splits;
+  const int row = (int)blockIdx.x / splits;
+  const int slice = (int)blockIdx.x - row * splits;
+  const tabby_row_params P = L.params[row];
+  if (!is_head_row(P, L)) return;
+  const RowState rs = W.row_state[row];
+  if (rs.status != TABBY_OK) return;
+  const int V = L.vocab;
+  const int begin = slice * L.h_slice_len;
+  const int n = min(L.h_slice_len, V - begin);
+  const int nchunks = (n + kWChunk - 1) / kWChunk;
+  const int full_chunks = n / kWChunk;
+  const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
+  const float hv = value_of(rs.head_key);
+  uint32_t *head_count = W.head_count + row;
+  uint64_t *head = W.head + (size_t)row * W.head_stride;
+
+  int count = 0;
+  float x[kWChunkPerLane], y[kWChunkPerLane];
+  if (full_chunks > 0) wave_load_full<In, VEC>(src, 0, x); else wave_load<In, VEC>(src, n, 0, x);
+  for (int c = 0; c < nchunks; ++c) {
+    const int nc = min(c + 1, nchunks - 1);
+    if (nc < full_chunks) wave_load_full<In, VEC>(src, nc, y); else wave_load<In, VEC>(src, n, nc, y);
+    if (c >= full_chunks) {
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e)
+        if (wave_local<VEC>(c, e) >= n) x[e] = __builtin_nanf("");  // fails x >= hv
+    }
+#pragma unroll
+    for (int e = 0; e < kWChunkPerLane; ++e) {
+      if (count > kWListCap - kWaveSize) {
+        flush_head(list, count, head_count, head);
+        count = 0;
+      }
+      const bool take = x[e] >= hv;
+      const uint64_t mask = __ballot(take);
+      if (mask) {
+        if (take) list[count + (int)lanes_below(mask)] = composite(key_of(x[e]), (uint32_t)(begin + wave_local<VEC>(c, e)));
+        count = __builtin_amdgcn_readfirstlane(count + (int)__popcll(mask));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kWChunkPerLane; ++e) x[e] = y[e];
+  }
+  if (count > 0) flush_head(list, count, head_count, head);
+}
+
+constexpr int kHeadBatch = 4096;
+
+struct HeadSmem {
+  BlockScratch bs;
+  uint64_t batch[kHeadBatch];
+  double vals[kHeadBatch];
+  uint32_t hist[kBins];
+  double scaled_total;
+  double run;
+  int cut;
+};
+
+template <typename In>
+__global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace W) {
+  __shared__ HeadSmem sm;
+  const int row = (int)blockIdx.x;
+  const tabby_row_params P = L.params[row];
+  if (!is_head_row(P, L)) return;
+  const RowState rs = W.row_state[row];
+  if (rs.status != TABBY_OK) return;
+  const int V = L.vocab;
+  const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V;
+  const int H = (int)W.head_count[row];
+  const uint64_t *head = W.head + (size_t)row * W.head_stride;
+  uint64_t *sorted = W.head_sorted + (size_t)row * W.head_stride;
+  double *sg = W.head_s + (size_t)row * W.head_stride;
+  double *cg = W.head_c + (size_t)row * W.head_stride;
+  const float M = rs.max;
+  const double S1 = rs.sum_exp;
+  const double T = P.temperature;
+
+  // Pass 1: the head in descending batches of up to kHeadBatch; each batch is the top of
+  // what is left below the previous batch's smallest entry.
+  if (threadIdx.x == 0) sm.scaled_total = 0.0;
+  double pool_head = 0.0, e_head = 0.0;
+  uint64_t upper = ~0ull;  // exclusive; real composites are all smaller
+  for (int pos = 0; pos < H;) {
+    const int b = min(kHeadBatch, H - pos);
+    if (threadIdx.x == 0) sm.bs.slot = 0u;
+    __syncthreads();
+    auto below = [&](auto &&f) {
+      constexpr int B = 8;
+      for (int base = 0; base < H; base += B * kBlock) {
+        uint64_t v[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int i = base + u * kBlock + (int)threadIdx.x;
+          v[u] = i < H ? head[i] : ~0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+          if (v[u] < upper) f(v[u]);
+      }
+    };
+    if (H - pos > b) {
+      const SelectResult r = radix_select(below, (uint32_t)b, sm.hist, sm.bs);
+      below([&](uint64_t v) {
+        if (selected(v, r)) {
+          const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
+          if (at < (uint32_t)b) sm.batch[at] = v;
+        }
+      });
+    } else {
+      below([&](uint64_t v) {
+        const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
+        if (at < (uint32_t)b) sm.batch[at] = v;
+      });
+    }
+    const int npow = next_pow2(b);
+    for (int i = b + (int)threadIdx.x; i < npow; i += kBlock) sm.batch[i] = 0ull;
+    __syncthreads();
+    bitonic_sort_desc(sm.batch, npow);
+    double pool_part = 0.0, e_part = 0.0;
+    for (int i = threadIdx.x; i < b; i += kBlock) {
+      const uint64_t v = sm.batch[i];
+      const double d = (double)value_of(composite_key(v)) - (double)M;
+      const double e = fdlibm_exp(d);
+      const double sv = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
+      pool_part += e / S1;
+      e_part += e;
+      sm.vals[i] = sv;
+      sorted[pos + i] = v;
+      sg[pos + i] = sv;
+    }
+    pool_head += block_sum(pool_part, sm.bs);
+    e_head += block_sum(e_part, sm.bs);
+    if (threadIdx.x == 0) {  // the scaled total, sequentially in sorted order
+      double S = sm.scaled_total;
+      for (int i = 0; i < b; ++i) S += sm.vals[i];
+      sm.scaled_total = S;
+    }
+    upper = sm.batch[b - 1];
+    pos += b;
+    __syncthreads();
+  }
+  // poolMass: the head's exact terms plus the mass of everything below the head.
+  const double pool_mass = pool_head + fmax(0.0, S1 - e_head) / S1;
+
+  tabby_row_result res;
+  res.max_logit = M;
+  res.sum_exp = S1;
+  res.pool_mass = pool_mass;
+  res.status = TABBY_OK;
+  res.topk_count = min(H, L.topk_cap);
+  int chosen = 0;
+  if (T <= 0.0) {
+    res.considered = 1;
+    res.pool_exhausted = 0;
+  } else {
+    // Pass 2: running sums of w = s / S, in sorted order, until top-p is reached.
+    const double S = sm.scaled_total;
+    const double top_p = P.top_p;
+    if (threadIdx.x == 0) {
+      sm.run = 0.0;
+      sm.cut = -1;
+    }
+    int stop = H;  // running sums exist for [0, stop)
+    for (int pos = 0; pos < H; pos += kHeadBatch) {
+      const int b = min(kHeadBatch, H - pos);
+      __syncthreads();
+      for (int i = threadIdx.x; i < b; i += kBlock) sm.vals[i] = sg[pos + i] / S;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        double c = sm.run;
+        for (int i = 0; i < b; ++i) {
+          c += sm.vals[i];
+          cg[pos + i] = c;
+          if (top_p < 1.0 && c >= top_p) {
+            sm.cut = pos + i + 1;
+            break;
+          }
+        }
+        sm.run = c;
+      }
+      __syncthreads();
+      if (sm.cut >= 0) {
+        stop = sm.cut;
+        break;
+      }
+    }
+    const int cut = sm.cut >= 0 ? sm.cut : V;  // no cut: the whole vocabulary is considered
+    const double target = P.uniform * sm.run;   // the running sum at the cut: the total
+    // First i < stop with target < running_i (running sums are non-decreasing).
+    int lo = 0, hi = stop - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (target < cg[mid]) hi = mid; else lo = mid + 1;
+    }
+    chosen = lo;
+    res.considered = (uint32_t)cut;
+    res.pool_exhausted = (top_p < 1.0 && pool_mass < top_p) ? 1 : 0;
+  }
+  const uint64_t cv = sorted[chosen];
+  res.id = (int32_t)composite_index(cv);
+  res.probability = fdlibm_exp((double)value_of(composite_key(cv)) - (double)M) / S1;
+  if (threadIdx.x == 0) L.results[row] = res;
+  if (L.topk_cap > 0) {
+    const int m = min(H, L.topk_cap);
+    for (int i = threadIdx.x; i < m; i += kBlock) {
+      const uint32_t idx = composite_index(sorted[i]);
+      L.topk_ids[(size_t)row * L.topk_cap + i] = (int32_t)idx;
+      L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(V - 1)));
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1181,13 +1446,24 @@ hipError_t launch_pair(const Launch &L, const Workspace &W, hipStream_t stream) 
   return hipGetLastError();
 }
 
+template <typename In, int VEC>
+hipError_t launch_head(const Launch &L, const Workspace &W, hipStream_t stream) {
+  hipLaunchKernelGGL((head_kernel<In, VEC>), dim3((unsigned)(L.rows * L.h_splits)), dim3(kWaveSize), 0,
+                     stream, L, W);
+  hipLaunchKernelGGL((head_finish_kernel<In>), dim3((unsigned)L.rows), dim3(kBlock), 0, stream, L, W);
+  return hipGetLastError();
+}
+
 hipError_t dispatch(int dtype, const Plan &p, const Launch &L, const Workspace &W, hipStream_t s) {
+  hipError_t e;
   if (dtype == TABBY_F32) {
-    if (p.vec == 4) return launch_pair<float, 4>(L, W, s);
-    return launch_pair<float, 1>(L, W, s);
+    e = p.vec == 4 ? launch_pair<float, 4>(L, W, s) : launch_pair<float, 1>(L, W, s);
+    if (e == hipSuccess && L.head_pass) e = p.vec == 4 ? launch_head<float, 4>(L, W, s) : launch_head<float, 1>(L, W, s);
+    return e;
   }
-  if (p.vec == 8) return launch_pair<uint16_t, 8>(L, W, s);
-  return launch_pair<uint16_t, 1>(L, W, s);
+  e = p.vec == 8 ? launch_pair<uint16_t, 8>(L, W, s) : launch_pair<uint16_t, 1>(L, W, s);
+  if (e == hipSuccess && L.head_pass) e = p.vec == 8 ? launch_head<uint16_t, 8>(L, W, s) : launch_head<uint16_t, 1>(L, W, s);
+  return e;
 }
 
 int check_common(tabby_sampler *h, const void *logits, int32_t dtype, int32_t rows, int32_t vocab,
@@ -1295,8 +1571,31 @@ int tabby_sampler_sample_device(tabby_sampler *h, const void *logits_dev, int32_
   if (!params_dev || !results_dev) return fail(TABBY_EINVAL, "params and results pointers must be non-null");
   if (topk_cap > 0 && (!topk_ids_dev || !topk_logits_dev))
     return fail(TABBY_EINVAL, "topk_cap > 0 needs both top-k output pointers");
-  if (flags & TABBY_FLAG_FULL_VOCAB)
-    return fail(TABBY_ECAPACITY, "whole-vocabulary pools (top_k = 0) are not available in this build");
+  if ((flags & TABBY_FLAG_FULL_VOCAB) && topk_cap > h->k_max)
+    return fail(TABBY_EINVAL, "topk_cap must be <= k_max (" + std::to_string(h->k_max) +
+                                  ") when whole-vocabulary rows are sampled, got " + std::to_string(topk_cap));
+  if (flags & TABBY_FLAG_FULL_VOCAB) {
+    // Head buffers for whole-vocabulary rows: four arrays of vocab_max 8-byte entries per
+    // row, allocated on first use and grown to the largest batch seen.
+    if ((size_t)rows > h->head_rows_cap) {
+      HIP_TRY(hipSetDevice(h->device));
+      if (h->head_base) {
+        HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+        HIP_TRY(hipFree(h->head_base));
+        h->head_base = nullptr;
+        h->head_rows_cap = 0;
+      }
+      const size_t per = (size_t)rows * (size_t)h->vocab_max;
+      HIP_TRY(hipMalloc(&h->head_base, per * 32));
+      char *b = (char *)h->head_base;
+      h->ws.head = (uint64_t *)b;
+      h->ws.head_sorted = (uint64_t *)(b + per * 8);
+      h->ws.head_s = (double *)(b + per * 16);
+      h->ws.head_c = (double *)(b + per * 24);
+      h->ws.head_stride = h->vocab_max;
+      h->head_rows_cap = (size_t)rows;
+    }
+  }
 
   const int kcap = h->k_max <= kKcapSmall ? kKcapSmall : kKcapLarge;
   const Plan p = make_plan(rows, vocab, dtype, logits_dev, kcap <= kWaveKcap);
@@ -1313,7 +1612,10 @@ int tabby_sampler_sample_device(tabby_sampler *h, const void *logits_dev, int32_
   L.topk_cap = topk_cap;
   L.k_max = h->k_max;
   L.kcap = kcap;
-  L.head_pass = 0;
+  L.head_pass = (flags & TABBY_FLAG_FULL_VOCAB) ? 1 : 0;
+  const Plan hp = make_plan(rows, vocab, dtype, logits_dev, true);
+  L.h_splits = hp.splits;
+  L.h_slice_len = hp.slice_len;
   HIP_TRY(hipSetDevice(h->device));
   HIP_TRY(dispatch(dtype, p, L, h->ws, (hipStream_t)stream));
   return TABBY_OK;

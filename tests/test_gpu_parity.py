@@ -158,3 +158,52 @@ def test_module_level_sample_matches_oracle(oracle):
     u = S.SeededRandom(42).next()
     o = oracle.sample_row(w.logits[0], 40, 0.7, 0.9, u)
     assert out.id == o["id"] and out.consideredCount == o["considered"]
+
+
+# ---- whole-vocabulary pools (top_k = 0): the head path -----------------------------------
+
+def test_config4_f16_full_vocab_top_p(oracle):
+    w = synth.config(4)
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=64)
+    _log("config4", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
+@pytest.mark.parametrize("temperature", [0.0, 0.3, 1.0])
+def test_full_vocab_temperatures(oracle, temperature):
+    w = synth.config(4, rows=8)
+    w.temperature[:] = temperature
+    w.top_p[:] = np.array([0.5, 0.9, 0.95, 0.99, 1.0, 0.95, 0.8, 1.0])
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=64)
+    _log(f"full vocab T={temperature}", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
+def test_full_vocab_flat_row_takes_batched_head(oracle):
+    # A hot temperature puts every element in the head: H = V, several sort batches.
+    w = synth.random_workload(rows=2, vocab=20000, seed=31, k_choices=(0,), temperatures=(50.0,),
+                              top_ps=(0.9, 1.0), sigma=1.0)
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=64)
+    compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64)
+
+
+def test_full_vocab_all_equal_and_ties(oracle):
+    w = synth.random_workload(rows=3, vocab=9000, seed=41, k_choices=(0,), temperatures=(0.7,),
+                              top_ps=(0.9,), ties=True, neg_inf_frac=0.3)
+    w.logits[0] = 2.0
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=64)
+    compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64)
+
+
+def test_full_vocab_mixed_with_finite_rows(oracle):
+    w = synth.config(3, rows=12, vocab=30000)
+    w.top_k[::3] = 0
+    res, ids, vals = run_gpu(w, k_max=128, topk_cap=100)
+    compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100)
+
+
+def test_full_vocab_rejects_list_above_k_max():
+    import torch
+    x = torch.zeros(1, 5000, device="cuda")
+    with S.GpuSampler(vocab_max=5000, rows_max=1, k_max=64) as g:
+        p = S.make_params(S.SamplingParams(0.7, 0, 0.9), 1, 0.5)
+        with pytest.raises(S.SamplingError, match="topk_cap"):
+            g.sample_params(x, p, topk_cap=65)
