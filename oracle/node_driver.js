@@ -9,7 +9,7 @@
  *                                                   worker_threads when spec.threads > 1)
  *
  * SPEC.json: {logits: path (f32, row-major), rows, vocab, topK[], temperature[], topP[],
- *             uniform[], out: path (JSON outcomes), threads, seconds}
+ *             uniform[], out: path (JSON outcomes), topkCap, threads, seconds}
  */
 const fs = require('fs');
 const os = require('os');
@@ -41,7 +41,7 @@ function runRows(spec, rows, first, count) {
   const out = [];
   for (let i = 0; i < count; i++) {
     const r = (first + i) % spec.rows;
-    out.push(oracle.sampleRow(rows[r], paramsOf(spec, r), spec.uniform[r]));
+    out.push(oracle.sampleRow(rows[r], paramsOf(spec, r), spec.uniform[r], spec.topkCap || 0));
   }
   return out;
 }

@@ -7,6 +7,7 @@ The reference functions each one follows are listed in ``tabby_oracle.h``.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import json
 import os
@@ -51,34 +52,52 @@ def build() -> None:
 _lib = None
 
 
+def load(path: str) -> ctypes.CDLL:
+    """Loads a build of tabby_oracle.c at `path` with its ctypes signatures."""
+    L = ctypes.CDLL(path)
+    P = ctypes.POINTER
+    L.tabby_oracle_mulberry32_fill.argtypes = [ctypes.c_uint32, P(ctypes.c_double), ctypes.c_int64]
+    L.tabby_oracle_exp.argtypes = [ctypes.c_double]
+    L.tabby_oracle_exp.restype = ctypes.c_double
+    L.tabby_oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.tabby_oracle_f16_to_f32.restype = ctypes.c_float
+    L.tabby_oracle_argmax.argtypes = [P(ctypes.c_float), ctypes.c_int32]
+    L.tabby_oracle_argmax.restype = ctypes.c_int32
+    L.tabby_oracle_topk.argtypes = [P(ctypes.c_float), ctypes.c_int32, ctypes.c_int32,
+                                    P(ctypes.c_int32), P(ctypes.c_float)]
+    L.tabby_oracle_topk.restype = ctypes.c_int32
+    L.tabby_oracle_sum_exp.argtypes = [P(ctypes.c_float), ctypes.c_int32, ctypes.c_float]
+    L.tabby_oracle_sum_exp.restype = ctypes.c_double
+    L.tabby_oracle_sample_from_topk.argtypes = [
+        P(ctypes.c_int32), P(ctypes.c_float), ctypes.c_int32, ctypes.c_double,
+        ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double, P(Outcome)]
+    L.tabby_oracle_sample_row.argtypes = [
+        P(ctypes.c_float), ctypes.c_int32, ctypes.c_int32, ctypes.c_double, ctypes.c_double,
+        ctypes.c_double, P(Outcome), P(ctypes.c_int32), P(ctypes.c_float), ctypes.c_int32,
+        P(ctypes.c_float), P(ctypes.c_double)]
+    return L
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        L = ctypes.CDLL(LIB_PATH)
-        P = ctypes.POINTER
-        L.tabby_oracle_mulberry32_fill.argtypes = [ctypes.c_uint32, P(ctypes.c_double), ctypes.c_int64]
-        L.tabby_oracle_exp.argtypes = [ctypes.c_double]
-        L.tabby_oracle_exp.restype = ctypes.c_double
-        L.tabby_oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
-        L.tabby_oracle_f16_to_f32.restype = ctypes.c_float
-        L.tabby_oracle_argmax.argtypes = [P(ctypes.c_float), ctypes.c_int32]
-        L.tabby_oracle_argmax.restype = ctypes.c_int32
-        L.tabby_oracle_topk.argtypes = [P(ctypes.c_float), ctypes.c_int32, ctypes.c_int32,
-                                        P(ctypes.c_int32), P(ctypes.c_float)]
-        L.tabby_oracle_topk.restype = ctypes.c_int32
-        L.tabby_oracle_sum_exp.argtypes = [P(ctypes.c_float), ctypes.c_int32, ctypes.c_float]
-        L.tabby_oracle_sum_exp.restype = ctypes.c_double
-        L.tabby_oracle_sample_from_topk.argtypes = [
-            P(ctypes.c_int32), P(ctypes.c_float), ctypes.c_int32, ctypes.c_double,
-            ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double, P(Outcome)]
-        L.tabby_oracle_sample_row.argtypes = [
-            P(ctypes.c_float), ctypes.c_int32, ctypes.c_int32, ctypes.c_double, ctypes.c_double,
-            ctypes.c_double, P(Outcome), P(ctypes.c_int32), P(ctypes.c_float), ctypes.c_int32,
-            P(ctypes.c_float), P(ctypes.c_double)]
-        _lib = L
+        _lib = load(LIB_PATH)
     return _lib
+
+
+@contextlib.contextmanager
+def using(library: ctypes.CDLL):
+    """Routes every function of this module through `library` (a build from `load`) for
+    the duration; the tests use it to run their pins against deliberately broken builds."""
+    global _lib
+    saved = lib()
+    _lib = library
+    try:
+        yield
+    finally:
+        _lib = saved
 
 
 def _ptr(a: np.ndarray, ctype):
@@ -218,9 +237,9 @@ def _write_spec(d, logits, top_k, temperature, top_p, uniform, **extra):
     return sp, spec
 
 
-def node_sample_batch(logits, top_k, temperature, top_p, uniform) -> list:
+def node_sample_batch(logits, top_k, temperature, top_p, uniform, topk_cap: int = 0) -> list:
     with tempfile.TemporaryDirectory() as d:
-        sp, spec = _write_spec(d, logits, top_k, temperature, top_p, uniform)
+        sp, spec = _write_spec(d, logits, top_k, temperature, top_p, uniform, topkCap=int(topk_cap))
         subprocess.run(["node", NODE_DRIVER, "sample", sp], check=True)
         with open(spec["out"]) as f:
             return json.load(f)

@@ -112,8 +112,9 @@ function sampleFromTopK(top, params, uniformSource) {
   };
 }
 
-// One row end to end. `row` is a Float32Array; `uniform` a number in [0,1).
-function sampleRow(row, params, uniform) {
+// One row end to end. `row` is a Float32Array; `uniform` a number in [0,1). With
+// topkCap > 0 the outcome also carries the first topkCap ids of the sorted pool.
+function sampleRow(row, params, uniform, topkCap) {
   const k = params.topK <= 0 || params.topK >= row.length ? row.length : params.topK;
   const cands = topK(row, k);
   const maxLogit = cands[0].value;
@@ -126,6 +127,7 @@ function sampleRow(row, params, uniform) {
   const outcome = sampleFromTopK(top, params, uniform);
   outcome.maxLogit = maxLogit;
   outcome.sumExp = top.sumExp;
+  if (topkCap > 0) outcome.topIds = top.ids.slice(0, topkCap);
   return outcome;
 }
 

@@ -4,13 +4,17 @@
  * Parity status of each function (what pins it, beyond this file):
  *   mulberry32      closed form; checked against the Node restatement (V8 integer semantics)
  *                   on >= 1e6 outputs per seed in tests/test_oracle.py
- *   exp             checked bit-for-bit against V8's Math.exp on ~2e6 arguments
- *   argmax / topk   brute force over every permutation of tie-heavy tiny rows, library sort
- *                   (numpy lexsort) on large rows, special cases (all equal, -inf, +-0)
- *   sum_exp         definition (sequential f64 sum), checked against math.fsum bounds
+ *   exp             bit-for-bit against V8's Math.exp: 6,000 committed vectors and 1e6 live
+ *                   arguments; within 1 ulp of glibc's exp
+ *   argmax / topk   brute force over every tie-heavy tiny row (values -inf, -1, -0, 0, .5, 1;
+ *                   lengths 1-5), numpy's stable argsort on large rows, special cases (all
+ *                   equal, all -inf, +-0)
+ *   sum_exp         definition (sequential f64 sum), checked against math.fsum
  *   sample_from_topk  closed forms on the reference's hand fixture
- *                   (tests/sampling.test.ts:206-250), inverse-CDF brute force over a u grid,
- *                   and cross-checked against the Node restatement on random rows
+ *                   (tests/sampling.test.ts:206-250), inverse-CDF counting over a u grid,
+ *                   shift invariance, and the Node restatement on committed and live rows
+ * tests/test_oracle_mutants.py builds broken copies of this file (a flipped comparison, a
+ * dropped term, a wrong constant) and requires these pins to reject every one.
  * Built with -ffp-contract=off: every f64 operation below must round exactly once, in the
  * order written, as V8 evaluates the reference's JavaScript.
  */

@@ -1,0 +1,177 @@
+"""Writes the committed golden vectors under tests/golden/ (run from the repo root:
+``python tests/golden/make_golden.py``). Needs ``node`` (the image's Node 12).
+
+The reference sampler is TypeScript and cannot run here (no TS toolchain, and its
+`generateGreedy` uses syntax Node 12 rejects), and the reference commits no logits or
+sampling vectors. So the expected values come from two sources:
+
+* ``sampling_fixture.json`` -- the reference's own CPU fixture (tests/sampling.test.ts:206-250:
+  a four-candidate TopKResult and its assertions), with each outcome's values worked out in
+  closed form below (exp of integers, the cumulative weights, the cut), not by any oracle.
+* ``node_vectors.json`` -- outputs of the Node restatement (oracle/sampler_oracle.js), which
+  runs V8's own Math.exp and Array.prototype.sort comparator the reference runs on: mulberry32
+  streams, Math.exp over assorted arguments, and sampled outcomes (+ sorted pool ids) of
+  small workloads. Their logits are integer-derived from mulberry32 draws (`golden_logits`),
+  exactly representable in f32 and reproducible without libm; a SHA-256 of each workload's
+  bytes is stored so a test can prove it regenerated the same inputs.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import math
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+from tabby_amd.synth import mulberry32_stream  # noqa: E402
+
+MULBERRY_SEEDS = (0, 1, 7, 42, 12345, 0xDEADBEEF, 0xFFFFFFFF)
+TOPK_CAP = 16
+
+# name -> (rows, vocab, seed, kind, top_k choices, temperatures, top_ps)
+WORKLOADS = {
+    "fine": (8, 4096, 101, "fine", (1, 5, 40, 64, 0), (0.0, 0.5, 1.0, 2.0), (0.5, 0.9, 1.0)),
+    "ties_neg_inf": (8, 1000, 202, "coarse_neg_inf", (0, 7, 64, 1024), (0.7, 1.0), (0.9, 0.98, 1.0)),
+    "whole_vocab": (4, 3000, 303, "fine", (0,), (0.3, 1.0), (0.95,)),
+    "special": (6, 512, 404, "special", (1, 40, 0), (0.0, 0.7, 1.0), (0.9, 1.0)),
+}
+
+
+def golden_logits(rows: int, vocab: int, seed: int, kind: str) -> np.ndarray:
+    """Integer-derived f32 logits (every value exact in f32; no transcendental functions).
+
+    fine:            top 24 bits of a mulberry32 draw, scaled to [-16, 16) in steps of 2^-19
+    coarse_neg_inf:  multiples of 0.25 in [-8, 8) (heavy ties), 30 % -inf, -0 canonicalised
+    special:         rows chosen to hit edge cases: all equal; +0/-0 mixes; one finite value
+                     among -inf; a max shared by many ids; two spikes; a ramp
+    """
+    out = np.empty((rows, vocab), dtype=np.float32)
+    for r in range(rows):
+        u = mulberry32_stream((seed * 7919 + r * 104729) & 0xFFFFFFFF, vocab)
+        bits = (u * 4294967296.0).astype(np.uint64)
+        if kind == "fine":
+            out[r] = ((bits >> np.uint64(8)).astype(np.float64) - 8388608.0) / 524288.0
+        elif kind == "coarse_neg_inf":
+            q = ((bits >> np.uint64(26)).astype(np.float64) - 32.0) * 0.25
+            q[q == 0.0] = 0.0
+            mask = mulberry32_stream((seed * 31 + r) & 0xFFFFFFFF, vocab) < 0.3
+            q[mask] = -np.inf
+            out[r] = q
+        elif kind == "special":
+            case = r % 6
+            if case == 0:
+                out[r] = 1.5
+            elif case == 1:
+                out[r] = np.where(bits % np.uint64(3) == 0, 0.0, -0.0)
+                out[r, 5] = -1.0
+            elif case == 2:
+                out[r] = -np.inf
+                out[r, vocab // 3] = -2.0
+            elif case == 3:
+                out[r] = ((bits >> np.uint64(28)).astype(np.float64)) * 0.5
+            elif case == 4:
+                out[r] = -3.0
+                out[r, 17] = 4.0
+                out[r, 300] = 4.0 - 2.0 ** -20
+            else:
+                out[r] = np.arange(vocab, dtype=np.float64)[::-1] / 64.0
+        else:
+            raise ValueError(kind)
+    return out
+
+
+def golden_params(rows: int, seed: int, ks, ts, ps):
+    pick = mulberry32_stream((seed * 65537 + 11) & 0xFFFFFFFF, 4 * rows).reshape(rows, 4)
+    k = np.asarray(ks, np.int32)[(pick[:, 0] * len(ks)).astype(int)]
+    t = np.asarray(ts, np.float64)[(pick[:, 1] * len(ts)).astype(int)]
+    p = np.asarray(ps, np.float64)[(pick[:, 2] * len(ps)).astype(int)]
+    return k, t, p, pick[:, 3].copy()
+
+
+def workload(name: str):
+    rows, vocab, seed, kind, ks, ts, ps = WORKLOADS[name]
+    logits = golden_logits(rows, vocab, seed, kind)
+    k, t, p, u = golden_params(rows, seed, ks, ts, ps)
+    return logits, k, t, p, u
+
+
+def exp_arguments() -> np.ndarray:
+    u = mulberry32_stream(0xE4F, 6000)
+    ln2 = math.log(2.0)
+    parts = [
+        -60.0 + 61.0 * u[:2000],             # the sampler's range: (l - m)/T and l - m
+        -745.5 + 1455.5 * u[2000:3000],       # the whole finite range, incl. under/overflow
+        (u[3000:3500] - 0.5) * 2.0 ** -26,    # |x| < 2^-27: the 1 + x branch
+        (u[3500:4000] - 0.5) * ln2,           # |x| < ln2/2: no reduction
+        np.round((u[4000:4500] - 0.5) * 200) * ln2 / 2 + (u[4500:5000] - 0.5) * 1e-9,  # k*ln2/2
+        np.array([0.0, -0.0, 1.0, -1.0, 0.5, -0.5, 709.782712893384, 709.79, -708.39641853226408,
+                  -745.13321910194111, -745.14, -37.0, -40.0, 2.0 ** -28, -(2.0 ** -28)]),
+    ]
+    return np.concatenate(parts)
+
+
+def closed_form_fixture() -> dict:
+    """tests/sampling.test.ts:206-250 with every expected value derived by hand."""
+    e = [math.exp(-i) for i in range(4)]  # exp(l - maxLogit) for l = 10, 9, 8, 7
+    s1 = sum(e)                            # 1 + e^-1 + e^-2 + e^-3
+    w = [v / s1 for v in e]                # weights at T = 1
+    c = list(np.cumsum(w))
+
+    def first_reaching(p):
+        return next(i for i, ci in enumerate(c) if ci >= p) + 1
+
+    return {
+        "source": "reference tests/sampling.test.ts:206-250",
+        "top": {"maxLogit": 10.0, "sumExp": 2.5, "ids": [1, 2, 3, 4], "logits": [10.0, 9.0, 8.0, 7.0]},
+        "cases": [
+            {"name": "argmax at temperature 0", "temperature": 0.0, "topP": 1.0, "sumExp": 2.5,
+             "expect": {"id": 1, "consideredCount": 1, "probability": 1.0 / 2.5,
+                        "poolMass": s1 / 2.5, "poolExhausted": False}},
+            {"name": "wide (topP 1)", "temperature": 1.0, "topP": 1.0, "sumExp": 2.5,
+             "expect": {"consideredCount": 4, "poolMass": s1 / 2.5, "poolExhausted": False}},
+            {"name": "narrow (topP 0.5)", "temperature": 1.0, "topP": 0.5, "sumExp": 2.5,
+             "expect": {"consideredCount": first_reaching(0.5), "id": 1,
+                        "poolMass": s1 / 2.5, "poolExhausted": False}},
+            {"name": "clipped by k (sumExp 100)", "temperature": 1.0, "topP": 0.9, "sumExp": 100.0,
+             "expect": {"poolMass": s1 / 100.0, "poolExhausted": True,
+                        "consideredCount": first_reaching(0.9)}},
+        ],
+        "weights_T1": w,
+        "spread": {"temperature": 2.0, "topP": 1.0, "seed": 12345, "draws": 200, "min_distinct": 2},
+    }
+
+
+def main() -> None:
+    import oracle as o
+
+    if not o.node_available():
+        raise SystemExit("node is required to write the golden vectors")
+    vec = {"mulberry32": {}, "exp": {}, "workloads": {}, "topk_cap": TOPK_CAP}
+    for seed in MULBERRY_SEEDS:
+        vec["mulberry32"][str(seed)] = [float(v) for v in o.node_mulberry32(seed, 64)]
+    x = exp_arguments()
+    y = o.node_exp(x)
+    vec["exp"] = {"x": [float(v) for v in x], "y": [float(v) for v in y]}
+    for name in WORKLOADS:
+        logits, k, t, p, u = workload(name)
+        outs = o.node_sample_batch(logits, k, t, p, u, topk_cap=TOPK_CAP)
+        vec["workloads"][name] = {
+            "sha256": hashlib.sha256(logits.tobytes()).hexdigest(),
+            "outcomes": outs,
+        }
+    with open(os.path.join(HERE, "node_vectors.json"), "w") as f:
+        json.dump(vec, f, separators=(",", ":"))
+    with open(os.path.join(HERE, "sampling_fixture.json"), "w") as f:
+        json.dump(closed_form_fixture(), f, indent=1)
+    print("wrote", os.listdir(HERE))
+
+
+if __name__ == "__main__":
+    main()
