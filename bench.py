@@ -38,7 +38,25 @@ def parse_args():
     ap.add_argument("--dtype", choices=["f32", "f16"], default="f32")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of known size (reference for the "
+                         "FETCH_SIZE / WRITE_SIZE counters) and print its JSON line")
     return ap.parse_args()
+
+
+def copy_calibration() -> int:
+    """A plain copy of 256 MiB, 10 times: each launch reads and writes exactly 256 MiB, so
+    the counters' KiB per dispatch over 262,144 KiB is their scale factor."""
+    import torch
+    n = 64 * 1024 * 1024  # f32 elements: 256 MiB
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_kib_read_per_launch": n * 4 // 1024,
+                      "copy_kib_written_per_launch": n * 4 // 1024, "launches": 10}), flush=True)
+    return 0
 
 
 def cpu_baseline(w, seconds: float) -> dict | None:
@@ -72,6 +90,8 @@ def cpu_baseline(w, seconds: float) -> dict | None:
 
 def main() -> int:
     args = parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the sampler is "
               f"single-device in this build; rows shard across GPUs with no communication.",
@@ -185,8 +205,10 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": "tabby::sample_kernel",
+            "kernel": ("one tabby_sampler_sample_device call = wave_kernel (streaming: max, "
+                       "sum-exp, candidates) + merge_kernel (exact top-k, top-p, draw)"),
             "bytes_per_launch": bytes_per_launch,
+            "duration_us": round(avg_ms * 1000, 2),
         },
         "cpu_baseline": cpu,
     }

@@ -122,7 +122,7 @@ __device__ __forceinline__ int digit_shift(int pass) {
 }
 
 template <class ForEach>
-__device__ SelectResult radix_select(ForEach for_each, uint32_t need, uint32_t *hist,
+__device__ __forceinline__ SelectResult radix_select(ForEach for_each, uint32_t need, uint32_t *hist,
                                      BlockScratch &s) {
   uint64_t prefix = 0;
   int done = 64;
