@@ -23,6 +23,7 @@ LIB_PATH = os.path.join(LIB_DIR, "libtabby_sampler.so")
 NODE_DIR = os.path.join(PKG, "node")
 NODE_ADDON = os.path.join(NODE_DIR, "build", "tabby_sampler.node")
 NODE_INCLUDE = "/usr/include/node"
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = os.environ.get("TABBY_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -67,8 +68,11 @@ def build_node_addon(verbose: bool = False) -> str | None:
     tmp = NODE_ADDON + ".tmp"
     cmd = [
         shutil.which("g++") or "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
-        f"-I{NODE_INCLUDE}", f"-I{INCLUDE}", "-o", tmp, os.path.join(NODE_DIR, "addon.cc"),
-        f"-L{LIB_DIR}", "-ltabby_sampler", "-Wl,-rpath,$ORIGIN/../../lib",
+        "-DNODE_GYP_MODULE_NAME=tabby_sampler", "-D__HIP_PLATFORM_AMD__",
+        f"-I{NODE_INCLUDE}", f"-I{INCLUDE}", f"-I{ROCM}/include", "-o", tmp,
+        os.path.join(NODE_DIR, "addon.cc"),
+        f"-L{LIB_DIR}", "-ltabby_sampler", f"-L{ROCM}/lib", "-lamdhip64",
+        "-Wl,-rpath,$ORIGIN/../../lib", f"-Wl,-rpath,{ROCM}/lib",
     ]
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -1,0 +1,246 @@
+// N-API addon: the Node side of the sampler's C ABI (include/tabby_sampler.h).
+//
+// It stays thin on purpose. Argument checking, the reference's error messages, the RNG
+// and the SampleOutcome objects live in index.js; this file only moves bytes:
+//   create / destroy             tabby_sampler_create / _destroy (ForwardPass scratch,
+//                                src/engine/forward.ts:243-248, 309-315)
+//   deviceAlloc / deviceFree /   device buffers for logits that the host holds (the
+//   upload                       reference's logits are already on its GPU; here a caller
+//                                without a HIP producer uploads them once)
+//   sample                       tabby_sampler_sample: params packed by index.js as
+//                                tabby_row_params, results returned as tabby_row_result bytes
+//                                (encodeSampling + readback, forward.ts:442-451, 522-601)
+//   version
+#define NAPI_VERSION 6
+#include <node_api.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "tabby_sampler.h"
+
+namespace {
+
+struct Handle {
+  tabby_sampler *sampler = nullptr;
+};
+
+struct DeviceBuffer {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  int device = 0;
+};
+
+napi_value fail(napi_env env, const std::string &msg) {
+  napi_throw_error(env, nullptr, msg.c_str());
+  return nullptr;
+}
+
+#define CHECK_NAPI(env, call)                                        \
+  do {                                                               \
+    if ((call) != napi_ok) return fail((env), "N-API call failed: " #call); \
+  } while (0)
+
+bool get_args(napi_env env, napi_callback_info info, size_t want, napi_value *argv) {
+  size_t argc = want;
+  if (napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr) != napi_ok) return false;
+  return argc == want;
+}
+
+bool get_i64(napi_env env, napi_value v, int64_t *out) {
+  return napi_get_value_int64(env, v, out) == napi_ok;
+}
+
+void finalize_handle(napi_env, void *data, void *) {
+  Handle *h = static_cast<Handle *>(data);
+  if (h->sampler) tabby_sampler_destroy(h->sampler);
+  delete h;
+}
+
+void finalize_buffer(napi_env, void *data, void *) {
+  DeviceBuffer *b = static_cast<DeviceBuffer *>(data);
+  if (b->ptr) {
+    (void)hipSetDevice(b->device);
+    (void)hipFree(b->ptr);
+  }
+  delete b;
+}
+
+template <typename T>
+T *unwrap_external(napi_env env, napi_value v) {
+  void *p = nullptr;
+  if (napi_get_value_external(env, v, &p) != napi_ok) return nullptr;
+  return static_cast<T *>(p);
+}
+
+// create(device, vocabMax, rowsMax, kMax) -> external
+napi_value Create(napi_env env, napi_callback_info info) {
+  napi_value argv[4];
+  if (!get_args(env, info, 4, argv)) return fail(env, "create(device, vocabMax, rowsMax, kMax)");
+  int64_t a[4];
+  for (int i = 0; i < 4; ++i)
+    if (!get_i64(env, argv[i], &a[i])) return fail(env, "create: integer arguments expected");
+  tabby_sampler *s = nullptr;
+  const int rc = tabby_sampler_create((int)a[0], (int32_t)a[1], (int32_t)a[2], (int32_t)a[3], &s);
+  if (rc) return fail(env, tabby_last_error());
+  Handle *h = new Handle{s};
+  napi_value out;
+  CHECK_NAPI(env, napi_create_external(env, h, finalize_handle, nullptr, &out));
+  return out;
+}
+
+// destroy(handle): frees the scratch now rather than at garbage collection.
+napi_value Destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return fail(env, "destroy(handle)");
+  Handle *h = unwrap_external<Handle>(env, argv[0]);
+  if (!h) return fail(env, "destroy: not a sampler handle");
+  if (h->sampler) tabby_sampler_destroy(h->sampler);
+  h->sampler = nullptr;
+  return nullptr;
+}
+
+// deviceAlloc(device, bytes) -> external
+napi_value DeviceAlloc(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return fail(env, "deviceAlloc(device, bytes)");
+  int64_t device, bytes;
+  if (!get_i64(env, argv[0], &device) || !get_i64(env, argv[1], &bytes) || bytes <= 0)
+    return fail(env, "deviceAlloc: device and a positive byte count expected");
+  if (hipSetDevice((int)device) != hipSuccess) return fail(env, "deviceAlloc: hipSetDevice failed");
+  DeviceBuffer *b = new DeviceBuffer{nullptr, (size_t)bytes, (int)device};
+  if (hipMalloc(&b->ptr, b->bytes) != hipSuccess) {
+    delete b;
+    return fail(env, "deviceAlloc: hipMalloc of " + std::to_string(bytes) + " bytes failed");
+  }
+  napi_value out;
+  CHECK_NAPI(env, napi_create_external(env, b, finalize_buffer, nullptr, &out));
+  return out;
+}
+
+napi_value DeviceFree(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return fail(env, "deviceFree(buffer)");
+  DeviceBuffer *b = unwrap_external<DeviceBuffer>(env, argv[0]);
+  if (!b) return fail(env, "deviceFree: not a device buffer");
+  if (b->ptr) {
+    (void)hipSetDevice(b->device);
+    (void)hipFree(b->ptr);
+  }
+  b->ptr = nullptr;
+  b->bytes = 0;
+  return nullptr;
+}
+
+// upload(buffer, typedArray): synchronous host -> device copy of the array's bytes.
+napi_value Upload(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return fail(env, "upload(buffer, typedArray)");
+  DeviceBuffer *b = unwrap_external<DeviceBuffer>(env, argv[0]);
+  if (!b || !b->ptr) return fail(env, "upload: not a live device buffer");
+  napi_typedarray_type type;
+  size_t length;
+  void *data;
+  napi_value ab;
+  size_t offset;
+  if (napi_get_typedarray_info(env, argv[1], &type, &length, &data, &ab, &offset) != napi_ok)
+    return fail(env, "upload: a typed array is expected");
+  size_t elem = 0;
+  switch (type) {
+    case napi_float32_array: elem = 4; break;
+    case napi_uint16_array: elem = 2; break;
+    default: return fail(env, "upload: Float32Array (f32) or Uint16Array (f16 bits) expected");
+  }
+  const size_t bytes = length * elem;
+  if (bytes > b->bytes) return fail(env, "upload: the array is larger than the device buffer");
+  (void)hipSetDevice(b->device);
+  if (hipMemcpy(b->ptr, data, bytes, hipMemcpyHostToDevice) != hipSuccess)
+    return fail(env, "upload: hipMemcpy failed");
+  return nullptr;
+}
+
+// sample(handle, buffer, dtype, rows, vocab, paramsBytes, topkCap)
+//   -> { results: ArrayBuffer(rows*48), topkIds: Int32Array|null, topkLogits: Float32Array|null }
+napi_value Sample(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  if (!get_args(env, info, 7, argv))
+    return fail(env, "sample(handle, buffer, dtype, rows, vocab, params, topkCap)");
+  Handle *h = unwrap_external<Handle>(env, argv[0]);
+  if (!h || !h->sampler) return fail(env, "sample: the sampler was destroyed");
+  DeviceBuffer *b = unwrap_external<DeviceBuffer>(env, argv[1]);
+  if (!b || !b->ptr) return fail(env, "sample: not a live device buffer");
+  int64_t dtype, rows, vocab, cap;
+  if (!get_i64(env, argv[2], &dtype) || !get_i64(env, argv[3], &rows) ||
+      !get_i64(env, argv[4], &vocab) || !get_i64(env, argv[6], &cap))
+    return fail(env, "sample: integer dtype, rows, vocab and topkCap expected");
+  if (rows <= 0 || vocab <= 0 || cap < 0) return fail(env, "sample: rows and vocab must be positive");
+  const size_t elem = dtype == TABBY_F16 ? 2 : 4;
+  if ((size_t)rows * (size_t)vocab * elem > b->bytes)
+    return fail(env, "sample: rows x vocab exceeds the device buffer");
+  void *pdata;
+  size_t plen;
+  if (napi_get_arraybuffer_info(env, argv[5], &pdata, &plen) != napi_ok ||
+      plen != (size_t)rows * sizeof(tabby_row_params))
+    return fail(env, "sample: params must be an ArrayBuffer of rows x 32 bytes");
+
+  napi_value results_ab, ids_ab = nullptr, logits_ab = nullptr;
+  void *res_ptr, *ids_ptr = nullptr, *logits_ptr = nullptr;
+  CHECK_NAPI(env, napi_create_arraybuffer(env, (size_t)rows * sizeof(tabby_row_result), &res_ptr, &results_ab));
+  if (cap > 0) {
+    CHECK_NAPI(env, napi_create_arraybuffer(env, (size_t)rows * cap * 4, &ids_ptr, &ids_ab));
+    CHECK_NAPI(env, napi_create_arraybuffer(env, (size_t)rows * cap * 4, &logits_ptr, &logits_ab));
+  }
+  const int rc = tabby_sampler_sample(h->sampler, b->ptr, (int32_t)dtype, (int32_t)rows,
+                                      (int32_t)vocab, static_cast<const tabby_row_params *>(pdata),
+                                      static_cast<tabby_row_result *>(res_ptr),
+                                      static_cast<int32_t *>(ids_ptr), static_cast<float *>(logits_ptr),
+                                      (int32_t)cap, nullptr);
+  if (rc) {
+    napi_value err, msg, code;
+    CHECK_NAPI(env, napi_create_string_utf8(env, tabby_last_error(), NAPI_AUTO_LENGTH, &msg));
+    CHECK_NAPI(env, napi_create_error(env, nullptr, msg, &err));
+    CHECK_NAPI(env, napi_create_int32(env, rc, &code));
+    CHECK_NAPI(env, napi_set_named_property(env, err, "status", code));
+    napi_throw(env, err);
+    return nullptr;
+  }
+  napi_value out, ids = nullptr, logits = nullptr, null_value;
+  CHECK_NAPI(env, napi_create_object(env, &out));
+  CHECK_NAPI(env, napi_get_null(env, &null_value));
+  CHECK_NAPI(env, napi_set_named_property(env, out, "results", results_ab));
+  if (cap > 0) {
+    CHECK_NAPI(env, napi_create_typedarray(env, napi_int32_array, (size_t)rows * cap, ids_ab, 0, &ids));
+    CHECK_NAPI(env, napi_create_typedarray(env, napi_float32_array, (size_t)rows * cap, logits_ab, 0, &logits));
+  }
+  CHECK_NAPI(env, napi_set_named_property(env, out, "topkIds", ids ? ids : null_value));
+  CHECK_NAPI(env, napi_set_named_property(env, out, "topkLogits", logits ? logits : null_value));
+  return out;
+}
+
+napi_value Version(napi_env env, napi_callback_info) {
+  napi_value out;
+  CHECK_NAPI(env, napi_create_string_utf8(env, tabby_version(), NAPI_AUTO_LENGTH, &out));
+  return out;
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+  const napi_property_descriptor props[] = {
+      {"create", nullptr, Create, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"destroy", nullptr, Destroy, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"deviceAlloc", nullptr, DeviceAlloc, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"deviceFree", nullptr, DeviceFree, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"upload", nullptr, Upload, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"sample", nullptr, Sample, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"version", nullptr, Version, nullptr, nullptr, nullptr, napi_default, nullptr},
+  };
+  if (napi_define_properties(env, exports, sizeof props / sizeof props[0], props) != napi_ok)
+    return nullptr;
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)
