@@ -6,18 +6,23 @@
 // (src/shaders/topk_partial.wgsl, topk_select.wgsl), orchestrated by encodeSampling
 // (src/engine/forward.ts:522-601); the f64 tail runs on the CPU (src/engine/sampler.ts:147-212).
 //
-// Here one launch samples a whole batch:
-//   * grid = rows x splits; each 256-lane workgroup owns one slice of one row and reads it
-//     from HBM exactly once, 16 bytes per lane per load, into registers;
-//   * from registers it computes the slice max, the slice sum of exp(x - max) (f32 terms,
-//     f64 accumulation), and the exact top-k of the slice by radix select on 64-bit
-//     (value key, ~index) composites -- the lower index wins ties, as in sampler.ts:28;
-//   * the last workgroup of a row to finish (an atomic arrival counter, reset by that same
-//     workgroup) merges the slices: max, sum-exp, a radix select over the slices'
-//     candidates, an LDS bitonic sort, and then sampleFromTopK's f64 tail in the reference's
-//     exact order of operations (sequential sums; V8's exp via the fdlibm method).
-// Rows whose pool is the whole vocabulary (top_k = 0) are finished by a second kernel that
-// re-reads the row's head (see head_kernel).
+// Here one call samples a whole batch with two kernels on the caller's stream:
+//   * wave_kernel (slice_kernel for pools above 256): grid = rows x splits; each wave
+//     (workgroup) owns one slice of one row and reads it from HBM exactly once with 16-byte
+//     nontemporal loads into registers. From registers it keeps the slice max, the slice sum
+//     of exp(x - max) (f32 terms, f64 accumulation), and a superset of the slice's top-k: every
+//     element at or above a bound that never exceeds the slice's k-th largest value, held in a
+//     wave-private LDS list (pruned by histogram when it fills) and written unsorted to the
+//     slice's candidate region. Waves of a row share the best bound any of them has proven.
+//   * merge_kernel: grid = rows; each 256-lane workgroup combines its row's slices: max,
+//     sum-exp (slice sums rescaled in f64, in slice order), an exact radix select over the
+//     64-bit (value key, ~index) composites -- the lower index wins ties, as in sampler.ts:28 --
+//     a sort, and sampleFromTopK's f64 tail in the reference's exact order of operations
+//     (sequential sums; V8's exp by the fdlibm method).
+// The kernel boundary orders the first kernel's writes before the second's reads; no
+// workgroup waits on another. Rows whose pool is the whole vocabulary (top_k = 0 beyond the
+// pool capacity) are finished by two more kernels that collect and sort the row's head
+// (see head_kernel).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -56,9 +61,7 @@ struct RowState {
 };
 
 struct Workspace {
-  uint32_t *arrivals;       // [rows_cap] arrival counters of the sampling kernel
   uint32_t *row_theta;      // [rows_cap] key of the row's shared candidate bound (see wave_kernel)
-  uint32_t *head_arrivals;  // [rows_cap] arrival counters of the head kernel
   uint32_t *head_count;     // [rows_cap] head sizes
   SliceStat *stats;         // [rows_cap * kMaxSplits]
   uint64_t *cands;          // [rows_cap * row_cand_stride]
@@ -1512,7 +1515,7 @@ int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_
     off += (bytes + 255) & ~(size_t)255;
     return at;
   };
-  const size_t o_arr = carve(rows * 4), o_harr = carve(rows * 4), o_hcnt = carve(rows * 4);
+  const size_t o_hcnt = carve(rows * 4);
   const size_t o_rth = carve(rows * 4);
   const size_t o_stats = carve(rows * kMaxSplits * sizeof(SliceStat));
   const size_t o_cands = carve(rows * (size_t)h->ws.row_cand_stride * 8);
@@ -1525,9 +1528,7 @@ int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_
     return hip_fail(e, "hipMalloc(workspace)");
   }
   char *b = (char *)h->ws_base;
-  h->ws.arrivals = (uint32_t *)(b + o_arr);
   h->ws.row_theta = (uint32_t *)(b + o_rth);
-  h->ws.head_arrivals = (uint32_t *)(b + o_harr);
   h->ws.head_count = (uint32_t *)(b + o_hcnt);
   h->ws.stats = (SliceStat *)(b + o_stats);
   h->ws.cands = (uint64_t *)(b + o_cands);

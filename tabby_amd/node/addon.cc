@@ -7,6 +7,7 @@
 //   deviceAlloc / deviceFree /   device buffers for logits that the host holds (the
 //   upload                       reference's logits are already on its GPU; here a caller
 //                                without a HIP producer uploads them once)
+//   wrapDevicePointer            logits a HIP producer in this process already wrote
 //   sample                       tabby_sampler_sample: params packed by index.js as
 //                                tabby_row_params, results returned as tabby_row_result bytes
 //                                (encodeSampling + readback, forward.ts:442-451, 522-601)
@@ -32,6 +33,7 @@ struct DeviceBuffer {
   void *ptr = nullptr;
   size_t bytes = 0;
   int device = 0;
+  bool owned = true;  // false for a caller's pointer (wrapDevicePointer): never freed here
 };
 
 napi_value fail(napi_env env, const std::string &msg) {
@@ -62,7 +64,7 @@ void finalize_handle(napi_env, void *data, void *) {
 
 void finalize_buffer(napi_env, void *data, void *) {
   DeviceBuffer *b = static_cast<DeviceBuffer *>(data);
-  if (b->ptr) {
+  if (b->ptr && b->owned) {
     (void)hipSetDevice(b->device);
     (void)hipFree(b->ptr);
   }
@@ -126,13 +128,32 @@ napi_value DeviceFree(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 1, argv)) return fail(env, "deviceFree(buffer)");
   DeviceBuffer *b = unwrap_external<DeviceBuffer>(env, argv[0]);
   if (!b) return fail(env, "deviceFree: not a device buffer");
-  if (b->ptr) {
+  if (b->ptr && b->owned) {
     (void)hipSetDevice(b->device);
     (void)hipFree(b->ptr);
   }
   b->ptr = nullptr;
   b->bytes = 0;
   return nullptr;
+}
+
+// wrapDevicePointer(device, address: BigInt, bytes) -> external over memory the caller owns
+// (e.g. logits a HIP forward pass wrote in this process); the addon never frees it.
+napi_value WrapDevicePointer(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return fail(env, "wrapDevicePointer(device, address, bytes)");
+  int64_t device, bytes;
+  uint64_t address = 0;
+  bool lossless = false;
+  if (!get_i64(env, argv[0], &device) || !get_i64(env, argv[2], &bytes) || bytes <= 0)
+    return fail(env, "wrapDevicePointer: device and a positive byte count expected");
+  if (napi_get_value_bigint_uint64(env, argv[1], &address, &lossless) != napi_ok || !lossless ||
+      address == 0)
+    return fail(env, "wrapDevicePointer: the address must be a nonzero BigInt");
+  DeviceBuffer *b = new DeviceBuffer{reinterpret_cast<void *>(address), (size_t)bytes, (int)device, false};
+  napi_value out;
+  CHECK_NAPI(env, napi_create_external(env, b, finalize_buffer, nullptr, &out));
+  return out;
 }
 
 // upload(buffer, typedArray): synchronous host -> device copy of the array's bytes.
@@ -232,6 +253,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"destroy", nullptr, Destroy, nullptr, nullptr, nullptr, napi_default, nullptr},
       {"deviceAlloc", nullptr, DeviceAlloc, nullptr, nullptr, nullptr, napi_default, nullptr},
       {"deviceFree", nullptr, DeviceFree, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"wrapDevicePointer", nullptr, WrapDevicePointer, nullptr, nullptr, nullptr, napi_default, nullptr},
       {"upload", nullptr, Upload, nullptr, nullptr, nullptr, napi_default, nullptr},
       {"sample", nullptr, Sample, nullptr, nullptr, nullptr, napi_default, nullptr},
       {"version", nullptr, Version, nullptr, nullptr, nullptr, napi_default, nullptr},

@@ -45,6 +45,8 @@ export declare class DeviceLogits {
   readonly rows: number;
   readonly vocab: number;
   readonly dtype: 0 | 1;
+  static fromDevicePointer(address: bigint, rows: number, vocab: number, dtype?: 0 | 1,
+                           device?: number): DeviceLogits;
   upload(data: Float32Array | Uint16Array): this;
   free(): void;
 }

@@ -42,12 +42,23 @@ const DEFAULT_SAMPLING = Object.freeze({ temperature: 0.7, topK: 40, topP: 0.9, 
 
 /** Logits resident on the GPU: [rows, vocab] of f32, or of f16 given as Uint16Array bits. */
 class DeviceLogits {
-  constructor(device, rows, vocab, dtype) {
+  constructor(device, rows, vocab, dtype, address) {
     this.device = device;
     this.rows = rows;
     this.vocab = vocab;
     this.dtype = dtype;
-    this.buffer = native.deviceAlloc(device, rows * vocab * (dtype === F16 ? 2 : 4));
+    const bytes = rows * vocab * (dtype === F16 ? 2 : 4);
+    this.buffer = address === undefined
+      ? native.deviceAlloc(device, bytes)
+      : native.wrapDevicePointer(device, BigInt(address), bytes);
+  }
+
+  /**
+   * Logits that a HIP producer in this process already wrote (the decode loop's lm_head):
+   * `address` is the device pointer as a BigInt. The memory stays the caller's.
+   */
+  static fromDevicePointer(address, rows, vocab, dtype, device) {
+    return new DeviceLogits(device || 0, rows, vocab, dtype === undefined ? F32 : dtype, address);
   }
 
   upload(data) {
