@@ -36,6 +36,9 @@ def parse_args():
     ap.add_argument("--mixed-params", action="store_true",
                     help="config 3's per-row mix of k/T/p instead of k=50, p=0.9 on every row")
     ap.add_argument("--dtype", choices=["f32", "f16"], default="f32")
+    ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5], default=None,
+                    help="run BASELINE.json's configs[N-1] exactly as generated (parameters, "
+                         "dtype and shape) instead of the headline; a secondary measurement")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -109,12 +112,15 @@ def main() -> int:
 
     # Workload: config-3 logits (N(0, 3^2) + 8 spikes of +12..+18 per row), generated on the
     # host once; params per row from config 3, with k/p overridden to the headline's.
-    w = synth.config(3, rows=args.rows, vocab=args.vocab)
-    if not args.mixed_params:
-        w.top_k[:] = args.top_k
-        w.top_p[:] = args.top_p
-    if args.dtype == "f16":
-        w.logits = w.logits.astype(np.float16)
+    if args.config is not None:
+        w = synth.config(args.config)
+    else:
+        w = synth.config(3, rows=args.rows, vocab=args.vocab)
+        if not args.mixed_params:
+            w.top_k[:] = args.top_k
+            w.top_p[:] = args.top_p
+        if args.dtype == "f16":
+            w.logits = w.logits.astype(np.float16)
     itemsize = w.logits.dtype.itemsize
     bytes_per_launch = w.rows * w.vocab * itemsize
 
@@ -134,8 +140,13 @@ def main() -> int:
     sampler = S.GpuSampler(vocab_max=w.vocab, rows_max=w.rows, k_max=k_max)
     stream = torch.cuda.current_stream()
 
+    kcap = 256 if k_max <= 256 else 1024
+    whole = bool(np.any((w.top_k <= 0) | (w.top_k >= w.vocab))) and w.vocab > kcap
+    flags = S.TABBY_FLAG_FULL_VOCAB if whole else 0
+
     def step(i: int) -> None:
-        sampler.sample_device(buffers[i % ROTATE], pbufs[i % ROTATE], results, stream=stream)
+        sampler.sample_device(buffers[i % ROTATE], pbufs[i % ROTATE], results, flags=flags,
+                              stream=stream)
 
     for i in range(args.warmup):
         step(i)
@@ -168,14 +179,35 @@ def main() -> int:
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "sample_kernel_config3_traffic.json")
-    if os.path.exists(tpath) and args.dtype == "f32" and not args.mixed_params:
+    headline = args.config is None and args.dtype == "f32" and not args.mixed_params
+    if os.path.exists(tpath) and headline:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
 
+    dtype_name = "f16" if w.logits.dtype == np.float16 else "f32"
+    if args.config is None:
+        metric = "sampled rows/sec + achieved HBM GB/s, 256x151936 fp32 logits, top-k50/top-p0.9"
+        config = {
+            "workload": "config3-headline" if not args.mixed_params else "config3-mixed",
+            "rows": w.rows, "vocab": w.vocab,
+            "top_k": "per-row {1,20,50,100}" if args.mixed_params else args.top_k,
+            "top_p": "per-row {0.8,0.95,1.0}" if args.mixed_params else args.top_p,
+            "temperature": "per-row {0.5,0.7,1.0}",
+            "parallelism": "single GPU",
+        }
+    else:
+        metric = (f"sampled rows/sec + achieved HBM GB/s, BASELINE configs[{args.config - 1}] "
+                  f"({w.rows}x{w.vocab} {dtype_name})")
+        ks = sorted(set(int(k) for k in w.top_k))
+        config = {"workload": f"config{args.config}", "rows": w.rows, "vocab": w.vocab,
+                  "top_k": ks if len(ks) > 1 else ks[0],
+                  "top_p": sorted(set(float(p) for p in w.top_p)),
+                  "temperature": sorted(set(float(t) for t in w.temperature)),
+                  "parallelism": "single GPU"}
     out = {
-        "metric": "sampled rows/sec + achieved HBM GB/s, 256x151936 fp32 logits, top-k50/top-p0.9",
+        "metric": metric,
         "value": round(rows_per_s, 1),
         "unit": "rows/s",
         "n_gpus": 1,
@@ -185,16 +217,9 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": args.dtype,
-        "data": "synthetic (mulberry32 + Box-Muller, N(0,3^2) + 8 spikes/row; 4 rotated device batches)",
-        "config": {
-            "workload": "config3-headline" if not args.mixed_params else "config3-mixed",
-            "rows": w.rows, "vocab": w.vocab,
-            "top_k": "per-row {1,20,50,100}" if args.mixed_params else args.top_k,
-            "top_p": "per-row {0.8,0.95,1.0}" if args.mixed_params else args.top_p,
-            "temperature": "per-row {0.5,0.7,1.0}",
-            "parallelism": "single GPU",
-        },
+        "dtype": dtype_name,
+        "data": "synthetic (mulberry32 + Box-Muller, seeded per config; 4 rotated device batches)",
+        "config": config,
         "hbm_gbps": round(bytes_per_launch * args.steps / wall / 1e9, 1),
         "kernel_us_avg": round(avg_ms * 1000, 2),
         "kernel_us_median": round(med_ms * 1000, 2),
@@ -206,7 +231,7 @@ def main() -> int:
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
             "kernel": ("one tabby_sampler_sample_device call = wave_kernel (streaming: max, "
-                       "sum-exp, candidates) + merge_kernel (exact top-k, top-p, draw)"),
+                       "sum-exp, candidates) + wave_merge_kernel (exact top-k, top-p, draw)"),
             "bytes_per_launch": bytes_per_launch,
             "duration_us": round(avg_ms * 1000, 2),
         },

@@ -42,7 +42,7 @@ __device__ __forceinline__ uint32_t composite_key(uint64_t c) { return (uint32_t
 // scaling by 2^k. Contraction is off: each operation must round once, in this order, to
 // reproduce V8 to the last bit.
 // ---------------------------------------------------------------------------------------
-__device__ __noinline__ double fdlibm_exp(double x) {
+__device__ __forceinline__ double fdlibm_exp_inline(double x) {
 #pragma clang fp contract(off)
   const double ln2_hi = 6.93147180369123816490e-01;
   const double ln2_lo = 1.90821492927058770002e-10;
@@ -104,5 +104,8 @@ __device__ __noinline__ double fdlibm_exp(double x) {
                  (long long)((uint64_t)(0x3ff00000u + ((uint32_t)(k + 1000) << 20)) << 32)) *
          9.33263618503218878990e-302;
 }
+
+// Out-of-line form for call sites where code size matters more than the call.
+__device__ __noinline__ double fdlibm_exp(double x) { return fdlibm_exp_inline(x); }
 
 }  // namespace tabby

@@ -61,7 +61,6 @@ struct RowState {
 };
 
 struct Workspace {
-  uint32_t *row_theta;      // [rows_cap] key of the row's shared candidate bound (see wave_kernel)
   uint32_t *head_count;     // [rows_cap] head sizes
   SliceStat *stats;         // [rows_cap * kMaxSplits]
   uint64_t *cands;          // [rows_cap * row_cand_stride]
@@ -251,6 +250,14 @@ __device__ void finish_row(Smem &sm, const Launch &L, int row, const In *row_src
   }
 }
 
+// The first active lane's f64, bit for bit (the readfirstlane builtin takes 32-bit ints).
+__device__ __forceinline__ double readfirstlane_f64(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
 __device__ __forceinline__ double readlane_f64(double v, int lane) {
   const long long b = __double_as_longlong(v);
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b, lane);
@@ -407,10 +414,8 @@ struct SliceSmem {
   uint32_t flushed;     // candidates already written to global memory
   uint32_t wave_count[2][kWaves];  // by chunk parity: chunk c+1 writes while c is read
   float theta;
-  union {
-    uint32_t hist[kBins];      // only for the first chunk's theta, before any append
-    uint64_t list[kListCap];
-  };
+  uint32_t hist[kBins];       // radix-select histograms (first-chunk theta, list pruning)
+  uint64_t list[kListCap];
 };
 
 // theta from a selection threshold key, clamped to [-inf, +inf]: an early-exit prefix can
@@ -470,6 +475,39 @@ __device__ __forceinline__ void flush_list(SliceSmem &sm, uint64_t *region, uint
   __syncthreads();
 }
 
+// Drops from the LDS list every entry below the key of its kk-th largest composite and
+// raises sm.theta to that key. Whole workgroup; returns the new length (>= kk).
+__device__ __forceinline__ uint32_t prune_list(SliceSmem &sm, uint32_t have, uint32_t kk) {
+  auto each = [&](auto &&f) {
+    for (uint32_t i = threadIdx.x; i < have; i += kBlock) f(sm.list[i]);
+  };
+  const SelectResult r = radix_select(each, kk, sm.hist, sm.bs);
+  const uint32_t key = min(max((uint32_t)(r.prefix >> 32), kNegInfKey), 0xff800000u);
+  constexpr int kPer = kListCap / kBlock;
+  uint64_t v[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const uint32_t i = (uint32_t)(q * kBlock) + threadIdx.x;
+    v[q] = i < have ? sm.list[i] : 0ull;
+  }
+  if (threadIdx.x == 0) sm.bs.slot = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const uint32_t i = (uint32_t)(q * kBlock) + threadIdx.x;
+    if (i < have && composite_key(v[q]) >= key) sm.list[atomicAdd(&sm.bs.slot, 1u)] = v[q];
+  }
+  __syncthreads();
+  const uint32_t kept = sm.bs.slot;
+  if (threadIdx.x == 0) {
+    sm.theta = fmaxf(sm.theta, value_of(key));
+    sm.list_count = kept;
+    sm.committed = kept;
+  }
+  __syncthreads();
+  return kept;
+}
+
 template <typename In, int VEC>
 __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
   constexpr int ITEMS = kChunkPerLane / VEC;
@@ -522,28 +560,20 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
     }
 
     if (kk > 0) {
-      if (c == 0 && kk < n) {
-        // theta from the first chunk's lane or vector maxima.
-        if (kk <= kBlock) {
-          auto lanes = [&](auto &&f) { f(composite(key_of(cm), threadIdx.x)); };
-          const SelectResult r = radix_select(lanes, (uint32_t)kk, sm.hist, sm.bs);
-          if (threadIdx.x == 0) sm.theta = theta_of(r.prefix);
-        } else if (kk <= kBlock * ITEMS) {
-          auto vecs = [&](auto &&f) {
+      if (c == 0 && kk < min(n, kChunk)) {
+        // theta: the exact kk-th largest element of the first chunk (its padding excluded).
+        auto elems = [&](auto &&f) {
 #pragma unroll
-            for (int j = 0; j < ITEMS; ++j) {
-              float m = x[j * VEC];
-#pragma unroll
-              for (int q = 1; q < VEC; ++q) m = fmaxf(m, x[j * VEC + q]);
-              f(composite(key_of(m), (uint32_t)(j * kBlock + (int)threadIdx.x)));
-            }
-          };
-          const SelectResult r = radix_select(vecs, (uint32_t)kk, sm.hist, sm.bs);
-          if (threadIdx.x == 0) sm.theta = theta_of(r.prefix);
-        }
+          for (int e = 0; e < kChunkPerLane; ++e) {
+            const int local = chunk_local<VEC>(0, e);
+            if (local < n) f(composite(key_of(x[e]), (uint32_t)local));
+          }
+        };
+        const SelectResult r = radix_select(elems, (uint32_t)kk, sm.hist, sm.bs);
+        if (threadIdx.x == 0) sm.theta = theta_of(r.prefix);
         __syncthreads();
       }
-      const float theta = sm.theta;
+      float theta = sm.theta;
       const bool check_index = !(theta > -INFINITY);
       // Count first, so that a list that would overflow is flushed before the appends.
       uint32_t mine = 0;
@@ -557,8 +587,13 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
       uint32_t incoming = 0;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) incoming += sm.wave_count[c & 1][w];
-      const uint32_t have = sm.committed;
+      uint32_t have = sm.committed;
       if (incoming > 0) {
+        if (have + incoming > (uint32_t)kListCap && have >= (uint32_t)kk) {
+          // Prune: keep the entries whose key reaches the list's kk-th largest, and raise
+          // theta to it. Only massive ties can leave the list too full; it is then flushed.
+          have = prune_list(sm, have, (uint32_t)kk);
+        }
         if (have + incoming > (uint32_t)kListCap) flush_list(sm, region, have);
 #pragma unroll
         for (int e = 0; e < kChunkPerLane; ++e) {
@@ -590,7 +625,9 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
   const double ss = block_sum(term, sm.bs);
   uint32_t total = 0;
   if (kk > 0) {
-    const uint32_t have = sm.committed;
+    uint32_t have = sm.committed;
+    // A last prune keeps the merge's candidate set small (about kk plus ties per slice).
+    if (have > (uint32_t)kk + (uint32_t)kk / 4u) have = prune_list(sm, have, (uint32_t)kk);
     total = sm.flushed + have;
     const uint32_t at = sm.flushed;
     for (uint32_t i = threadIdx.x; i < have; i += kBlock) region[at + i] = sm.list[i];
@@ -616,11 +653,8 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
 // range), theta rises to the lower edge of the bin that holds the kk-th largest entry, and
 // the entries below are dropped -- no sort. (Only massive ties can keep a bin from
 // shrinking the list; then it is sorted in registers and cut to kk.)
-// A wave's bound on its own kk-th largest (kk = the row's pool size when the slice is longer
-// than the pool) also bounds the row's pool-th largest, so the waves of a row share the
-// largest bound any of them has proven: row_theta, raised with atomicMax; the merge drops
-// candidates below it. The list goes, unsorted, to the slice's candidate region; the merge
-// selects exactly.
+// At the end the list is sorted in registers and the slice's top min(count, kk) go to its
+// candidate region, so the merge works on sorted lists.
 // ---------------------------------------------------------------------------------------
 constexpr int kWChunkPerLane = 16;
 constexpr int kWChunk = kWaveSize * kWChunkPerLane;
@@ -678,6 +712,24 @@ __device__ __forceinline__ void wave_sort_list(uint64_t *list, int count, int ke
     if (i < keep) list[i] = v[r];
   }
   wave_lds_sync();
+}
+
+// Sorts list[0..count) descending in registers (count <= 64*R) and writes its top `keep`
+// to out[0..keep).
+template <int R>
+__device__ __forceinline__ void store_sorted_top(const uint64_t *list, int count, int keep, uint64_t *out) {
+  uint64_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + wave_lane();
+    v[r] = i < count ? list[i] : 0ull;
+  }
+  wave_sort_desc<R>(v);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + wave_lane();
+    if (i < keep) out[i] = v[r];
+  }
 }
 
 struct WaveSmem {
@@ -790,9 +842,6 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   const int kk = slice_keep(valid_params, keff, n, L.kcap, L.head_pass, L.topk_cap);
   const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
   uint64_t *region = W.cands + (size_t)row * W.row_cand_stride + (size_t)begin;
-  // The row's shared bound applies when this wave selects the row's whole pool.
-  const bool share = kk > 0 && kk == keff && kk < n;
-  uint32_t *row_theta = W.row_theta + row;
   const int prune_at = kWListCap - kWaveSize;
 
   float lane_max = -INFINITY;
@@ -800,12 +849,6 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   int count = 0;          // entries in the list; wave-uniform (readfirstlane keeps it scalar)
   uint32_t theta_key = kNegInfKey;
   float theta = -INFINITY;  // == value_of(theta_key)
-
-  auto publish = [&]() {
-    if (share) {
-      if (wave_lane() == 0) atomicMax(row_theta, theta_key);  // not waited for
-    }
-  };
 
   // Processes chunk c held in `cur` while chunk `nxt_chunk` loads into `nxt`.
   auto step = [&](int c, float (&cur)[kWChunkPerLane], float (&nxt)[kWChunkPerLane]) {
@@ -836,7 +879,6 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
       wave_sort_desc<1>(k1);
       theta_key = min(max((uint32_t)__builtin_amdgcn_readlane((int)k1[0], kk - 1), kNegInfKey), 0xff800000u);
       theta = value_of(theta_key);
-      publish();
     }
     // No lane reaches theta: nothing in this chunk can be a candidate.
     if (!__ballot(cm >= theta) && !partial) return;
@@ -853,7 +895,6 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
         count = __builtin_amdgcn_readfirstlane(pr.count);
         theta_key = (uint32_t)__builtin_amdgcn_readfirstlane((int)pr.theta_key);
         theta = value_of(theta_key);
-        publish();
       }
       const bool take = cur[e] >= theta;
       const uint64_t mask = __ballot(take);
@@ -876,23 +917,44 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
                           ? 0.0
                           : lane_sum * (double)__builtin_amdgcn_exp2f((lane_max - ms) * kLog2e);
   const double ss = wave_sum(term);
+  // The slice's top min(count, kk), sorted descending, go to its region: the merge only
+  // has to merge sorted lists.
+  int keep = 0;
   if (kk > 0) {
-    if (count > 2 * kk) {
+    if (count > 2 * kk || count > 4 * kWaveSize) {
       const Pruned pr = wave_prune_any(sm, count, kk, theta_key);
       count = __builtin_amdgcn_readfirstlane(pr.count);
-      theta_key = pr.theta_key;
-      publish();
     }
+    keep = min(count, kk);
     wave_lds_sync();
-    for (int i = wave_lane(); i < count; i += kWaveSize) region[i] = sm.list[i];
+    if (count <= kWaveSize) store_sorted_top<1>(sm.list, count, keep, region);
+    else if (count <= 2 * kWaveSize) store_sorted_top<2>(sm.list, count, keep, region);
+    else if (count <= 4 * kWaveSize) store_sorted_top<4>(sm.list, count, keep, region);
+    else store_sorted_top<8>(sm.list, count, keep, region);
   }
   if (wave_lane() == 0) {
     SliceStat st_out;
     st_out.max = ms;
-    st_out.count = (uint32_t)count;
+    st_out.count = (uint32_t)keep;
     st_out.sum = ss;
     W.stats[(size_t)row * kMaxSplits + slice] = st_out;
   }
+}
+
+// Smallest key whose scaled logit (l - max)/T in f64 is >= -40 (the max's key when T <= 0:
+// greedy needs only the row's maxima). Anything below has exp(.) < 2^-54 and, added in sorted
+// order, can change neither the scaled total nor a running sum, both of which are >= their
+// first term when it is added.
+__device__ __forceinline__ uint32_t head_threshold(float row_max, double T) {
+  const uint32_t top = key_of(row_max);
+  if (!(T > 0.0)) return top;
+  uint32_t lo = kNegInfKey, hi = top;
+  while (hi - lo > 1u) {
+    const uint32_t mid = lo + (hi - lo) / 2u;
+    const double q = ((double)value_of(mid) - (double)row_max) / T;
+    if (q >= -40.0) hi = mid; else lo = mid;
+  }
+  return hi;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -909,7 +971,6 @@ struct MergeSmem {
   double sum_exp;
   double pool_mass;
   double scaled_total;
-  uint32_t row_theta;
   uint32_t slice_first[kMaxSplits];
   double slice_term[kMaxSplits];
   uint64_t sorted[KCAP];
@@ -979,10 +1040,6 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
   }
   if (threadIdx.x == 0) {
     sm.bs.slot = 0u;
-    // The row's shared candidate bound: everything below it was already dropped by some
-    // slices and cannot be in the pool. Reset for the next launch.
-    sm.row_theta = W.row_theta[row];
-    W.row_theta[row] = kNegInfKey;
   }
 
   // 1. Row max and sum-exp, in slice order.
@@ -1016,7 +1073,7 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
   // 2. The exact top-keff of the row's candidates, sorted. The candidates include every
   //    element of the row's top-keff (each slice kept all elements >= a lower bound of its
   //    own kk-th largest value).
-  const uint32_t floor_key = sm.row_theta;  // read after the barriers above
+  const uint32_t floor_key = kNegInfKey;
   auto from_lds = [&](auto &&f) {
     for (int i = threadIdx.x; i < C; i += kBlock) {
       const uint64_t v = sm.cand[i];
@@ -1059,21 +1116,7 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
       rs.sum_exp = sum_exp;
       rs.status = TABBY_OK;
       rs.pad = 0;
-      const uint32_t top = key_of(row_max);
-      uint32_t head_key = top;  // greedy needs only the row's maxima
-      if (P.temperature > 0.0) {
-        // Smallest key whose scaled logit (l - max)/T in f64 is >= -40. Anything below has
-        // exp(.) < 2^-54 and can change neither the scaled total nor a running sum, both of
-        // which are >= their first term when it is added.
-        uint32_t lo = kNegInfKey, hi = top;
-        while (hi - lo > 1u) {
-          const uint32_t mid = lo + (hi - lo) / 2u;
-          const double q = ((double)value_of(mid) - (double)row_max) / P.temperature;
-          if (q >= -40.0) hi = mid; else lo = mid;
-        }
-        head_key = hi;
-      }
-      rs.head_key = min(head_key, list_key);
+      rs.head_key = min(head_threshold(row_max, P.temperature), list_key);
       W.row_state[row] = rs;
       W.head_count[row] = 0u;
     }
@@ -1112,6 +1155,311 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
   __syncthreads();
   bitonic_sort_desc(sm.sorted, npow);
   finish_row<KCAP, In>(sm, L, row, row_src, keff, row_max, sum_exp, P);
+}
+
+// ---------------------------------------------------------------------------------------
+// Kernel 2 for pools of at most 256 (wave_merge_kernel): one wave per row. Every slice left
+// its top min(kk, count) candidates sorted descending, so the row's top-k is a merge of
+// sorted lists: the accumulator (the first list) and each further list, loaded reversed, give
+// max(a_i, b_(n-1-i)) -- the top n of their union as a bitonic sequence -- which a bitonic
+// clean (register strides, then lane strides through DPP / permlane) sorts again. The slice
+// statistics and the head of every list are loaded in one round trip; the f64 tail of
+// sampleFromTopK then runs from LDS, its sequential sums on one lane.
+// ---------------------------------------------------------------------------------------
+struct WaveMergeSmem {
+  uint64_t sorted[kWaveKcap];
+  double a[kWaveKcap];  // exact terms exp(l - max) / sumExp
+  double b[kWaveKcap];  // exp((l - max) / T), then the weights
+  double c[kWaveKcap];  // running sums of the weights
+};
+
+// Bitonic clean of 64*R values (index r*64 + lane) into descending order.
+template <int R>
+__device__ __forceinline__ void bitonic_clean_desc(uint64_t (&a)[R]) {
+#pragma unroll
+  for (int rs = R / 2; rs > 0; rs >>= 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if ((r & rs) == 0) {
+        const uint64_t x = a[r], y = a[r | rs];
+        a[r] = tmax(x, y);
+        a[r | rs] = tmin(x, y);
+      }
+    }
+  }
+  const int lane = wave_lane();
+#pragma unroll
+  for (int stride = kWaveSize / 2; stride > 0; stride >>= 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint64_t o = xor_lane_by(a[r], stride);
+      a[r] = (lane & stride) == 0 ? tmax(a[r], o) : tmin(a[r], o);
+    }
+  }
+}
+
+// Row statistics from the slice statistics: max, and sum-exp as a fixed butterfly over the
+// slices' rescaled sums (deterministic for given inputs). Lane s holds slices s, s + 64, ...
+struct RowStats {
+  float max;
+  double sum_exp;
+  uint32_t cnt[kMaxSplits / kWaveSize];  // list lengths, by lane
+};
+
+__device__ __forceinline__ RowStats row_stats(const SliceStat *stats, int splits) {
+  const int lane = wave_lane();
+  SliceStat st[kMaxSplits / kWaveSize];
+#pragma unroll
+  for (int q = 0; q < kMaxSplits / kWaveSize; ++q) {
+    const int s = q * kWaveSize + lane;
+    st[q].max = -INFINITY;
+    st[q].count = 0u;
+    st[q].sum = 0.0;
+    if (s < splits) st[q] = stats[s];
+  }
+  RowStats out;
+  float m = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < kMaxSplits / kWaveSize; ++q) {
+    out.cnt[q] = st[q].count;
+    m = fmaxf(m, st[q].max);
+  }
+  out.max = wave_max(m);
+  double part = 0.0;
+#pragma unroll
+  for (int q = 0; q < kMaxSplits / kWaveSize; ++q)
+    if (st[q].max != -INFINITY) part += st[q].sum * fdlibm_exp_inline((double)st[q].max - (double)out.max);
+  out.sum_exp = wave_sum(part);
+  return out;
+}
+
+// Length of slice s's list (s wave-uniform).
+__device__ __forceinline__ int list_count(const RowStats &rs, int s) {
+  // One readlane per register and a scalar select (an indexed register array would be
+  // placed in scratch memory).
+  const int l = s % kWaveSize, q = s / kWaveSize;
+  const int c0 = __builtin_amdgcn_readlane((int)rs.cnt[0], l);
+  if (q == 0) return c0;
+  const int c1 = __builtin_amdgcn_readlane((int)rs.cnt[1], l);
+  const int c2 = __builtin_amdgcn_readlane((int)rs.cnt[2], l);
+  const int c3 = __builtin_amdgcn_readlane((int)rs.cnt[3], l);
+  return q == 1 ? c1 : q == 2 ? c2 : c3;
+}
+
+// Merges the row's sorted slice lists into the top 64*R composites, sorted descending, in
+// registers. Slice s's list starts at base + s*slice_len and holds rs.cnt(s) entries; reads
+// stay inside the row's `row_stride` entries and past a list's end are masked.
+template <int R>
+struct ListMerger {
+  static constexpr int kBatch = 4;  // lists whose loads are in flight together
+  const uint64_t *base;
+  int slice_len;
+  int64_t row_stride;
+  int splits;
+  uint64_t acc[R];
+  uint64_t raw[kBatch][R];
+
+  __device__ __forceinline__ void issue(int s, uint64_t (&dst)[R], bool reversed) const {
+    const uint64_t *list = base + (int64_t)s * slice_len;
+    const int room = (int)min((int64_t)slice_len, row_stride - (int64_t)s * slice_len);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int p = r * kWaveSize + wave_lane();
+      const int j = reversed ? kWaveSize * R - 1 - p : p;
+      dst[r] = list[min(j, room - 1)];
+    }
+  }
+  __device__ __forceinline__ static void mask(int n, uint64_t (&v)[R], bool reversed) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int p = r * kWaveSize + wave_lane();
+      const int j = reversed ? kWaveSize * R - 1 - p : p;
+      if (j >= n) v[r] = 0ull;
+    }
+  }
+  // Issues the first lists' loads (nothing is waited for).
+  __device__ __forceinline__ void start() {
+    issue(0, acc, false);
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q)
+      if (1 + q < splits) issue(1 + q, raw[q], true);
+  }
+  __device__ __forceinline__ void finish(const RowStats &rs) {
+    mask(list_count(rs, 0), acc, false);
+    for (int s0 = 1; s0 < splits; s0 += kBatch) {
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int s = s0 + q;
+        if (s < splits) {
+          uint64_t b[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) b[r] = raw[q][r];
+          if (s + kBatch < splits) issue(s + kBatch, raw[q], true);
+          mask(list_count(rs, s), b, true);
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r] = tmax(acc[r], b[r]);
+          bitonic_clean_desc<R>(acc);
+        }
+      }
+    }
+  }
+};
+
+// sampleFromTopK (src/engine/sampler.ts:147-212) over sm.sorted[0..K), K >= 1, in the
+// reference's order of f64 operations. Per-element terms are computed by all lanes; the
+// sums (poolMass, the scaled total, the running sums of the draw, which are the top-p
+// cumulative sums) are sequential left-to-right sums on lane 0.
+template <typename In>
+__device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch &L, int row,
+                                          const In *row_src, float max_logit, double sum_exp,
+                                          const tabby_row_params &P) {
+  const int lane = wave_lane();
+  const double T = P.temperature;
+  const double M = (double)max_logit;
+  for (int i = lane; i < K; i += kWaveSize) {
+    const double d = (double)value_of(composite_key(sm.sorted[i])) - M;
+    sm.a[i] = fdlibm_exp_inline(d) / sum_exp;
+    sm.b[i] = T > 0.0 ? fdlibm_exp_inline(d / T) : 0.0;
+  }
+  wave_lds_sync();
+  double pool = 0.0, scaled = 0.0;
+  if (lane == 0) {
+    for (int i = 0; i < K; ++i) {
+      pool += sm.a[i];
+      scaled += sm.b[i];
+    }
+  }
+  pool = readfirstlane_f64(pool);
+  tabby_row_result res;
+  res.max_logit = max_logit;
+  res.sum_exp = sum_exp;
+  res.pool_mass = pool;
+  res.status = TABBY_OK;
+  res.topk_count = min(K, L.topk_cap);
+  int chosen = 0;
+  if (!(T > 0.0)) {  // sampler.ts:159-167: greedy, the uniform unused
+    res.considered = 1;
+    res.pool_exhausted = 0;
+  } else {
+    scaled = readfirstlane_f64(scaled);
+    for (int i = lane; i < K; i += kWaveSize) sm.b[i] = sm.b[i] / scaled;
+    wave_lds_sync();
+    const double top_p = P.top_p;
+    int cut = K;
+    double total = 0.0;
+    if (lane == 0) {
+      double c = 0.0;
+      for (int i = 0; i < K; ++i) {
+        c += sm.b[i];
+        sm.c[i] = c;
+        if (top_p < 1.0 && c >= top_p) {
+          cut = i + 1;
+          break;
+        }
+      }
+      total = c;  // the running sum at cut - 1: the reference's total
+    }
+    wave_lds_sync();
+    cut = __builtin_amdgcn_readfirstlane(cut);
+    total = readfirstlane_f64(total);
+    const double target = P.uniform * total;
+    chosen = cut - 1;
+    for (int base = 0; base < cut; base += kWaveSize) {
+      const int i = base + lane;
+      const uint64_t hit = __ballot(i < cut && target < sm.c[min(i, cut - 1)]);
+      if (hit) {
+        chosen = base + __ffsll((unsigned long long)hit) - 1;
+        break;
+      }
+    }
+    res.considered = (uint32_t)cut;
+    res.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
+  }
+  const uint64_t cv = sm.sorted[chosen];
+  res.id = (int32_t)composite_index(cv);
+  res.probability = sm.a[chosen];
+  if (lane == 0) L.results[row] = res;
+  if (L.topk_cap > 0) {
+    const int m = min(K, L.topk_cap);
+    for (int i = lane; i < m; i += kWaveSize) {
+      const uint32_t idx = composite_index(sm.sorted[i]);
+      L.topk_ids[(size_t)row * L.topk_cap + i] = (int32_t)idx;
+      L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(L.vocab - 1)));
+    }
+  }
+}
+
+// Loads and merges the lists (R registers per lane), with the statistics math done while the
+// first lists are in flight; writes the merged top K to sm.sorted. Returns the row stats.
+template <int R>
+__device__ __forceinline__ RowStats merge_row(WaveMergeSmem &sm, const SliceStat *stats,
+                                              const uint64_t *lists, const Launch &L,
+                                              const Workspace &W, int K) {
+  ListMerger<R> mg;
+  mg.base = lists;
+  mg.slice_len = L.slice_len;
+  mg.row_stride = W.row_cand_stride;
+  mg.splits = L.splits;
+  mg.start();
+  const RowStats rs = row_stats(stats, L.splits);
+  mg.finish(rs);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (r * kWaveSize + wave_lane() < K) sm.sorted[r * kWaveSize + wave_lane()] = mg.acc[r];
+  wave_lds_sync();
+  return rs;
+}
+
+template <typename In>
+__global__ __launch_bounds__(kWaveSize) void wave_merge_kernel(Launch L, Workspace W) {
+  __shared__ WaveMergeSmem sm;
+  const int row = (int)blockIdx.x;
+  const int lane = wave_lane();
+  const int V = L.vocab;
+  const tabby_row_params P = L.params[row];
+  const bool valid_params = params_valid(P, L.k_max);
+  const int keff = effective_k(P, V);
+  const bool finite = valid_params && keff <= L.kcap;
+  const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V;
+  // Pool to merge: the row's top-k, or for a whole-vocabulary row the caller's top-k list.
+  const int K = !valid_params ? 0 : finite ? keff : L.head_pass ? min(L.topk_cap, V) : 0;
+  const SliceStat *stats = W.stats + (size_t)row * kMaxSplits;
+  const uint64_t *lists = W.cands + (size_t)row * W.row_cand_stride;
+
+  RowStats rs;
+  if (K <= 0) rs = row_stats(stats, L.splits);
+  else if (K <= kWaveSize) rs = merge_row<1>(sm, stats, lists, L, W, K);
+  else if (K <= 2 * kWaveSize) rs = merge_row<2>(sm, stats, lists, L, W, K);
+  else rs = merge_row<4>(sm, stats, lists, L, W, K);
+  const float row_max = rs.max;
+  const double sum_exp = rs.sum_exp;
+  const bool in_domain = (row_max > -INFINITY) && (row_max < INFINITY) && (sum_exp > 0.0) &&
+                         (sum_exp < INFINITY);
+  if (!valid_params || !in_domain || (!finite && !L.head_pass)) {
+    const int32_t status = !valid_params ? TABBY_EINVAL : !in_domain ? TABBY_EDOMAIN : TABBY_EINVAL;
+    if (lane == 0) {
+      write_status(L, row, status, row_max, sum_exp);
+      W.row_state[row].status = status;
+    }
+    return;
+  }
+  if (!finite) {
+    // Whole-vocabulary row: hand max / sum-exp / the head threshold to the head kernels. The
+    // head also covers the caller's top-k list: sorted[K-1] is its K-th entry.
+    if (lane == 0) {
+      RowState st;
+      st.max = row_max;
+      st.sum_exp = sum_exp;
+      st.status = TABBY_OK;
+      st.pad = 0;
+      const uint32_t list_key = K > 0 ? composite_key(sm.sorted[K - 1]) : 0xffffffffu;
+      st.head_key = min(head_threshold(row_max, P.temperature), list_key);
+      W.row_state[row] = st;
+      W.head_count[row] = 0u;
+    }
+    return;
+  }
+  wave_tail<In>(sm, K, L, row, row_src, row_max, sum_exp, P);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1438,12 +1786,9 @@ hipError_t launch_pair(const Launch &L, const Workspace &W, hipStream_t stream) 
   const dim3 slices((unsigned)(L.rows * L.splits)), rows((unsigned)L.rows);
   if (L.kcap <= kWaveKcap) {
     hipLaunchKernelGGL((wave_kernel<In, VEC>), slices, dim3(kWaveSize), 0, stream, L, W);
+    hipLaunchKernelGGL((wave_merge_kernel<In>), rows, dim3(kWaveSize), 0, stream, L, W);
   } else {
     hipLaunchKernelGGL((slice_kernel<In, VEC>), slices, dim3(kBlock), 0, stream, L, W);
-  }
-  if (L.kcap <= kKcapSmall) {
-    hipLaunchKernelGGL((merge_kernel<kKcapSmall, In>), rows, dim3(kBlock), 0, stream, L, W);
-  } else {
     hipLaunchKernelGGL((merge_kernel<kKcapLarge, In>), rows, dim3(kBlock), 0, stream, L, W);
   }
   return hipGetLastError();
@@ -1516,7 +1861,6 @@ int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_
     return at;
   };
   const size_t o_hcnt = carve(rows * 4);
-  const size_t o_rth = carve(rows * 4);
   const size_t o_stats = carve(rows * kMaxSplits * sizeof(SliceStat));
   const size_t o_cands = carve(rows * (size_t)h->ws.row_cand_stride * 8);
   const size_t o_rs = carve(rows * sizeof(RowState));
@@ -1528,7 +1872,6 @@ int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_
     return hip_fail(e, "hipMalloc(workspace)");
   }
   char *b = (char *)h->ws_base;
-  h->ws.row_theta = (uint32_t *)(b + o_rth);
   h->ws.head_count = (uint32_t *)(b + o_hcnt);
   h->ws.stats = (SliceStat *)(b + o_stats);
   h->ws.cands = (uint64_t *)(b + o_cands);
@@ -1536,7 +1879,6 @@ int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_
   h->params_dev = (tabby_row_params *)(b + o_par);
   h->results_dev = (tabby_row_result *)(b + o_res);
   e = hipMemset(h->ws_base, 0, off);
-  if (e == hipSuccess) e = hipMemsetD32((hipDeviceptr_t)h->ws.row_theta, (int)kNegInfKey, rows);
   if (e == hipSuccess) e = hipHostMalloc((void **)&h->params_pinned, rows * sizeof(tabby_row_params), hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc((void **)&h->results_pinned, rows * sizeof(tabby_row_result), hipHostMallocDefault);
   if (e == hipSuccess) e = hipDeviceSynchronize();

@@ -1,6 +1,7 @@
-// Wave-level (64-lane) building blocks: reductions, and a bitonic sort of 64*R values held
-// in registers (index r*64 + lane), which needs no LDS and no barrier -- the strides below
-// 64 are lane exchanges (__shfl_xor), the larger ones swaps between a lane's registers.
+// Wave-level (64-lane) building blocks: lane exchanges, reductions, and a bitonic sort of
+// 64*R values held in registers (index r*64 + lane), which needs no LDS and no barrier -- the
+// strides below 64 are lane exchanges (xor_lane), the larger ones swaps between a lane's
+// registers.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -12,16 +13,77 @@ constexpr int kWaveSize = 64;
 
 __device__ __forceinline__ int wave_lane() { return (int)(threadIdx.x & 63); }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+// The value held by lane (lane ^ S), S a power of two below 64, without going through LDS:
+// DPP quad permutes for 1 and 2, row shifts for 4, a row rotation for 8 (i + 8 mod 16 is
+// i ^ 8 within a 16-lane row), and gfx950's permlane swaps for 16 and 32, which exchange
+// alternate 16-lane rows and the two 32-lane halves of a pair of registers.
+template <int S>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  static_assert(S == 1 || S == 2 || S == 4 || S == 8 || S == 16 || S == 32, "lane stride");
+  if constexpr (S == 1) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+  } else if constexpr (S == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+  } else if constexpr (S == 4) {
+    const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x104, 0xF, 0xF, false);  // row_shl:4
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    return (wave_lane() & 4) ? dn : up;
+  } else if constexpr (S == 8) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (S == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (wave_lane() & 16) ? r[0] : r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (wave_lane() & 32) ? r[0] : r[1];
+  }
 }
 
+template <int S>
+__device__ __forceinline__ uint64_t xor_lane(uint64_t v) {
+  return (uint64_t)xor_lane<S>((uint32_t)v) | ((uint64_t)xor_lane<S>((uint32_t)(v >> 32)) << 32);
+}
+
+template <int S>
+__device__ __forceinline__ float xor_lane(float v) {
+  return __uint_as_float(xor_lane<S>(__float_as_uint(v)));
+}
+
+template <int S>
+__device__ __forceinline__ double xor_lane(double v) {
+  return __longlong_as_double((long long)xor_lane<S>((uint64_t)__double_as_longlong(v)));
+}
+
+// xor_lane with a stride known only after unrolling.
+template <typename T>
+__device__ __forceinline__ T xor_lane_by(T v, int stride) {
+  switch (stride) {
+    case 1: return xor_lane<1>(v);
+    case 2: return xor_lane<2>(v);
+    case 4: return xor_lane<4>(v);
+    case 8: return xor_lane<8>(v);
+    case 16: return xor_lane<16>(v);
+    default: return xor_lane<32>(v);
+  }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, xor_lane<32>(v));
+  v = fmaxf(v, xor_lane<16>(v));
+  v = fmaxf(v, xor_lane<8>(v));
+  v = fmaxf(v, xor_lane<4>(v));
+  v = fmaxf(v, xor_lane<2>(v));
+  return fmaxf(v, xor_lane<1>(v));
+}
+
+// A fixed butterfly: the same inputs give the same bits on every lane and every run.
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v += xor_lane<32>(v);
+  v += xor_lane<16>(v);
+  v += xor_lane<8>(v);
+  v += xor_lane<4>(v);
+  v += xor_lane<2>(v);
+  return v + xor_lane<1>(v);
 }
 
 // Makes this wave's LDS writes visible to its other lanes (LDS operations of one wave
@@ -57,7 +119,7 @@ __device__ __forceinline__ void wave_sort_desc(T (&v)[R]) {
       } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const T o = __shfl_xor(v[r], stride);
+          const T o = xor_lane_by(v[r], stride);
           const bool lower = (lane & stride) == 0;
           const bool desc = (((r * kWaveSize) | lane) & size) == 0;
           v[r] = (lower == desc) ? tmax(v[r], o) : tmin(v[r], o);
