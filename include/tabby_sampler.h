@@ -121,6 +121,16 @@ TABBY_API const char *tabby_version(void);
  */
 TABBY_API int tabby_debug_exp(const double *x_dev, double *y_dev, int64_t n, void *stream);
 
+/*
+ * Diagnostic: the device's bit-exact sequential f64 sum (the left-to-right sums of
+ * sampler.ts:156-203: poolMass, the scaled total, the running sums), computed in parallel by
+ * one wave. terms_dev[0..n) must be >= 0 with terms_dev[0] > 0; prefix_dev[j] receives the
+ * j-th partial sum up to the first that is >= stop_at (INFINITY: none), and *count_dev the
+ * number of partial sums written. For parity tests.
+ */
+TABBY_API int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double stop_at,
+                                  double *prefix_dev, int32_t *count_dev, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

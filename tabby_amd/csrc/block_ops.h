@@ -121,12 +121,14 @@ __device__ __forceinline__ int digit_shift(int pass) {
   return pass == 0 ? 53 : pass == 1 ? 42 : pass == 2 ? 32 : pass == 3 ? 21 : pass == 4 ? 10 : 0;
 }
 
+// max_passes < 6 stops early: the result then only bounds the need-th largest from below
+// (every selected element is still >= prefix, and at least `need` elements are selected).
 template <class ForEach>
 __device__ __forceinline__ SelectResult radix_select(ForEach for_each, uint32_t need, uint32_t *hist,
-                                     BlockScratch &s) {
+                                     BlockScratch &s, int max_passes = 6) {
   uint64_t prefix = 0;
   int done = 64;
-  for (int pass = 0; pass < 6; ++pass) {
+  for (int pass = 0; pass < max_passes; ++pass) {
     const int shift = digit_shift(pass);
     const uint32_t dmask = (pass == 2 || pass == 5) ? 0x3ffu : 0x7ffu;
     for (int i = threadIdx.x; i < kBins; i += kBlock) hist[i] = 0u;

@@ -1,0 +1,197 @@
+// Sequential f64 sums, bit for bit, computed by a whole wave.
+//
+// The reference adds its terms one at a time, left to right (src/engine/sampler.ts:156-203:
+// poolMass, the scaled total, the running sums of the draw), so each partial sum is
+// P_j = fl(P_(j-1) + t_j) with IEEE round-to-nearest-even. For non-negative terms this
+// chain can be evaluated in parallel without changing a single bit:
+//
+//   While P lies in one binade [2^E, 2^(E+1)) its ulp is u = 2^(E-52) and P = m*u with an
+//   integer m < 2^53. The exact sum P + t rounds to the nearest multiple of u as long as the
+//   result stays below 2^(E+1), so fl(P + t) = P + u * rint(t / u) -- except when t / u has
+//   a fractional part of exactly 1/2, where the tie goes to the even multiple and so depends
+//   on m. t / u is an exact power-of-two scaling of t. Hence, between "events", the partial
+//   sums are m*u + u * (an integer prefix sum of rint(t_j / u)), and an integer prefix sum
+//   has no order dependence.
+//
+//   An event is a term whose addition is a tie, or that takes the integer sum to 2^53 or
+//   beyond (the sum leaves the binade and is rounded with a coarser ulp). That one term is
+//   added with an ordinary f64 add from the exact P before it; then the binade is
+//   recomputed and the scan resumes after it. P only grows (terms are >= 0), so there are at
+//   most a few dozen binade changes; exact ties need terms whose bits end exactly half an
+//   ulp below P, which are rare in practice and are handled correctly when they occur.
+//
+// Integers below 2^53 are exact in f64, so the prefix sums are done in f64: every partial
+// sum of non-negative integers is exact while it is below 2^53, and once the true value
+// reaches 2^53 the rounded value is >= 2^53 too (2^53 is representable and rounding is
+// monotone), which is exactly the event test.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "wave_ops.h"
+
+namespace tabby {
+
+constexpr double kTwo52 = 4503599627370496.0;
+constexpr double kTwo53 = 9007199254740992.0;
+constexpr int kSeqShort = 256;  // sums up to this length run on one lane
+
+// Lane i receives lane i - S of its 16-lane row, or +0 for the first S lanes of the row.
+template <int S>
+__device__ __forceinline__ double row_shift_up(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, 0x110 + S, 0xF, 0xF, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), 0x110 + S, 0xF, 0xF, true);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+__device__ __forceinline__ double lane_f64(double v, int lane) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Inclusive prefix sum over the wave's lanes of non-negative integer-valued v (see above:
+// exact below 2^53, >= 2^53 otherwise): within rows of 16 by DPP shifts, then the totals of
+// the rows below.
+__device__ __forceinline__ double wave_inclusive_scan(double x) {
+  x += row_shift_up<1>(x);
+  x += row_shift_up<2>(x);
+  x += row_shift_up<4>(x);
+  x += row_shift_up<8>(x);
+  const double r0 = lane_f64(x, 15), r1 = lane_f64(x, 31), r2 = lane_f64(x, 47);
+  const int row = wave_lane() >> 4;
+  const double below = row == 0 ? 0.0 : row == 1 ? r0 : row == 2 ? r0 + r1 : (r0 + r1) + r2;
+  return x + below;
+}
+
+struct SeqSum {
+  double total;  // the last partial sum computed
+  int count;     // terms added (the sum stopped early if count < n)
+};
+
+// Short sums: lane 0 adds left to right, eight loads ahead of the adds.
+__device__ __forceinline__ SeqSum lane_seq_sum(const double *t, int n, double *out, double stop_at) {
+  double P = 0.0;
+  int count = n;
+  if (wave_lane() == 0) {
+    P = t[0];
+    if (out) out[0] = P;
+    if (P >= stop_at) count = 1;
+    for (int b = 1; b < n && count == n; b += 8) {
+      double v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = b + q < n ? t[b + q] : 0.0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        if (b + q < n && count == n) {
+          P += v[q];
+          if (out) out[b + q] = P;
+          if (P >= stop_at) count = b + q + 1;
+        }
+      }
+    }
+  }
+  const uint64_t bits = (uint64_t)__double_as_longlong(P);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bits);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bits >> 32));
+  return {__longlong_as_double((long long)(((uint64_t)hi << 32) | lo)),
+          __builtin_amdgcn_readfirstlane(count)};
+}
+
+// Adds t[0..n) left to right (n >= 1, every t_j >= 0, t[0] > 0, and every partial sum at
+// least 2^-960 so that its ulp is a normal number) exactly as a sequential f64 loop would.
+// If out is non-null, out[j] receives the j-th partial sum (out may be t itself). The sum
+// stops at the first j whose partial sum is >= stop_at (INFINITY: none); count is then
+// j + 1. t and out live in LDS or global memory; all 64 lanes call this together.
+__device__ __forceinline__ SeqSum wave_seq_sum(const double *t, int n, double *out, double stop_at) {
+  if (n <= kSeqShort) return lane_seq_sum(t, n, out, stop_at);
+  const int lane = wave_lane();
+  double P = t[0];
+  if (out && lane == 0) out[0] = P;
+  if (P >= stop_at) return {P, 1};
+  int a = 1;
+  while (a < n) {
+    // The binade of P: P = m * u with m in [2^52, 2^53).
+    const int E = ((int)((uint64_t)__double_as_longlong(P) >> 52) & 0x7ff) - 1023;
+    const double u = __longlong_as_double((long long)((uint64_t)(E - 52 + 1023) << 52));
+    const double scale = __longlong_as_double((long long)((uint64_t)(52 - E + 1023) << 52));
+    const double m = P * scale;
+    // Lane L takes term a + L: its rounded increment and whether it is a tie.
+    const int j = a + lane;
+    const double q = j < n ? t[j] * scale : 0.0;
+    const double r = __builtin_rint(q);
+    const bool tie = q < kTwo52 && q - __builtin_floor(q) == 0.5;
+    const double cum = m + wave_inclusive_scan(r);
+    const bool crosses = cum >= kTwo53;
+    const bool stops = cum * u >= stop_at;
+    const uint64_t flagged = __ballot(j < n && (tie || crosses || stops));
+    const int Lf = flagged ? __ffsll((unsigned long long)flagged) - 1 : kWaveSize;
+    // Partial sums before the first flagged term are exact: cum * u.
+    if (out && j < n && lane < Lf) out[j] = cum * u;
+    if (Lf == kWaveSize) {
+      const int last = min(n, a + kWaveSize) - 1;
+      P = lane_f64(cum, last - a) * u;
+      a = last + 1;
+      continue;
+    }
+    const int jf = a + Lf;
+    const bool plain_stop = (__builtin_amdgcn_readlane((int)(stops && !tie && !crosses), Lf)) != 0;
+    if (plain_stop) {  // exact partial sum that reaches stop_at
+      const double at = lane_f64(cum, Lf) * u;
+      if (out && lane == 0) out[jf] = at;
+      return {at, jf + 1};
+    }
+    // A tie or a binade change: one ordinary f64 add from the exact partial sum before it.
+    const double before = (Lf == 0 ? m : lane_f64(cum, Lf - 1)) * u;
+    P = before + t[jf];
+    if (out && lane == 0) out[jf] = P;
+    if (P >= stop_at) return {P, jf + 1};
+    a = jf + 1;
+  }
+  return {P, n};
+}
+
+// Two independent left-to-right sums over the same length (poolMass and the scaled total):
+// short ones interleave on lane 0, long ones use the wave scan for each. The second is
+// skipped (0) when want_b is false.
+__device__ __forceinline__ void wave_seq_sum2(const double *a, const double *b, int n, bool want_b,
+                                              double *sum_a, double *sum_b) {
+  if (n > kSeqShort) {
+    *sum_a = wave_seq_sum(a, n, nullptr, INFINITY).total;
+    *sum_b = want_b ? wave_seq_sum(b, n, nullptr, INFINITY).total : 0.0;
+    return;
+  }
+  double pa = 0.0, pb = 0.0;
+  if (wave_lane() == 0) {
+    pa = a[0];
+    pb = b[0];
+    for (int base = 1; base < n; base += 8) {
+      double va[8], vb[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        va[q] = base + q < n ? a[base + q] : 0.0;
+        vb[q] = base + q < n ? b[base + q] : 0.0;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        if (base + q < n) {
+          pa += va[q];
+          pb += vb[q];
+        }
+      }
+    }
+  }
+  auto bcast = [](double v) {
+    const uint64_t bits = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bits);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bits >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+  };
+  *sum_a = bcast(pa);
+  *sum_b = want_b ? bcast(pb) : 0.0;
+}
+
+}  // namespace tabby

@@ -35,6 +35,7 @@
 
 #include "block_ops.h"
 #include "device_math.h"
+#include "seqsum.h"
 #include "wave_ops.h"
 #include "tabby_sampler.h"
 
@@ -177,68 +178,64 @@ __device__ void finish_row(Smem &sm, const Launch &L, int row, const In *row_src
                            int count, float max_logit, double sum_exp,
                            const tabby_row_params &P) {
   const double T = P.temperature;
+  double *exact = sm.u.tail.exact;
+  double *w = sm.u.tail.w;
   for (int i = threadIdx.x; i < count; i += kBlock) {
     const float l = value_of(composite_key(sm.sorted[i]));
     const double d = (double)l - (double)max_logit;
-    sm.u.tail.exact[i] = fdlibm_exp(d) / sum_exp;
-    sm.u.tail.w[i] = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
+    exact[i] = fdlibm_exp(d) / sum_exp;
+    w[i] = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    double pool = 0.0, scaled = 0.0;
-    for (int i = 0; i < count; ++i) {
-      pool += sm.u.tail.exact[i];
-      scaled += sm.u.tail.w[i];
+  // Sequential sums (bit-exact, computed by wave 0; see seqsum.h).
+  if (wave_id() == 0) {
+    double pool, scaled;
+    wave_seq_sum2(exact, w, count, T > 0.0, &pool, &scaled);
+    if (lane_id() == 0) {
+      sm.pool_mass = pool;
+      sm.scaled_total = scaled;
     }
-    sm.pool_mass = pool;
-    sm.scaled_total = scaled;
   }
   __syncthreads();
   const double pool_mass = sm.pool_mass;
   const double scaled_total = sm.scaled_total;
   if (T > 0.0) {
-    for (int i = threadIdx.x; i < count; i += kBlock) sm.u.tail.w[i] = sm.u.tail.w[i] / scaled_total;
+    for (int i = threadIdx.x; i < count; i += kBlock) w[i] = w[i] / scaled_total;
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
+  if (wave_id() == 0) {
     tabby_row_result r;
     r.max_logit = max_logit;
     r.sum_exp = sum_exp;
     r.pool_mass = pool_mass;
     r.status = TABBY_OK;
     r.topk_count = min(count, L.topk_cap);
+    int chosen = 0;
     if (T <= 0.0) {
-      r.id = (int32_t)composite_index(sm.sorted[0]);
-      r.probability = sm.u.tail.exact[0];
       r.considered = 1;
       r.pool_exhausted = 0;
     } else {
-      double *c = sm.u.tail.w;  // becomes the running sums in place
+      // The running sums of the weights (in place), up to the first that reaches top-p.
       const double top_p = P.top_p;
-      int cut = count;
-      double acc = 0.0;
-      for (int i = 0; i < count; ++i) {
-        acc += c[i];
-        c[i] = acc;
-        if (top_p < 1.0 && acc >= top_p) {
-          cut = i + 1;
+      const SeqSum run = wave_seq_sum(w, count, w, top_p < 1.0 ? top_p : INFINITY);
+      wave_lds_sync();
+      const int cut = run.count;
+      const double target = P.uniform * run.total;
+      chosen = cut - 1;
+      for (int base = 0; base < cut; base += kWaveSize) {
+        const int i = base + lane_id();
+        const uint64_t hit = __ballot(i < cut && target < w[min(i, cut - 1)]);
+        if (hit) {
+          chosen = base + __ffsll((unsigned long long)hit) - 1;
           break;
         }
       }
-      const double target = P.uniform * c[cut - 1];
-      int chosen = cut - 1;
-      for (int i = 0; i < cut; ++i) {
-        if (target < c[i]) {
-          chosen = i;
-          break;
-        }
-      }
-      r.id = (int32_t)composite_index(sm.sorted[chosen]);
-      r.probability = sm.u.tail.exact[chosen];
       r.considered = (uint32_t)cut;
       r.pool_exhausted = (top_p < 1.0 && pool_mass < top_p) ? 1 : 0;
     }
-    L.results[row] = r;
+    r.id = (int32_t)composite_index(sm.sorted[chosen]);
+    r.probability = exact[chosen];
+    if (lane_id() == 0) L.results[row] = r;
   }
   if (L.topk_cap > 0) {
     const int m = min(count, L.topk_cap);
@@ -409,7 +406,7 @@ constexpr int kListCap = kChunk;  // a whole chunk always fits after a flush
 
 struct SliceSmem {
   BlockScratch bs;
-  uint32_t list_count;  // appended to with atomics during a chunk
+  uint32_t list_count;  // list length after a prune or flush
   uint32_t committed;   // list_count as of the last chunk boundary (stable between barriers)
   uint32_t flushed;     // candidates already written to global memory
   uint32_t wave_count[2][kWaves];  // by chunk parity: chunk c+1 writes while c is read
@@ -481,7 +478,8 @@ __device__ __forceinline__ uint32_t prune_list(SliceSmem &sm, uint32_t have, uin
   auto each = [&](auto &&f) {
     for (uint32_t i = threadIdx.x; i < have; i += kBlock) f(sm.list[i]);
   };
-  const SelectResult r = radix_select(each, kk, sm.hist, sm.bs);
+  // Two radix passes (the key's top 22 bits) suffice: entries tied on the key are kept anyway.
+  const SelectResult r = radix_select(each, kk, sm.hist, sm.bs, 2);
   const uint32_t key = min(max((uint32_t)(r.prefix >> 32), kNegInfKey), 0xff800000u);
   constexpr int kPer = kListCap / kBlock;
   uint64_t v[kPer];
@@ -573,20 +571,27 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
         if (threadIdx.x == 0) sm.theta = theta_of(r.prefix);
         __syncthreads();
       }
-      float theta = sm.theta;
+      const float theta = sm.theta;
       const bool check_index = !(theta > -INFINITY);
-      // Count first, so that a list that would overflow is flushed before the appends.
+      // Count first (ballots, kept for the appends), so that a list that would overflow is
+      // pruned or flushed before anything is appended; each wave's slots then follow from
+      // the per-wave counts, with no atomics.
+      uint64_t masks[kChunkPerLane];
       uint32_t mine = 0;
 #pragma unroll
-      for (int e = 0; e < kChunkPerLane; ++e)
-        mine += (x[e] >= theta && (!check_index || chunk_local<VEC>(c, e) < n)) ? 1u : 0u;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) mine += __shfl_xor(mine, o);
+      for (int e = 0; e < kChunkPerLane; ++e) {
+        masks[e] = __ballot(x[e] >= theta && (!check_index || chunk_local<VEC>(c, e) < n));
+        mine += (uint32_t)__popcll(masks[e]);
+      }
       if (lane_id() == 0) sm.wave_count[c & 1][wave_id()] = mine;
       __syncthreads();
-      uint32_t incoming = 0;
+      uint32_t incoming = 0, before = 0;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) incoming += sm.wave_count[c & 1][w];
+      for (int w = 0; w < kWaves; ++w) {
+        const uint32_t wc = sm.wave_count[c & 1][w];
+        before += w < wave_id() ? wc : 0u;
+        incoming += wc;
+      }
       uint32_t have = sm.committed;
       if (incoming > 0) {
         if (have + incoming > (uint32_t)kListCap && have >= (uint32_t)kk) {
@@ -594,23 +599,23 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
           // theta to it. Only massive ties can leave the list too full; it is then flushed.
           have = prune_list(sm, have, (uint32_t)kk);
         }
-        if (have + incoming > (uint32_t)kListCap) flush_list(sm, region, have);
+        if (have + incoming > (uint32_t)kListCap) {
+          flush_list(sm, region, have);
+          have = 0;
+        }
+        uint32_t at = have + before;  // a chunk holds at most kChunk <= kListCap candidates
 #pragma unroll
         for (int e = 0; e < kChunkPerLane; ++e) {
-          const int local = chunk_local<VEC>(c, e);
-          const bool take = x[e] >= theta && (!check_index || local < n);
-          const uint64_t mask = __ballot(take);
+          const uint64_t mask = masks[e];
           if (mask) {
-            uint32_t base = 0;
-            if (lane_id() == 0) base = atomicAdd(&sm.list_count, (uint32_t)__popcll(mask));
-            base = __shfl(base, 0);
-            const uint32_t at = base + lanes_below(mask);
-            // A chunk holds at most kChunk == kListCap candidates; the bound is a guard.
-            if (take && at < (uint32_t)kListCap) sm.list[at] = composite(key_of(x[e]), (uint32_t)(begin + local));
+            if ((mask >> lane_id()) & 1ull)
+              sm.list[at + lanes_below(mask)] =
+                  composite(key_of(x[e]), (uint32_t)(begin + chunk_local<VEC>(c, e)));
+            at += (uint32_t)__popcll(mask);
           }
         }
         __syncthreads();
-        if (threadIdx.x == 0) sm.committed = sm.list_count;  // read after the next barrier
+        if (threadIdx.x == 0) sm.committed = have + incoming;  // read after the next barrier
       }
     }
 #pragma unroll
@@ -962,7 +967,7 @@ __device__ __forceinline__ uint32_t head_threshold(float row_max, double T) {
 // (in slice order, so the result does not depend on scheduling), the exact top-keff of the
 // slices' candidates, an LDS bitonic sort, and sampleFromTopK.
 // ---------------------------------------------------------------------------------------
-constexpr int kCandLds = 8192;  // candidate lists up to this size are staged in LDS
+constexpr int kCandLds = 4096;  // candidate lists up to this size are staged in LDS (two workgroups fit a CU)
 
 template <int KCAP>
 struct MergeSmem {
@@ -1322,14 +1327,8 @@ __device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch
     sm.b[i] = T > 0.0 ? fdlibm_exp_inline(d / T) : 0.0;
   }
   wave_lds_sync();
-  double pool = 0.0, scaled = 0.0;
-  if (lane == 0) {
-    for (int i = 0; i < K; ++i) {
-      pool += sm.a[i];
-      scaled += sm.b[i];
-    }
-  }
-  pool = readfirstlane_f64(pool);
+  double pool, scaled;
+  wave_seq_sum2(sm.a, sm.b, K, T > 0.0, &pool, &scaled);
   tabby_row_result res;
   res.max_logit = max_logit;
   res.sum_exp = sum_exp;
@@ -1341,27 +1340,14 @@ __device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch
     res.considered = 1;
     res.pool_exhausted = 0;
   } else {
-    scaled = readfirstlane_f64(scaled);
     for (int i = lane; i < K; i += kWaveSize) sm.b[i] = sm.b[i] / scaled;
     wave_lds_sync();
+    // The running sums of the weights, stopping at the first that reaches top-p: the cut.
     const double top_p = P.top_p;
-    int cut = K;
-    double total = 0.0;
-    if (lane == 0) {
-      double c = 0.0;
-      for (int i = 0; i < K; ++i) {
-        c += sm.b[i];
-        sm.c[i] = c;
-        if (top_p < 1.0 && c >= top_p) {
-          cut = i + 1;
-          break;
-        }
-      }
-      total = c;  // the running sum at cut - 1: the reference's total
-    }
+    const SeqSum run = wave_seq_sum(sm.b, K, sm.c, top_p < 1.0 ? top_p : INFINITY);
     wave_lds_sync();
-    cut = __builtin_amdgcn_readfirstlane(cut);
-    total = readfirstlane_f64(total);
+    const int cut = run.count;
+    const double total = run.total;  // the running sum at cut - 1: the reference's total
     const double target = P.uniform * total;
     chosen = cut - 1;
     for (int base = 0; base < cut; base += kWaveSize) {
@@ -1541,12 +1527,36 @@ constexpr int kHeadBatch = 4096;
 struct HeadSmem {
   BlockScratch bs;
   uint64_t batch[kHeadBatch];
-  double vals[kHeadBatch];
   uint32_t hist[kBins];
   double scaled_total;
-  double run;
+  double total;
   int cut;
+  int chosen;
 };
+
+// First i in [0, n) with target < c[i] (c non-decreasing), or n - 1 when there is none: a
+// 64-ary search by one wave, each step probing 64 evenly spaced entries.
+__device__ __forceinline__ int wave_first_above(const double *c, int n, double target) {
+  int lo = 0, hi = n;  // the answer lies in [lo, hi]; hi == n means "none yet"
+  while (hi - lo > kWaveSize) {
+    const int step = (hi - lo + kWaveSize - 1) / kWaveSize;
+    const int probe = lo + wave_lane() * step;
+    const uint64_t hit = __ballot(probe < hi && target < c[min(probe, n - 1)]);
+    if (!hit) {
+      lo = lo + (kWaveSize - 1) * step + 1;
+      lo = min(lo, hi);
+    } else {
+      const int f = __ffsll((unsigned long long)hit) - 1;
+      const int new_hi = lo + f * step;
+      lo = f == 0 ? lo : lo + (f - 1) * step + 1;
+      hi = new_hi;
+    }
+  }
+  const int i = lo + wave_lane();
+  const uint64_t hit = __ballot(i < hi && target < c[min(i, n - 1)]);
+  if (hit) return lo + __ffsll((unsigned long long)hit) - 1;
+  return hi < n ? hi : n - 1;
+}
 
 template <typename In>
 __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace W) {
@@ -1568,8 +1578,7 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
   const double T = P.temperature;
 
   // Pass 1: the head in descending batches of up to kHeadBatch; each batch is the top of
-  // what is left below the previous batch's smallest entry.
-  if (threadIdx.x == 0) sm.scaled_total = 0.0;
+  // what is left below the previous batch's smallest entry. Per element: exp((l - M)/T).
   double pool_head = 0.0, e_head = 0.0;
   uint64_t upper = ~0ull;  // exclusive; real composites are all smaller
   for (int pos = 0; pos < H;) {
@@ -1613,20 +1622,13 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
       const uint64_t v = sm.batch[i];
       const double d = (double)value_of(composite_key(v)) - (double)M;
       const double e = fdlibm_exp(d);
-      const double sv = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
       pool_part += e / S1;
       e_part += e;
-      sm.vals[i] = sv;
       sorted[pos + i] = v;
-      sg[pos + i] = sv;
+      sg[pos + i] = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
     }
     pool_head += block_sum(pool_part, sm.bs);
     e_head += block_sum(e_part, sm.bs);
-    if (threadIdx.x == 0) {  // the scaled total, sequentially in sorted order
-      double S = sm.scaled_total;
-      for (int i = 0; i < b; ++i) S += sm.vals[i];
-      sm.scaled_total = S;
-    }
     upper = sm.batch[b - 1];
     pos += b;
     __syncthreads();
@@ -1645,47 +1647,33 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
     res.considered = 1;
     res.pool_exhausted = 0;
   } else {
-    // Pass 2: running sums of w = s / S, in sorted order, until top-p is reached.
+    // The scaled total over the sorted head (bit-exact sequential sum, wave 0).
+    if (wave_id() == 0) {
+      const double S = wave_seq_sum(sg, H, nullptr, INFINITY).total;
+      if (lane_id() == 0) sm.scaled_total = S;
+    }
+    __syncthreads();
     const double S = sm.scaled_total;
+    for (int i = threadIdx.x; i < H; i += kBlock) cg[i] = sg[i] / S;
+    __syncthreads();
+    // Running sums of the weights up to the first that reaches top-p (the cut); without a
+    // cut the whole vocabulary is considered.
     const double top_p = P.top_p;
-    if (threadIdx.x == 0) {
-      sm.run = 0.0;
-      sm.cut = -1;
-    }
-    int stop = H;  // running sums exist for [0, stop)
-    for (int pos = 0; pos < H; pos += kHeadBatch) {
-      const int b = min(kHeadBatch, H - pos);
-      __syncthreads();
-      for (int i = threadIdx.x; i < b; i += kBlock) sm.vals[i] = sg[pos + i] / S;
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        double c = sm.run;
-        for (int i = 0; i < b; ++i) {
-          c += sm.vals[i];
-          cg[pos + i] = c;
-          if (top_p < 1.0 && c >= top_p) {
-            sm.cut = pos + i + 1;
-            break;
-          }
-        }
-        sm.run = c;
-      }
-      __syncthreads();
-      if (sm.cut >= 0) {
-        stop = sm.cut;
-        break;
+    if (wave_id() == 0) {
+      const SeqSum run = wave_seq_sum(cg, H, cg, top_p < 1.0 ? top_p : INFINITY);
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");  // the sums are read by other lanes
+      const bool reached = top_p < 1.0 && run.total >= top_p;
+      const double target = P.uniform * run.total;  // the running sum at the cut: the total
+      const int first = wave_first_above(cg, run.count, target);
+      if (lane_id() == 0) {
+        sm.cut = reached ? run.count : V;
+        sm.total = run.total;
+        sm.chosen = first;
       }
     }
-    const int cut = sm.cut >= 0 ? sm.cut : V;  // no cut: the whole vocabulary is considered
-    const double target = P.uniform * sm.run;   // the running sum at the cut: the total
-    // First i < stop with target < running_i (running sums are non-decreasing).
-    int lo = 0, hi = stop - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (target < cg[mid]) hi = mid; else lo = mid + 1;
-    }
-    chosen = lo;
-    res.considered = (uint32_t)cut;
+    __syncthreads();
+    chosen = sm.chosen;
+    res.considered = (uint32_t)sm.cut;
     res.pool_exhausted = (top_p < 1.0 && pool_mass < top_p) ? 1 : 0;
   }
   const uint64_t cv = sorted[chosen];
@@ -1705,6 +1693,13 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
 // ---------------------------------------------------------------------------------------
 // Diagnostic kernel: the device exp over an array.
 // ---------------------------------------------------------------------------------------
+// Diagnostic kernel: sequential partial sums of t[0..n) by one wave (wave_seq_sum).
+__global__ __launch_bounds__(kWaveSize) void seq_sum_kernel(const double *t, int32_t n, double stop_at,
+                                                           double *out, int32_t *count) {
+  const SeqSum r = wave_seq_sum(t, n, out, stop_at);
+  if (wave_lane() == 0) *count = r.count;
+}
+
 __global__ void exp_kernel(const double *x, double *y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = fdlibm_exp(x[i]);
@@ -2020,6 +2015,16 @@ int tabby_sampler_sample(tabby_sampler *h, const void *logits_dev, int32_t dtype
     if (st == TABBY_EEMPTY) return fail(st, "sampleFromTopK: empty candidate set");
     return fail(st, "row " + std::to_string(r) + " failed with status " + std::to_string(st));
   }
+  return TABBY_OK;
+}
+
+int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double stop_at, double *prefix_dev,
+                        int32_t *count_dev, void *stream) {
+  if (!terms_dev || !prefix_dev || !count_dev) return fail(TABBY_EINVAL, "null pointer");
+  if (n < 1) return fail(TABBY_EINVAL, "n must be >= 1");
+  hipLaunchKernelGGL(seq_sum_kernel, dim3(1), dim3(kWaveSize), 0, (hipStream_t)stream, terms_dev, n,
+                     stop_at, prefix_dev, count_dev);
+  HIP_TRY(hipGetLastError());
   return TABBY_OK;
 }
 

@@ -45,6 +45,7 @@ assert PARAMS_DTYPE.itemsize == 32 and RESULT_DTYPE.itemsize == 48
 EXPORTED_SYMBOLS = (
     "tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
     "tabby_sampler_sample", "tabby_last_error", "tabby_version", "tabby_debug_exp",
+    "tabby_debug_seq_sum",
 )
 
 
@@ -75,8 +76,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     L.tabby_last_error.restype = ctypes.c_char_p
     L.tabby_version.restype = ctypes.c_char_p
     L.tabby_debug_exp.argtypes = [vp, vp, i64, vp]
+    L.tabby_debug_seq_sum.argtypes = [vp, i32, ctypes.c_double, vp, vp, vp]
     for name in ("tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
-                 "tabby_sampler_sample", "tabby_debug_exp"):
+                 "tabby_sampler_sample", "tabby_debug_exp", "tabby_debug_seq_sum"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -296,3 +298,19 @@ def device_exp(x) -> "object":
     _check(load_library().tabby_debug_exp(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()),
                                           x.numel(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
     return y
+
+
+def device_seq_sum(terms, stop_at: float = float("inf")):
+    """The device's sequential f64 partial sums of a CUDA float64 tensor (diagnostic):
+    returns (prefix sums actually written, as a CUDA tensor, count)."""
+    import torch
+    t = terms.contiguous()
+    out = torch.zeros_like(t)
+    cnt = torch.zeros(1, dtype=torch.int32, device=t.device)
+    stream = torch.cuda.current_stream()
+    _check(load_library().tabby_debug_seq_sum(ctypes.c_void_p(t.data_ptr()), int(t.numel()),
+                                              float(stop_at), ctypes.c_void_p(out.data_ptr()),
+                                              ctypes.c_void_p(cnt.data_ptr()),
+                                              ctypes.c_void_p(stream.cuda_stream)))
+    n = int(cnt.item())
+    return out[:n], n

@@ -1,0 +1,56 @@
+"""The device's parallel evaluation of left-to-right f64 sums (the sequential sums of
+sampler.ts:156-203) against numpy's sequential cumsum, bit for bit."""
+import numpy as np
+import pytest
+
+from tabby_amd import sampler as S
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(terms, stop_at=np.inf):
+    import torch
+    terms = np.ascontiguousarray(terms, dtype=np.float64)
+    prefix, n = S.device_seq_sum(torch.from_numpy(terms).cuda(), stop_at)
+    expected = np.cumsum(terms)  # numpy's cumsum is a sequential left-to-right loop
+    hits = np.nonzero(expected >= stop_at)[0]
+    want_n = int(hits[0]) + 1 if hits.size else terms.size
+    assert n == want_n, (n, want_n)
+    got = prefix.cpu().numpy()
+    bad = np.nonzero(got.view(np.uint64) != expected[:n].view(np.uint64))[0]
+    assert bad.size == 0, f"{bad.size} differ, first at {bad[0]}: {got[bad[0]]!r} vs {expected[bad[0]]!r}"
+
+
+@pytest.mark.parametrize("n", [1, 2, 15, 16, 17, 63, 64, 65, 1023, 1024, 1025, 4097, 20000])
+def test_sorted_exponential_terms(n):
+    rng = np.random.default_rng(n)
+    l = np.sort(rng.normal(0, 3, n))[::-1]
+    _check(np.exp((l - l[0]) / 0.7))
+
+
+def test_many_binade_crossings_and_flat_terms():
+    _check(np.ones(5000))                  # integer sums: a crossing at every power of two
+    _check(np.full(3000, 1.0 / 3.0))
+    _check(np.linspace(1.0, 1e-3, 7000))
+
+
+def test_exact_half_ulp_ties_round_to_even():
+    # 1 + 2^-53 is a tie (stays 1), then terms that make odd and even sums alternate.
+    t = [1.0] + [2.0 ** -53] * 40 + [2.0 ** -52] + [2.0 ** -53] * 40 + [3 * 2.0 ** -53] * 30
+    _check(np.array(t))
+    rng = np.random.default_rng(7)
+    base = np.ldexp(1.0, -rng.integers(40, 56, 3000).astype(np.int64))
+    _check(np.concatenate([[0.75], np.sort(base)[::-1]]))
+
+
+def test_tiny_and_zero_terms():
+    _check(np.concatenate([[1.0], np.full(100, 1e-300), np.zeros(200), [5e-324] * 10]))
+
+
+@pytest.mark.parametrize("stop", [0.5, 0.9, 0.95, 0.999999, 1.0])
+def test_stop_at_threshold(stop):
+    rng = np.random.default_rng(11)
+    l = np.sort(rng.normal(0, 1, 3000))[::-1]
+    s = np.exp(l - l[0])
+    w = s / s.sum()
+    _check(w, stop)
