@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "wave_ops.h"
+
 namespace tabby {
 
 constexpr int kBlock = 256;
@@ -171,6 +173,50 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t *a, int n) {
       }
       __syncthreads();
     }
+  }
+}
+
+// In-place descending sort of a[0..n) in LDS, n a power of two, by the whole workgroup:
+// each wave sorts 256-entry chunks in registers (the network's stages below 256 need no
+// barrier), and only the strides of 256 and above go through LDS with a barrier each.
+__device__ __forceinline__ void block_sort_desc(uint64_t *a, int n) {
+  constexpr int R = 4, kChunkN = kWaveSize * R;  // 256 entries per wave pass
+  if (n < kChunkN) {
+    bitonic_sort_desc(a, n);
+    return;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  auto chunk_pass = [&](int size, bool full) {
+    for (int base = wave * kChunkN; base < n; base += kWaves * kChunkN) {
+      uint64_t v[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[r] = a[base + r * kWaveSize + lane];
+      if (full) {
+        for (int sz = 2; sz <= kChunkN; sz <<= 1) wave_bitonic_stages<R>(v, base, sz);
+      } else {
+        wave_bitonic_stages<R>(v, base, size);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) a[base + r * kWaveSize + lane] = v[r];
+    }
+    __syncthreads();
+  };
+  chunk_pass(0, true);
+  for (int size = 2 * kChunkN; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride >= kChunkN; stride >>= 1) {
+      for (int i = threadIdx.x; i < (n >> 1); i += kBlock) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t x = a[lo], y = a[hi];
+        if ((x < y) == desc) {
+          a[lo] = y;
+          a[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+    chunk_pass(size, false);
   }
 }
 

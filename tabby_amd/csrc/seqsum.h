@@ -154,6 +154,104 @@ __device__ __forceinline__ SeqSum wave_seq_sum(const double *t, int n, double *o
   return {P, n};
 }
 
+// The same sum for long sequences in global memory: each lane takes 16 consecutive terms
+// (one 128-byte line) per step, so a step covers 1024 terms; an event restarts the step
+// after the event term. Same contract as wave_seq_sum.
+__device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, double *out, double stop_at) {
+  constexpr int kPer = 16, kStep = kWaveSize * kPer;
+  if (n <= kSeqShort) return lane_seq_sum(t, n, out, stop_at);
+  const int lane = wave_lane();
+  double P = t[0];
+  if (out && lane == 0) out[0] = P;
+  if (P >= stop_at) return {P, 1};
+  int a = 1;
+  while (a < n) {
+    const int E = ((int)((uint64_t)__double_as_longlong(P) >> 52) & 0x7ff) - 1023;
+    const double u = __longlong_as_double((long long)((uint64_t)(E - 52 + 1023) << 52));
+    const double scale = __longlong_as_double((long long)((uint64_t)(52 - E + 1023) << 52));
+    const double m = P * scale;
+    const int first = a + lane * kPer;
+    double tv[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) tv[i] = first + i < n ? t[first + i] : 0.0;
+    double pre[kPer];
+    uint32_t tie_bits = 0;
+    double run = 0.0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const double q = tv[i] * scale;
+      const double r = __builtin_rint(q);
+      if (q < kTwo52 && q - __builtin_floor(q) == 0.5) tie_bits |= 1u << i;
+      run += r;
+      pre[i] = run;
+    }
+    const double incl = wave_inclusive_scan(run);
+    // Exclusive prefix: the inclusive scan of the lane below (exact while below 2^53, and
+    // >= 2^53 otherwise, which only matters past an event) -- a one-lane shift within each
+    // 16-lane row, with the row starts filled from the last lane of the row below.
+    double below = row_shift_up<1>(incl);
+    const double i15 = lane_f64(incl, 15), i31 = lane_f64(incl, 31), i47 = lane_f64(incl, 47);
+    if (lane == 16) below = i15;
+    if (lane == 32) below = i31;
+    if (lane == 48) below = i47;
+    const double base = m + below;
+    uint32_t ev_bits = tie_bits;
+    int stop_i = kPer;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const double cum = base + pre[i];
+      if (first + i < n) {
+        if (cum >= kTwo53) ev_bits |= 1u << i;
+        if (stop_i == kPer && cum * u >= stop_at) stop_i = i;
+      }
+    }
+    const int ev_i = ev_bits ? __builtin_ctz(ev_bits) : kPer;
+    const int my_first = min(ev_i, stop_i);
+    const uint64_t has = __ballot(my_first < kPer);
+    const int Lf = has ? __ffsll((unsigned long long)has) - 1 : kWaveSize;
+    const int fi = Lf < kWaveSize ? __builtin_amdgcn_readlane(my_first, Lf) : 0;
+    const int flagged = Lf < kWaveSize ? a + Lf * kPer + fi : n;
+    if (out) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int j = first + i;
+        if (j < n && j < flagged) out[j] = (base + pre[i]) * u;
+      }
+    }
+    if (flagged >= n) {
+      const int last = min(n, a + kStep) - 1;
+      const int ll = (last - a) / kPer, li = (last - a) % kPer;
+      double cum_last = 0.0;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+        if (i == li) cum_last = base + pre[i];
+      P = lane_f64(cum_last, ll) * u;
+      a = last + 1;
+      continue;
+    }
+    const bool is_stop = __builtin_amdgcn_readlane(stop_i, Lf) == fi &&
+                         !((__builtin_amdgcn_readlane((int)ev_bits, Lf) >> fi) & 1u);
+    double before_mine = 0.0, at_mine = 0.0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      if (i == fi) {
+        before_mine = i == 0 ? base : base + pre[i - 1];
+        at_mine = base + pre[i];
+      }
+    }
+    if (is_stop) {
+      const double at = lane_f64(at_mine, Lf) * u;
+      if (out && lane == 0) out[flagged] = at;
+      return {at, flagged + 1};
+    }
+    P = lane_f64(before_mine, Lf) * u + t[flagged];
+    if (out && lane == 0) out[flagged] = P;
+    if (P >= stop_at) return {P, flagged + 1};
+    a = flagged + 1;
+  }
+  return {P, n};
+}
+
 // Two independent left-to-right sums over the same length (poolMass and the scaled total):
 // short ones interleave on lane 0, long ones use the wave scan for each. The second is
 // skipped (0) when want_b is false.

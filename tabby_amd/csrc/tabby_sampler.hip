@@ -70,6 +70,9 @@ struct Workspace {
   uint64_t *head_sorted;    // [head_rows * head_stride] the head, sorted
   double *head_s;           // [head_rows * head_stride] exp((l - max)/T) in sorted order
   double *head_c;           // [head_rows * head_stride] running sums of the weights
+  uint32_t *head_plan;      // [head_rows * plan_stride] segment offsets of the sorted head
+  double *head_part;        // [head_rows * 2 * (plan_stride - 2)] per-segment exp sums
+  int32_t plan_stride;
   int64_t row_cand_stride;  // composites per row in cands
   int32_t head_stride;
 };
@@ -1158,7 +1161,7 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
   const int npow = next_pow2(keff);
   for (int i = keff + (int)threadIdx.x; i < npow; i += kBlock) sm.sorted[i] = 0ull;
   __syncthreads();
-  bitonic_sort_desc(sm.sorted, npow);
+  block_sort_desc(sm.sorted, npow);
   finish_row<KCAP, In>(sm, L, row, row_src, keff, row_max, sum_exp, P);
 }
 
@@ -1522,14 +1525,197 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
   if (count > 0) flush_head(list, count, head_count, head);
 }
 
+// The sorted head is built by two kernels. head_plan_kernel (one workgroup per row) bins the
+// head by key into 4096 buckets (bucket = (max_key - key) >> shift, so bucket order is
+// descending key order), scatters it into bucket order, and cuts the bucket sequence into
+// segments: a new segment starts at each bucket whose start offset crosses the next
+// multiple of kSegCap. head_sort_kernel (one workgroup per segment) sorts each segment in
+// place -- in LDS when it fits (at most kSegCap plus one bucket, normally), otherwise by
+// batches in descending order. The concatenation of the sorted segments is the sorted head.
+constexpr int kHeadBuckets = 4096;
+constexpr int kSegCap = 4096;
+constexpr int kSegLds = 8192;
 constexpr int kHeadBatch = 4096;
+
+// Plan layout per row: [0] = number of segment slots used (max segment index + 1),
+// [1] = head size, [2 + g] = start offset of segment g, or ~0u if no segment starts there.
+__host__ __device__ __forceinline__ int plan_slots(int vocab_max) { return vocab_max / kSegCap + 2; }
+
+struct PlanSmem {
+  BlockScratch bs;
+  uint32_t hist[kHeadBuckets];
+  uint32_t start[kHeadBuckets];
+};
+
+__global__ __launch_bounds__(kBlock) void head_plan_kernel(Launch L, Workspace W) {
+  __shared__ PlanSmem sm;
+  const int row = (int)blockIdx.x;
+  uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
+  const tabby_row_params P = L.params[row];
+  const RowState rs = W.row_state[row];
+  if (!is_head_row(P, L) || rs.status != TABBY_OK) {
+    if (threadIdx.x == 0) plan[0] = 0u;
+    return;
+  }
+  const int H = (int)W.head_count[row];
+  const uint64_t *head = W.head + (size_t)row * W.head_stride;
+  uint64_t *sorted = W.head_sorted + (size_t)row * W.head_stride;
+  const uint32_t kmax = key_of(rs.max);
+  const uint32_t range = kmax - min(rs.head_key, kmax);
+  const int bits = range == 0 ? 0 : 32 - __clz((int)range);
+  const int shift = bits > 12 ? bits - 12 : 0;
+  auto bucket_of = [&](uint64_t v) {
+    return min((kmax - min(composite_key(v), kmax)) >> shift, (uint32_t)(kHeadBuckets - 1));
+  };
+  for (int b = threadIdx.x; b < kHeadBuckets; b += kBlock) sm.hist[b] = 0u;
+  __syncthreads();
+  for (int i = threadIdx.x; i < H; i += kBlock) atomicAdd(&sm.hist[bucket_of(head[i])], 1u);
+  __syncthreads();
+  // Exclusive scan of the bucket counts: 16 buckets per thread, then across threads.
+  constexpr int kPer = kHeadBuckets / kBlock;
+  uint32_t local[kPer], run = 0;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    local[q] = run;
+    run += sm.hist[threadIdx.x * kPer + q];
+  }
+  uint32_t total;
+  const uint32_t base = block_exclusive_scan(run, sm.bs, &total);
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) sm.start[threadIdx.x * kPer + q] = base + local[q];
+  __syncthreads();
+  const int slots = min((int)((uint32_t)H / kSegCap) + 1, W.plan_stride - 2);
+  for (int g = threadIdx.x; g < slots; g += kBlock) plan[2 + g] = g == 0 ? 0u : ~0u;
+  __syncthreads();
+  // Segment starts: a bucket whose start reaches a new multiple of kSegCap.
+  for (int b = 1 + (int)threadIdx.x; b < kHeadBuckets; b += kBlock) {
+    const uint32_t st = sm.start[b];
+    const uint32_t g = st / kSegCap, gp = sm.start[b - 1] / kSegCap;
+    if (g != gp && st < (uint32_t)H && (int)g < slots) plan[2 + g] = st;
+  }
+  if (threadIdx.x == 0) {
+    plan[0] = (uint32_t)slots;
+    plan[1] = (uint32_t)H;
+  }
+  // Scatter into bucket order (unsorted within a bucket).
+  __syncthreads();
+  for (int i = threadIdx.x; i < H; i += kBlock) {
+    const uint64_t v = head[i];
+    sorted[atomicAdd(&sm.start[bucket_of(v)], 1u)] = v;
+  }
+}
+
+struct SortSmem {
+  BlockScratch bs;
+  uint32_t hist[kBins];
+  uint64_t buf[kSegLds];
+};
+
+__global__ __launch_bounds__(kBlock) void head_sort_kernel(Launch L, Workspace W) {
+  __shared__ SortSmem sm;
+  const int slots_max = W.plan_stride - 2;
+  const int row = (int)blockIdx.x / slots_max;
+  const int g = (int)blockIdx.x - row * slots_max;
+  const uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
+  const int slots = (int)plan[0];
+  if (g >= slots) return;
+  const uint32_t lo = plan[2 + g];
+  if (lo == ~0u) return;
+  const int H = (int)plan[1];
+  uint32_t hi = (uint32_t)H;
+  for (int q = g + 1; q < slots; ++q) {
+    if (plan[2 + q] != ~0u) {
+      hi = plan[2 + q];
+      break;
+    }
+  }
+  const int n = (int)(hi - lo);
+  uint64_t *seg = W.head_sorted + (size_t)row * W.head_stride + lo;
+  // Per element of the sorted segment: exp((l - M)/T) into head_s; the segment's sums of
+  // exp(l - M) and exp(l - M)/sumExp into head_part (summed in segment order later).
+  const RowState rs = W.row_state[row];
+  const double T = L.params[row].temperature;
+  double *sg = W.head_s + (size_t)row * W.head_stride + lo;
+  double *part = W.head_part + ((size_t)row * slots_max + g) * 2;
+  auto terms = [&](const uint64_t *src) {
+    double pool_part = 0.0, e_part = 0.0;
+    for (int i = threadIdx.x; i < n; i += kBlock) {
+      const double d = (double)value_of(composite_key(src[i])) - (double)rs.max;
+      const double e = fdlibm_exp(d);
+      pool_part += e / rs.sum_exp;
+      e_part += e;
+      sg[i] = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
+    }
+    const double ps = block_sum(pool_part, sm.bs);
+    const double es = block_sum(e_part, sm.bs);
+    if (threadIdx.x == 0) {
+      part[0] = ps;
+      part[1] = es;
+    }
+  };
+  if (n <= kSegLds) {
+    const int npow = next_pow2(n);
+    for (int i = threadIdx.x; i < npow; i += kBlock) sm.buf[i] = i < n ? seg[i] : 0ull;
+    __syncthreads();
+    if (n > 1) block_sort_desc(sm.buf, npow);
+    for (int i = threadIdx.x; i < n; i += kBlock) seg[i] = sm.buf[i];
+    terms(sm.buf);
+    return;
+  }
+  // Oversized segment (one bucket holds more than kSegLds entries: massive ties): batches
+  // of the kHeadBatch largest below the previous batch, read from the segment and written to
+  // the same range of the (no longer needed) unsorted head, then copied back.
+  uint64_t *out = W.head + (size_t)row * W.head_stride + lo;
+  uint64_t upper = ~0ull;
+  for (int pos = 0; pos < n;) {
+    const int b = min(kHeadBatch, n - pos);
+    if (threadIdx.x == 0) sm.bs.slot = 0u;
+    __syncthreads();
+    auto below = [&](auto &&f) {
+      constexpr int B = 8;
+      for (int base = 0; base < n; base += B * kBlock) {
+        uint64_t v[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int i = base + u * kBlock + (int)threadIdx.x;
+          v[u] = i < n ? seg[i] : ~0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+          if (v[u] < upper) f(v[u]);
+      }
+    };
+    if (n - pos > b) {
+      const SelectResult r = radix_select(below, (uint32_t)b, sm.hist, sm.bs);
+      below([&](uint64_t v) {
+        if (selected(v, r)) {
+          const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
+          if (at < (uint32_t)b) sm.buf[at] = v;
+        }
+      });
+    } else {
+      below([&](uint64_t v) {
+        const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
+        if (at < (uint32_t)b) sm.buf[at] = v;
+      });
+    }
+    const int npow = next_pow2(b);
+    for (int i = b + (int)threadIdx.x; i < npow; i += kBlock) sm.buf[i] = 0ull;
+    __syncthreads();
+    block_sort_desc(sm.buf, npow);
+    for (int i = threadIdx.x; i < b; i += kBlock) out[pos + i] = sm.buf[i];
+    upper = sm.buf[b - 1];
+    pos += b;
+    __syncthreads();
+  }
+  for (int i = threadIdx.x; i < n; i += kBlock) seg[i] = out[i];
+  terms(out);
+}
 
 struct HeadSmem {
   BlockScratch bs;
-  uint64_t batch[kHeadBatch];
-  uint32_t hist[kBins];
+  double pool, e;
   double scaled_total;
-  double total;
   int cut;
   int chosen;
 };
@@ -1558,6 +1744,8 @@ __device__ __forceinline__ int wave_first_above(const double *c, int n, double t
   return hi < n ? hi : n - 1;
 }
 
+// sampleFromTopK over the sorted head (see the comment on head_kernel): the head's terms,
+// the scaled total and the running sums (bit-exact sequential sums), the cut and the draw.
 template <typename In>
 __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace W) {
   __shared__ HeadSmem sm;
@@ -1569,70 +1757,32 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
   const int V = L.vocab;
   const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V;
   const int H = (int)W.head_count[row];
-  const uint64_t *head = W.head + (size_t)row * W.head_stride;
-  uint64_t *sorted = W.head_sorted + (size_t)row * W.head_stride;
+  const uint64_t *sorted = W.head_sorted + (size_t)row * W.head_stride;
   double *sg = W.head_s + (size_t)row * W.head_stride;
   double *cg = W.head_c + (size_t)row * W.head_stride;
   const float M = rs.max;
   const double S1 = rs.sum_exp;
   const double T = P.temperature;
 
-  // Pass 1: the head in descending batches of up to kHeadBatch; each batch is the top of
-  // what is left below the previous batch's smallest entry. Per element: exp((l - M)/T).
+  // The segments' sums, in segment order (head_sort_kernel wrote them).
+  const uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
+  const int slots_max = W.plan_stride - 2;
+  const double *part = W.head_part + (size_t)row * slots_max * 2;
   double pool_head = 0.0, e_head = 0.0;
-  uint64_t upper = ~0ull;  // exclusive; real composites are all smaller
-  for (int pos = 0; pos < H;) {
-    const int b = min(kHeadBatch, H - pos);
-    if (threadIdx.x == 0) sm.bs.slot = 0u;
-    __syncthreads();
-    auto below = [&](auto &&f) {
-      constexpr int B = 8;
-      for (int base = 0; base < H; base += B * kBlock) {
-        uint64_t v[B];
-#pragma unroll
-        for (int u = 0; u < B; ++u) {
-          const int i = base + u * kBlock + (int)threadIdx.x;
-          v[u] = i < H ? head[i] : ~0ull;
-        }
-#pragma unroll
-        for (int u = 0; u < B; ++u)
-          if (v[u] < upper) f(v[u]);
+  if (threadIdx.x == 0) {
+    const int slots = (int)plan[0];
+    for (int g = 0; g < slots; ++g) {
+      if (plan[2 + g] != ~0u) {
+        pool_head += part[2 * g];
+        e_head += part[2 * g + 1];
       }
-    };
-    if (H - pos > b) {
-      const SelectResult r = radix_select(below, (uint32_t)b, sm.hist, sm.bs);
-      below([&](uint64_t v) {
-        if (selected(v, r)) {
-          const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
-          if (at < (uint32_t)b) sm.batch[at] = v;
-        }
-      });
-    } else {
-      below([&](uint64_t v) {
-        const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
-        if (at < (uint32_t)b) sm.batch[at] = v;
-      });
     }
-    const int npow = next_pow2(b);
-    for (int i = b + (int)threadIdx.x; i < npow; i += kBlock) sm.batch[i] = 0ull;
-    __syncthreads();
-    bitonic_sort_desc(sm.batch, npow);
-    double pool_part = 0.0, e_part = 0.0;
-    for (int i = threadIdx.x; i < b; i += kBlock) {
-      const uint64_t v = sm.batch[i];
-      const double d = (double)value_of(composite_key(v)) - (double)M;
-      const double e = fdlibm_exp(d);
-      pool_part += e / S1;
-      e_part += e;
-      sorted[pos + i] = v;
-      sg[pos + i] = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
-    }
-    pool_head += block_sum(pool_part, sm.bs);
-    e_head += block_sum(e_part, sm.bs);
-    upper = sm.batch[b - 1];
-    pos += b;
-    __syncthreads();
+    sm.pool = pool_head;
+    sm.e = e_head;
   }
+  __syncthreads();
+  pool_head = sm.pool;
+  e_head = sm.e;
   // poolMass: the head's exact terms plus the mass of everything below the head.
   const double pool_mass = pool_head + fmax(0.0, S1 - e_head) / S1;
 
@@ -1649,7 +1799,7 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
   } else {
     // The scaled total over the sorted head (bit-exact sequential sum, wave 0).
     if (wave_id() == 0) {
-      const double S = wave_seq_sum(sg, H, nullptr, INFINITY).total;
+      const double S = wave_seq_sum_wide(sg, H, nullptr, INFINITY).total;
       if (lane_id() == 0) sm.scaled_total = S;
     }
     __syncthreads();
@@ -1660,14 +1810,13 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
     // cut the whole vocabulary is considered.
     const double top_p = P.top_p;
     if (wave_id() == 0) {
-      const SeqSum run = wave_seq_sum(cg, H, cg, top_p < 1.0 ? top_p : INFINITY);
+      const SeqSum run = wave_seq_sum_wide(cg, H, cg, top_p < 1.0 ? top_p : INFINITY);
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");  // the sums are read by other lanes
       const bool reached = top_p < 1.0 && run.total >= top_p;
       const double target = P.uniform * run.total;  // the running sum at the cut: the total
       const int first = wave_first_above(cg, run.count, target);
       if (lane_id() == 0) {
         sm.cut = reached ? run.count : V;
-        sm.total = run.total;
         sm.chosen = first;
       }
     }
@@ -1695,8 +1844,8 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
 // ---------------------------------------------------------------------------------------
 // Diagnostic kernel: sequential partial sums of t[0..n) by one wave (wave_seq_sum).
 __global__ __launch_bounds__(kWaveSize) void seq_sum_kernel(const double *t, int32_t n, double stop_at,
-                                                           double *out, int32_t *count) {
-  const SeqSum r = wave_seq_sum(t, n, out, stop_at);
+                                                           double *out, int32_t *count, int32_t wide) {
+  const SeqSum r = wide ? wave_seq_sum_wide(t, n, out, stop_at) : wave_seq_sum(t, n, out, stop_at);
   if (wave_lane() == 0) *count = r.count;
 }
 
@@ -1792,6 +1941,9 @@ hipError_t launch_pair(const Launch &L, const Workspace &W, hipStream_t stream) 
 template <typename In, int VEC>
 hipError_t launch_head(const Launch &L, const Workspace &W, hipStream_t stream) {
   hipLaunchKernelGGL((head_kernel<In, VEC>), dim3((unsigned)(L.rows * L.h_splits)), dim3(kWaveSize), 0,
+                     stream, L, W);
+  hipLaunchKernelGGL(head_plan_kernel, dim3((unsigned)L.rows), dim3(kBlock), 0, stream, L, W);
+  hipLaunchKernelGGL(head_sort_kernel, dim3((unsigned)(L.rows * (W.plan_stride - 2))), dim3(kBlock), 0,
                      stream, L, W);
   hipLaunchKernelGGL((head_finish_kernel<In>), dim3((unsigned)L.rows), dim3(kBlock), 0, stream, L, W);
   return hipGetLastError();
@@ -1924,8 +2076,13 @@ int tabby_sampler_sample_device(tabby_sampler *h, const void *logits_dev, int32_
         h->head_rows_cap = 0;
       }
       const size_t per = (size_t)rows * (size_t)h->vocab_max;
-      HIP_TRY(hipMalloc(&h->head_base, per * 32));
+      const int plan_stride = plan_slots(h->vocab_max) + 2;
+      const size_t plan_bytes = ((size_t)rows * plan_stride * 4 + 255) & ~(size_t)255;
+      HIP_TRY(hipMalloc(&h->head_base, per * 32 + plan_bytes + (size_t)rows * (plan_stride - 2) * 16));
       char *b = (char *)h->head_base;
+      h->ws.head_plan = (uint32_t *)(b + per * 32);
+      h->ws.head_part = (double *)(b + per * 32 + plan_bytes);
+      h->ws.plan_stride = plan_stride;
       h->ws.head = (uint64_t *)b;
       h->ws.head_sorted = (uint64_t *)(b + per * 8);
       h->ws.head_s = (double *)(b + per * 16);
@@ -2019,11 +2176,11 @@ int tabby_sampler_sample(tabby_sampler *h, const void *logits_dev, int32_t dtype
 }
 
 int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double stop_at, double *prefix_dev,
-                        int32_t *count_dev, void *stream) {
+                        int32_t *count_dev, int32_t wide, void *stream) {
   if (!terms_dev || !prefix_dev || !count_dev) return fail(TABBY_EINVAL, "null pointer");
   if (n < 1) return fail(TABBY_EINVAL, "n must be >= 1");
   hipLaunchKernelGGL(seq_sum_kernel, dim3(1), dim3(kWaveSize), 0, (hipStream_t)stream, terms_dev, n,
-                     stop_at, prefix_dev, count_dev);
+                     stop_at, prefix_dev, count_dev, wide);
   HIP_TRY(hipGetLastError());
   return TABBY_OK;
 }

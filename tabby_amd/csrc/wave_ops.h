@@ -95,6 +95,41 @@ __device__ __forceinline__ T tmax(T a, T b) { return a > b ? a : b; }
 template <typename T>
 __device__ __forceinline__ T tmin(T a, T b) { return a < b ? a : b; }
 
+// The bitonic network's stages for one `size` over strides below 64*R, on the 64*R values
+// v[r] at global indices base + r*64 + lane (base a multiple of 64*R); the direction of each
+// pair is descending where (index & size) == 0, as in a descending sort of the whole array.
+template <int R, typename T>
+__device__ __forceinline__ void wave_bitonic_stages(T (&v)[R], int base, int size) {
+  const int lane = wave_lane();
+  const int top = min(size >> 1, kWaveSize * R / 2);
+#pragma unroll
+  for (int stride = kWaveSize * R / 2; stride > 0; stride >>= 1) {
+    if (stride > top) continue;
+    if (stride >= kWaveSize) {
+      const int rs = stride / kWaveSize;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if ((r & rs) == 0) {
+          const int r2 = r | rs;
+          const bool desc = ((base + r * kWaveSize + lane) & size) == 0;
+          const T a = v[r], b = v[r2];
+          const bool swap = desc ? (a < b) : (a > b);
+          v[r] = swap ? b : a;
+          v[r2] = swap ? a : b;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const T o = xor_lane_by(v[r], stride);
+        const bool lower = (lane & stride) == 0;
+        const bool desc = ((base + r * kWaveSize + lane) & size) == 0;
+        v[r] = (lower == desc) ? tmax(v[r], o) : tmin(v[r], o);
+      }
+    }
+  }
+}
+
 // Descending bitonic sort of the 64*R values v[r] (element index r*64 + lane).
 template <int R, typename T>
 __device__ __forceinline__ void wave_sort_desc(T (&v)[R]) {

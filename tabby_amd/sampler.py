@@ -76,7 +76,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     L.tabby_last_error.restype = ctypes.c_char_p
     L.tabby_version.restype = ctypes.c_char_p
     L.tabby_debug_exp.argtypes = [vp, vp, i64, vp]
-    L.tabby_debug_seq_sum.argtypes = [vp, i32, ctypes.c_double, vp, vp, vp]
+    L.tabby_debug_seq_sum.argtypes = [vp, i32, ctypes.c_double, vp, vp, i32, vp]
     for name in ("tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
                  "tabby_sampler_sample", "tabby_debug_exp", "tabby_debug_seq_sum"):
         getattr(L, name).restype = ctypes.c_int
@@ -300,9 +300,10 @@ def device_exp(x) -> "object":
     return y
 
 
-def device_seq_sum(terms, stop_at: float = float("inf")):
+def device_seq_sum(terms, stop_at: float = float("inf"), wide: bool = False):
     """The device's sequential f64 partial sums of a CUDA float64 tensor (diagnostic):
-    returns (prefix sums actually written, as a CUDA tensor, count)."""
+    returns (prefix sums actually written, as a CUDA tensor, count). ``wide`` selects the
+    16-terms-per-lane form used for long sums in global memory."""
     import torch
     t = terms.contiguous()
     out = torch.zeros_like(t)
@@ -310,7 +311,7 @@ def device_seq_sum(terms, stop_at: float = float("inf")):
     stream = torch.cuda.current_stream()
     _check(load_library().tabby_debug_seq_sum(ctypes.c_void_p(t.data_ptr()), int(t.numel()),
                                               float(stop_at), ctypes.c_void_p(out.data_ptr()),
-                                              ctypes.c_void_p(cnt.data_ptr()),
+                                              ctypes.c_void_p(cnt.data_ptr()), int(wide),
                                               ctypes.c_void_p(stream.cuda_stream)))
     n = int(cnt.item())
     return out[:n], n

@@ -8,10 +8,15 @@ from tabby_amd import sampler as S
 pytestmark = pytest.mark.gpu
 
 
-def _check(terms, stop_at=np.inf):
+@pytest.fixture(params=[False, True], ids=["lds", "wide"])
+def wide(request):
+    return request.param
+
+
+def _check(terms, stop_at=np.inf, wide=False):
     import torch
     terms = np.ascontiguousarray(terms, dtype=np.float64)
-    prefix, n = S.device_seq_sum(torch.from_numpy(terms).cuda(), stop_at)
+    prefix, n = S.device_seq_sum(torch.from_numpy(terms).cuda(), stop_at, wide)
     expected = np.cumsum(terms)  # numpy's cumsum is a sequential left-to-right loop
     hits = np.nonzero(expected >= stop_at)[0]
     want_n = int(hits[0]) + 1 if hits.size else terms.size
@@ -22,35 +27,35 @@ def _check(terms, stop_at=np.inf):
 
 
 @pytest.mark.parametrize("n", [1, 2, 15, 16, 17, 63, 64, 65, 1023, 1024, 1025, 4097, 20000])
-def test_sorted_exponential_terms(n):
+def test_sorted_exponential_terms(n, wide):
     rng = np.random.default_rng(n)
     l = np.sort(rng.normal(0, 3, n))[::-1]
-    _check(np.exp((l - l[0]) / 0.7))
+    _check(np.exp((l - l[0]) / 0.7), wide=wide)
 
 
-def test_many_binade_crossings_and_flat_terms():
-    _check(np.ones(5000))                  # integer sums: a crossing at every power of two
-    _check(np.full(3000, 1.0 / 3.0))
-    _check(np.linspace(1.0, 1e-3, 7000))
+def test_many_binade_crossings_and_flat_terms(wide):
+    _check(np.ones(5000), wide=wide)                  # integer sums: a crossing at every power of two
+    _check(np.full(3000, 1.0 / 3.0), wide=wide)
+    _check(np.linspace(1.0, 1e-3, 7000), wide=wide)
 
 
-def test_exact_half_ulp_ties_round_to_even():
+def test_exact_half_ulp_ties_round_to_even(wide):
     # 1 + 2^-53 is a tie (stays 1), then terms that make odd and even sums alternate.
     t = [1.0] + [2.0 ** -53] * 40 + [2.0 ** -52] + [2.0 ** -53] * 40 + [3 * 2.0 ** -53] * 30
-    _check(np.array(t))
+    _check(np.array(t), wide=wide)
     rng = np.random.default_rng(7)
     base = np.ldexp(1.0, -rng.integers(40, 56, 3000).astype(np.int64))
-    _check(np.concatenate([[0.75], np.sort(base)[::-1]]))
+    _check(np.concatenate([[0.75], np.sort(base)[::-1]]), wide=wide)
 
 
-def test_tiny_and_zero_terms():
-    _check(np.concatenate([[1.0], np.full(100, 1e-300), np.zeros(200), [5e-324] * 10]))
+def test_tiny_and_zero_terms(wide):
+    _check(np.concatenate([[1.0], np.full(100, 1e-300), np.zeros(200), [5e-324] * 10]), wide=wide)
 
 
 @pytest.mark.parametrize("stop", [0.5, 0.9, 0.95, 0.999999, 1.0])
-def test_stop_at_threshold(stop):
+def test_stop_at_threshold(stop, wide):
     rng = np.random.default_rng(11)
     l = np.sort(rng.normal(0, 1, 3000))[::-1]
     s = np.exp(l - l[0])
     w = s / s.sum()
-    _check(w, stop)
+    _check(w, stop, wide)
