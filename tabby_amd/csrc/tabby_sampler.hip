@@ -1533,7 +1533,7 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
 // place -- in LDS when it fits (at most kSegCap plus one bucket, normally), otherwise by
 // batches in descending order. The concatenation of the sorted segments is the sorted head.
 constexpr int kHeadBuckets = 4096;
-constexpr int kSegCap = 4096;
+constexpr int kSegCap = 1024;
 constexpr int kSegLds = 8192;
 constexpr int kHeadBatch = 4096;
 
