@@ -72,33 +72,39 @@ struct SeqSum {
   int count;     // terms added (the sum stopped early if count < n)
 };
 
-// Short sums: lane 0 adds left to right, eight loads ahead of the adds.
-__device__ __forceinline__ SeqSum lane_seq_sum(const double *t, int n, double *out, double stop_at) {
-  double P = 0.0;
-  int count = n;
-  if (wave_lane() == 0) {
-    P = t[0];
-    if (out) out[0] = P;
-    if (P >= stop_at) count = 1;
-    for (int b = 1; b < n && count == n; b += 8) {
-      double v[8];
+// Short sums: every lane adds the same terms left to right (broadcast LDS reads, eight ahead
+// of the adds), so the loop is uniform scalar control flow with no per-lane branching; lane
+// 0 alone writes the partial sums. kStop: stop at the first partial sum >= stop_at.
+template <bool kOut, bool kStop>
+__device__ __forceinline__ SeqSum uniform_seq_sum(const double *t, int n, double *out, double stop_at) {
+  const bool writer = wave_lane() == 0;
+  double P = t[0];
+  if (kOut && writer) out[0] = P;
+  if (kStop && __ballot(P >= stop_at)) return {P, 1};
+  int i = 1;
+  for (; i + 8 <= n; i += 8) {
+    double v[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = b + q < n ? t[b + q] : 0.0;
+    for (int q = 0; q < 8; ++q) v[q] = t[i + q];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        if (b + q < n && count == n) {
-          P += v[q];
-          if (out) out[b + q] = P;
-          if (P >= stop_at) count = b + q + 1;
-        }
-      }
+    for (int q = 0; q < 8; ++q) {
+      P += v[q];
+      if (kOut && writer) out[i + q] = P;
+      if (kStop && __ballot(P >= stop_at)) return {P, i + q + 1};
     }
   }
-  const uint64_t bits = (uint64_t)__double_as_longlong(P);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bits);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bits >> 32));
-  return {__longlong_as_double((long long)(((uint64_t)hi << 32) | lo)),
-          __builtin_amdgcn_readfirstlane(count)};
+  for (; i < n; ++i) {
+    P += t[i];
+    if (kOut && writer) out[i] = P;
+    if (kStop && __ballot(P >= stop_at)) return {P, i + 1};
+  }
+  return {P, n};
+}
+
+__device__ __forceinline__ SeqSum lane_seq_sum(const double *t, int n, double *out, double stop_at) {
+  const bool stop = stop_at < INFINITY;
+  if (out) return stop ? uniform_seq_sum<true, true>(t, n, out, stop_at) : uniform_seq_sum<true, false>(t, n, out, stop_at);
+  return stop ? uniform_seq_sum<false, true>(t, n, out, stop_at) : uniform_seq_sum<false, false>(t, n, out, stop_at);
 }
 
 // Adds t[0..n) left to right (n >= 1, every t_j >= 0, t[0] > 0, and every partial sum at
@@ -262,25 +268,25 @@ __device__ __forceinline__ void wave_seq_sum2(const double *a, const double *b, 
     *sum_b = want_b ? wave_seq_sum(b, n, nullptr, INFINITY).total : 0.0;
     return;
   }
-  double pa = 0.0, pb = 0.0;
-  if (wave_lane() == 0) {
-    pa = a[0];
-    pb = b[0];
-    for (int base = 1; base < n; base += 8) {
-      double va[8], vb[8];
+  // Both chains on every lane, interleaved (uniform control flow, see uniform_seq_sum).
+  double pa = a[0], pb = b[0];
+  int i = 1;
+  for (; i + 8 <= n; i += 8) {
+    double va[8], vb[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        va[q] = base + q < n ? a[base + q] : 0.0;
-        vb[q] = base + q < n ? b[base + q] : 0.0;
-      }
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        if (base + q < n) {
-          pa += va[q];
-          pb += vb[q];
-        }
-      }
+    for (int q = 0; q < 8; ++q) {
+      va[q] = a[i + q];
+      vb[q] = b[i + q];
     }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      pa += va[q];
+      pb += vb[q];
+    }
+  }
+  for (; i < n; ++i) {
+    pa += a[i];
+    pb += b[i];
   }
   auto bcast = [](double v) {
     const uint64_t bits = (uint64_t)__double_as_longlong(v);

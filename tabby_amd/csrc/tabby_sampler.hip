@@ -1179,6 +1179,8 @@ struct WaveMergeSmem {
   double a[kWaveKcap];  // exact terms exp(l - max) / sumExp
   double b[kWaveKcap];  // exp((l - max) / T), then the weights
   double c[kWaveKcap];  // running sums of the weights
+  uint64_t part[kWaves][kWaveKcap];  // each wave's merged lists
+  double pool, scaled;               // poolMass and the scaled total
 };
 
 // Bitonic clean of 64*R values (index r*64 + lane) into descending order.
@@ -1254,16 +1256,17 @@ __device__ __forceinline__ int list_count(const RowStats &rs, int s) {
   return q == 1 ? c1 : q == 2 ? c2 : c3;
 }
 
-// Merges the row's sorted slice lists into the top 64*R composites, sorted descending, in
-// registers. Slice s's list starts at base + s*slice_len and holds rs.cnt(s) entries; reads
-// stay inside the row's `row_stride` entries and past a list's end are masked.
+// Merges the sorted slice lists s_begin..s_end-1 of a row into the top 64*R composites,
+// sorted descending, in registers (all zero without lists). Slice s's list starts at
+// base + s*slice_len and holds count_of(s) entries; reads stay inside the row's row_stride
+// entries, and entries past a list's end are masked.
 template <int R>
 struct ListMerger {
   static constexpr int kBatch = 4;  // lists whose loads are in flight together
   const uint64_t *base;
   int slice_len;
   int64_t row_stride;
-  int splits;
+  int s_begin, s_end;
   uint64_t acc[R];
   uint64_t raw[kBatch][R];
 
@@ -1287,23 +1290,29 @@ struct ListMerger {
   }
   // Issues the first lists' loads (nothing is waited for).
   __device__ __forceinline__ void start() {
-    issue(0, acc, false);
+    if (s_begin < s_end) issue(s_begin, acc, false);
 #pragma unroll
     for (int q = 0; q < kBatch; ++q)
-      if (1 + q < splits) issue(1 + q, raw[q], true);
+      if (s_begin + 1 + q < s_end) issue(s_begin + 1 + q, raw[q], true);
   }
-  __device__ __forceinline__ void finish(const RowStats &rs) {
-    mask(list_count(rs, 0), acc, false);
-    for (int s0 = 1; s0 < splits; s0 += kBatch) {
+  template <class CountOf>
+  __device__ __forceinline__ void finish(CountOf count_of) {
+    if (s_begin >= s_end) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0ull;
+      return;
+    }
+    mask(count_of(s_begin), acc, false);
+    for (int s0 = s_begin + 1; s0 < s_end; s0 += kBatch) {
 #pragma unroll
       for (int q = 0; q < kBatch; ++q) {
         const int s = s0 + q;
-        if (s < splits) {
+        if (s < s_end) {
           uint64_t b[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) b[r] = raw[q][r];
-          if (s + kBatch < splits) issue(s + kBatch, raw[q], true);
-          mask(list_count(rs, s), b, true);
+          if (s + kBatch < s_end) issue(s + kBatch, raw[q], true);
+          mask(count_of(s), b, true);
 #pragma unroll
           for (int r = 0; r < R; ++r) acc[r] = tmax(acc[r], b[r]);
           bitonic_clean_desc<R>(acc);
@@ -1312,6 +1321,14 @@ struct ListMerger {
     }
   }
 };
+
+// acc <- the top 64*R of acc and the sorted list `other` (64*R entries, in LDS), sorted.
+template <int R>
+__device__ __forceinline__ void merge_with(uint64_t (&acc)[R], const uint64_t *other) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = tmax(acc[r], other[kWaveSize * R - 1 - (r * kWaveSize + wave_lane())]);
+  bitonic_clean_desc<R>(acc);
+}
 
 // sampleFromTopK (src/engine/sampler.ts:147-212) over sm.sorted[0..K), K >= 1, in the
 // reference's order of f64 operations. Per-element terms are computed by all lanes; the
@@ -1323,15 +1340,7 @@ __device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch
                                           const tabby_row_params &P) {
   const int lane = wave_lane();
   const double T = P.temperature;
-  const double M = (double)max_logit;
-  for (int i = lane; i < K; i += kWaveSize) {
-    const double d = (double)value_of(composite_key(sm.sorted[i])) - M;
-    sm.a[i] = fdlibm_exp_inline(d) / sum_exp;
-    sm.b[i] = T > 0.0 ? fdlibm_exp_inline(d / T) : 0.0;
-  }
-  wave_lds_sync();
-  double pool, scaled;
-  wave_seq_sum2(sm.a, sm.b, K, T > 0.0, &pool, &scaled);
+  const double pool = sm.pool, scaled = sm.scaled;
   tabby_row_result res;
   res.max_logit = max_logit;
   res.sum_exp = sum_exp;
@@ -1378,52 +1387,107 @@ __device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch
   }
 }
 
-// Loads and merges the lists (R registers per lane), with the statistics math done while the
-// first lists are in flight; writes the merged top K to sm.sorted. Returns the row stats.
+// The four waves of the workgroup each merge a quarter of the row's lists (their loads
+// issued by the caller); then a two-level tree through LDS merges the four results into
+// sm.sorted[0..K).
+template <int R, class CountOf>
+__device__ __forceinline__ void merge_lists_4(WaveMergeSmem &sm, ListMerger<R> &mg, CountOf count_of,
+                                              int K) {
+  const int w = wave_id(), lane = wave_lane();
+  mg.finish(count_of);
+#pragma unroll
+  for (int r = 0; r < R; ++r) sm.part[w][r * kWaveSize + lane] = mg.acc[r];
+  __syncthreads();
+  if (w == 0 || w == 2) {
+    merge_with<R>(mg.acc, sm.part[w + 1]);
+    if (w == 2) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) sm.part[2][r * kWaveSize + lane] = mg.acc[r];
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    merge_with<R>(mg.acc, sm.part[2]);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (r * kWaveSize + lane < K) sm.sorted[r * kWaveSize + lane] = mg.acc[r];
+  }
+  __syncthreads();
+}
+
 template <int R>
-__device__ __forceinline__ RowStats merge_row(WaveMergeSmem &sm, const SliceStat *stats,
-                                              const uint64_t *lists, const Launch &L,
-                                              const Workspace &W, int K) {
+__device__ __forceinline__ ListMerger<R> lists_of_wave(const uint64_t *lists, const Launch &L,
+                                                       const Workspace &W) {
+  const int per = (L.splits + kWaves - 1) / kWaves;
   ListMerger<R> mg;
   mg.base = lists;
   mg.slice_len = L.slice_len;
   mg.row_stride = W.row_cand_stride;
-  mg.splits = L.splits;
-  mg.start();
-  const RowStats rs = row_stats(stats, L.splits);
-  mg.finish(rs);
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-    if (r * kWaveSize + wave_lane() < K) sm.sorted[r * kWaveSize + wave_lane()] = mg.acc[r];
-  wave_lds_sync();
-  return rs;
+  mg.s_begin = min(wave_id() * per, L.splits);
+  mg.s_end = min(mg.s_begin + per, L.splits);
+  return mg;
 }
 
 template <typename In>
-__global__ __launch_bounds__(kWaveSize) void wave_merge_kernel(Launch L, Workspace W) {
+__global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace W) {
   __shared__ WaveMergeSmem sm;
   const int row = (int)blockIdx.x;
   const int lane = wave_lane();
   const int V = L.vocab;
+  const SliceStat *stats = W.stats + (size_t)row * kMaxSplits;
+  const uint64_t *lists = W.cands + (size_t)row * W.row_cand_stride;
+  // The lists' first 64 entries are loaded before the parameters are known: pools of at
+  // most 64 (the common case) then need no second round trip.
+  ListMerger<1> m1 = lists_of_wave<1>(lists, L, W);
+  m1.start();
   const tabby_row_params P = L.params[row];
+  const RowStats rs = row_stats(stats, L.splits);
+  auto count_of = [&](int s) { return list_count(rs, s); };
   const bool valid_params = params_valid(P, L.k_max);
   const int keff = effective_k(P, V);
   const bool finite = valid_params && keff <= L.kcap;
   const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V;
   // Pool to merge: the row's top-k, or for a whole-vocabulary row the caller's top-k list.
   const int K = !valid_params ? 0 : finite ? keff : L.head_pass ? min(L.topk_cap, V) : 0;
-  const SliceStat *stats = W.stats + (size_t)row * kMaxSplits;
-  const uint64_t *lists = W.cands + (size_t)row * W.row_cand_stride;
-
-  RowStats rs;
-  if (K <= 0) rs = row_stats(stats, L.splits);
-  else if (K <= kWaveSize) rs = merge_row<1>(sm, stats, lists, L, W, K);
-  else if (K <= 2 * kWaveSize) rs = merge_row<2>(sm, stats, lists, L, W, K);
-  else rs = merge_row<4>(sm, stats, lists, L, W, K);
+  if (K > 0) {
+    if (K <= kWaveSize) {
+      merge_lists_4<1>(sm, m1, count_of, K);
+    } else if (K <= 2 * kWaveSize) {
+      ListMerger<2> m2 = lists_of_wave<2>(lists, L, W);
+      m2.start();
+      merge_lists_4<2>(sm, m2, count_of, K);
+    } else {
+      ListMerger<4> m4 = lists_of_wave<4>(lists, L, W);
+      m4.start();
+      merge_lists_4<4>(sm, m4, count_of, K);
+    }
+  }
   const float row_max = rs.max;
   const double sum_exp = rs.sum_exp;
   const bool in_domain = (row_max > -INFINITY) && (row_max < INFINITY) && (sum_exp > 0.0) &&
                          (sum_exp < INFINITY);
+  if (valid_params && in_domain && finite) {
+    // sampleFromTopK's two independent passes over the pool (sampler.ts:156-157, 170-172)
+    // on two waves: wave 0 the exact terms and poolMass, wave 1 the scaled terms and their
+    // total, each a left-to-right sum.
+    const int w = wave_id();
+    const double M = (double)row_max, T = P.temperature;
+    if (w == 0) {
+      for (int i = lane; i < K; i += kWaveSize)
+        sm.a[i] = fdlibm_exp_inline((double)value_of(composite_key(sm.sorted[i])) - M) / sum_exp;
+      wave_lds_sync();
+      const double pool = wave_seq_sum(sm.a, K, nullptr, INFINITY).total;
+      if (lane == 0) sm.pool = pool;
+    } else if (w == 1) {
+      for (int i = lane; i < K; i += kWaveSize)
+        sm.b[i] = T > 0.0 ? fdlibm_exp_inline(((double)value_of(composite_key(sm.sorted[i])) - M) / T) : 0.0;
+      wave_lds_sync();
+      const double scaled = T > 0.0 ? wave_seq_sum(sm.b, K, nullptr, INFINITY).total : 0.0;
+      if (lane == 0) sm.scaled = scaled;
+    }
+    __syncthreads();
+  }
+  if (wave_id() != 0) return;
   if (!valid_params || !in_domain || (!finite && !L.head_pass)) {
     const int32_t status = !valid_params ? TABBY_EINVAL : !in_domain ? TABBY_EDOMAIN : TABBY_EINVAL;
     if (lane == 0) {
@@ -1930,7 +1994,7 @@ hipError_t launch_pair(const Launch &L, const Workspace &W, hipStream_t stream) 
   const dim3 slices((unsigned)(L.rows * L.splits)), rows((unsigned)L.rows);
   if (L.kcap <= kWaveKcap) {
     hipLaunchKernelGGL((wave_kernel<In, VEC>), slices, dim3(kWaveSize), 0, stream, L, W);
-    hipLaunchKernelGGL((wave_merge_kernel<In>), rows, dim3(kWaveSize), 0, stream, L, W);
+    hipLaunchKernelGGL((wave_merge_kernel<In>), rows, dim3(kBlock), 0, stream, L, W);
   } else {
     hipLaunchKernelGGL((slice_kernel<In, VEC>), slices, dim3(kBlock), 0, stream, L, W);
     hipLaunchKernelGGL((merge_kernel<kKcapLarge, In>), rows, dim3(kBlock), 0, stream, L, W);
