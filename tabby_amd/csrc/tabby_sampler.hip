@@ -1331,9 +1331,10 @@ __device__ __forceinline__ void merge_with(uint64_t (&acc)[R], const uint64_t *o
 }
 
 // sampleFromTopK (src/engine/sampler.ts:147-212) over sm.sorted[0..K), K >= 1, in the
-// reference's order of f64 operations. Per-element terms are computed by all lanes; the
-// sums (poolMass, the scaled total, the running sums of the draw, which are the top-p
-// cumulative sums) are sequential left-to-right sums on lane 0.
+// reference's order of f64 operations. The caller has left the terms exp(x - max)/sum_exp in
+// sm.a with their sum in sm.pool (poolMass) and the weights exp(x/T) in sm.b with their sum
+// in sm.scaled. The running sums of the normalised weights (the top-p cumulative sums) are
+// left-to-right sums evaluated bit-exactly by the whole wave (wave_seq_sum).
 template <typename In>
 __device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch &L, int row,
                                           const In *row_src, float max_logit, double sum_exp,
@@ -1969,18 +1970,23 @@ struct Plan {
 // Enough slices per row that the batch fills the chip about once: 256 CUs x 5 resident
 // 256-lane workgroups, or x 12 one-wave workgroups for the wave kernel (fewer, longer
 // slices amortize each wave's selection work; the streaming rate is the same). Each
-// slice is at least one chunk long and aligned to the vector loads.
+// slice is at least one chunk long (two for the wave kernel) and aligned to the vector
+// loads. A row's wave slices are capped at kMaxWaveSplits: with few rows the chip is idle
+// anyway and the latency is one slice's chain plus the merge, whose cost grows with the
+// number of lists (measured on one row: 24 slices of 2048 beat 12 of 4096 and 48 of 1024
+// at vocab 49152; 37 slices of 4096 beat 46 and 74 at vocab 151936).
 constexpr int kTargetGroups = 1280;
 constexpr int kTargetWaves = 3072;
+constexpr int kMaxWaveSplits = 36;
 
 Plan make_plan(int rows, int vocab, int dtype, const void *logits, bool wave) {
   Plan p;
   const int vec_elems = dtype == TABBY_F32 ? 4 : 8;
   const bool aligned = ((uintptr_t)logits % 16u) == 0 && vocab % vec_elems == 0;
   p.vec = aligned ? vec_elems : 1;
-  const int chunk = wave ? 4 * kWChunk : kChunk;  // a wave slice spans at least 4 chunks
+  const int chunk = wave ? 2 * kWChunk : kChunk;
   const int target = wave ? kTargetWaves : kTargetGroups;
-  const int most = std::min(kMaxSplits, (vocab + chunk - 1) / chunk);
+  const int most = std::min(wave ? kMaxWaveSplits : kMaxSplits, (vocab + chunk - 1) / chunk);
   const int want = std::max(1, std::min(most, (target + rows - 1) / rows));
   const int granule = (wave ? kWaveSize : kBlock) * p.vec;
   const int per = (vocab + want - 1) / want;
