@@ -702,35 +702,49 @@ __device__ __forceinline__ int wave_local(int chunk, int e) {
   return chunk * kWChunk + ((e / VEC) * kWaveSize + wave_lane()) * VEC + e % VEC;
 }
 
-// Sorts list[0..count) descending in registers (count <= 64*R) and leaves its top `keep`
-// at list[0..keep).
+// The wave kernel's LDS list holds raw entries, (value bits << 32) | ~index, so that an
+// append needs no key transform; a prune or the final sort turns them into composites
+// (key_of(value) << 32 | ~index) as it reads them. key_of maps -0 to the key of +0.
+__device__ __forceinline__ uint64_t raw_entry(float x, uint32_t index) {
+  return ((uint64_t)__float_as_uint(x) << 32) | (uint64_t)(~index);
+}
+__device__ __forceinline__ uint32_t raw_key(uint64_t raw) { return key_of(__uint_as_float((uint32_t)(raw >> 32))); }
+__device__ __forceinline__ uint64_t composite_of_raw(uint64_t raw) {
+  return ((uint64_t)raw_key(raw) << 32) | (raw & 0xffffffffull);
+}
+__device__ __forceinline__ uint64_t raw_of_composite(uint64_t c) {
+  return ((uint64_t)__float_as_uint(value_of(composite_key(c))) << 32) | (c & 0xffffffffull);
+}
+
+// Sorts the raw list[0..count) descending in registers (count <= 64*R) and leaves its top
+// `keep` at list[0..keep), still raw.
 template <int R>
 __device__ __forceinline__ void wave_sort_list(uint64_t *list, int count, int keep) {
   uint64_t v[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int i = r * kWaveSize + wave_lane();
-    v[r] = i < count ? list[i] : 0ull;
+    v[r] = i < count ? composite_of_raw(list[i]) : 0ull;
   }
   wave_sort_desc<R>(v);
   wave_lds_sync();
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int i = r * kWaveSize + wave_lane();
-    if (i < keep) list[i] = v[r];
+    if (i < keep) list[i] = raw_of_composite(v[r]);
   }
   wave_lds_sync();
 }
 
-// Sorts list[0..count) descending in registers (count <= 64*R) and writes its top `keep`
-// to out[0..keep).
+// Sorts the raw list[0..count) descending in registers (count <= 64*R) and writes its top
+// `keep`, as composites, to out[0..keep).
 template <int R>
 __device__ __forceinline__ void store_sorted_top(const uint64_t *list, int count, int keep, uint64_t *out) {
   uint64_t v[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int i = r * kWaveSize + wave_lane();
-    v[r] = i < count ? list[i] : 0ull;
+    v[r] = i < count ? composite_of_raw(list[i]) : 0ull;
   }
   wave_sort_desc<R>(v);
 #pragma unroll
@@ -764,7 +778,7 @@ __device__ __noinline__ Pruned wave_prune(WaveSmem &sm, int count, int kk, uint3
   for (int r = 0; r < R; ++r) {
     const int i = r * kWaveSize + lane;
     v[r] = i < count ? sm.list[i] : 0ull;
-    k[r] = composite_key(v[r]);
+    k[r] = i < count ? raw_key(v[r]) : 0u;
     kmax = max(kmax, k[r]);
   }
 #pragma unroll
@@ -821,7 +835,7 @@ __device__ __noinline__ Pruned wave_prune(WaveSmem &sm, int count, int kk, uint3
   if (kept > kWListCap - kWaveSize) {  // massive ties: sort and cut exactly
     wave_sort_list<kWListCap / kWaveSize>(sm.list, kept, kk);
     kept = kk;
-    tk = composite_key(sm.list[kk - 1]);
+    tk = raw_key(sm.list[kk - 1]);
   }
   return {kept, tk};
 }
@@ -907,7 +921,7 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
       const bool take = cur[e] >= theta;
       const uint64_t mask = __ballot(take);
       if (mask) {
-        if (take) sm.list[count + (int)lanes_below(mask)] = composite(key_of(cur[e]), (uint32_t)(begin + wave_local<VEC>(c, e)));
+        if (take) sm.list[count + (int)lanes_below(mask)] = raw_entry(cur[e], (uint32_t)(begin + wave_local<VEC>(c, e)));
         count = __builtin_amdgcn_readfirstlane(count + (int)__popcll(mask));
       }
     }

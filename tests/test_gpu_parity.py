@@ -66,6 +66,27 @@ def test_ties_and_neg_inf(oracle):
     _log("ties+neg_inf", compare(w, res, ids, vals, run_oracle(oracle, w, 256), 256))
 
 
+@pytest.mark.parametrize("k", [20, 50, 64])
+def test_first_chunk_unrepresentative(oracle, k):
+    # Vocab 147,456 on 4 rows is cut into 36 slices of 4,096, and each slice's first chunk
+    # sets its starting theta. Rows 0-1 put one large value per lane in the first 256
+    # elements of every 4,096-block and keep the rest small (the first chunk holds the whole
+    # top of the slice); row 2 is sorted ascending (every first chunk is its slice's
+    # smallest: a low theta, many candidates, many prunes); row 3 descending.
+    V = 147456
+    w = synth.random_workload(rows=4, vocab=V, seed=41, k_choices=(k,), temperatures=(0.7,),
+                              top_ps=(0.9,), sigma=1.0)
+    big = np.zeros(V, dtype=bool)
+    big[(np.arange(V) % 4096 < 256) & (np.arange(V) % 4 == 0)] = True
+    rng = np.random.default_rng(k)
+    for r in (0, 1):
+        w.logits[r, big] = (20.0 + rng.standard_normal(int(big.sum()))).astype(np.float32)
+    w.logits[2] = np.sort(w.logits[2])
+    w.logits[3] = np.sort(w.logits[3])[::-1]
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=k)
+    _log(f"unrepresentative first chunk k={k}", compare(w, res, ids, vals, run_oracle(oracle, w, k), k))
+
+
 def test_all_equal_row_takes_lowest_ids(oracle):
     w = synth.random_workload(rows=2, vocab=5000, seed=3, k_choices=(64,))
     w.logits[:] = 1.5
