@@ -1,8 +1,8 @@
 // Workgroup-level building blocks for the sampler kernels: reductions, scans, the
 // radix select over 64-bit composites, and an LDS bitonic sort.
 //
-// Workgroups are kBlock = 256 lanes = 4 wave64s. Cross-lane steps inside a wave use
-// __shfl_xor / __shfl_up; the cross-wave step goes through a few words of LDS.
+// Workgroups are kBlock = 256 lanes = 4 wave64s. Cross-lane steps inside a wave use DPP and
+// permlane exchanges (wave_ops.h); the cross-wave step goes through a few words of LDS.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -28,8 +28,7 @@ struct BlockScratch {
 };
 
 __device__ __forceinline__ float block_max(float v, BlockScratch &s) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  v = wave_max(v);
   __syncthreads();
   if (lane_id() == 0) s.f[wave_id()] = v;
   __syncthreads();
@@ -41,8 +40,7 @@ __device__ __forceinline__ float block_max(float v, BlockScratch &s) {
 
 // Fixed reduction tree, so the result is bit-identical from run to run.
 __device__ __forceinline__ double block_sum(double v, BlockScratch &s) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  v = wave_sum(v);
   __syncthreads();
   if (lane_id() == 0) s.d[wave_id()] = v;
   __syncthreads();
@@ -56,12 +54,7 @@ __device__ __forceinline__ double block_sum(double v, BlockScratch &s) {
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, BlockScratch &s,
                                                          uint32_t *total) {
   const int lane = lane_id();
-  uint32_t inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t t = __shfl_up(inc, o);
-    if (lane >= o) inc += t;
-  }
+  const uint32_t inc = wave_inclusive_scan_u32(v);
   __syncthreads();
   if (lane == 63) s.u[wave_id()] = inc;
   __syncthreads();

@@ -781,8 +781,7 @@ __device__ __noinline__ Pruned wave_prune(WaveSmem &sm, int count, int kk, uint3
     k[r] = i < count ? raw_key(v[r]) : 0u;
     kmax = max(kmax, k[r]);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+  kmax = wave_max_u32(kmax);
   const uint32_t range = kmax - min(floor_key, kmax);
   const int bits = range == 0 ? 0 : 32 - __clz((int)range);
   const int shift = bits > 8 ? bits - 8 : 0;  // (kmax - key) >> shift < 256 for key >= floor
@@ -802,12 +801,7 @@ __device__ __noinline__ Pruned wave_prune(WaveSmem &sm, int count, int kk, uint3
     h[q] = sm.hist[lane * 4 + q];
     sum += h[q];
   }
-  uint32_t inc = sum;
-#pragma unroll
-  for (int o = 1; o < kWaveSize; o <<= 1) {
-    const uint32_t t = __shfl_up(inc, o);
-    if (lane >= o) inc += t;
-  }
+  const uint32_t inc = wave_inclusive_scan_u32(sum);
   const uint64_t reached = __ballot(inc >= (uint32_t)kk);
   const int owner = __ffsll((unsigned long long)reached) - 1;  // kk <= count: some lane reaches it
   int bin = 0;
@@ -818,7 +812,7 @@ __device__ __noinline__ Pruned wave_prune(WaveSmem &sm, int count, int kk, uint3
     if (before + h[0] + h[1] >= (uint32_t)kk) bin = lane * 4 + 1;
     if (before + h[0] >= (uint32_t)kk) bin = lane * 4;
   }
-  bin = __shfl(bin, owner);
+  bin = __builtin_amdgcn_readlane(bin, owner);
   // Smallest key in that bin; everything at or above it is kept.
   const uint32_t drop = ((uint32_t)bin + 1u) << shift;
   uint32_t tk = max(kmax - min(drop, kmax) + 1u, floor_key);
@@ -872,10 +866,12 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   uint32_t theta_key = kNegInfKey;
   float theta = -INFINITY;  // == value_of(theta_key)
 
-  // Processes chunk c held in `cur` while chunk `nxt_chunk` loads into `nxt`.
+  // Processes chunk c held in `cur` while chunk c + 1, if any, loads into `nxt`. (A load past
+  // the last chunk would be waited for by the end-of-slice prune.)
   auto step = [&](int c, float (&cur)[kWChunkPerLane], float (&nxt)[kWChunkPerLane]) {
-    const int nc = min(c + 1, nchunks - 1);
-    if (nc < full_chunks) wave_load_full<In, VEC>(src, nc, nxt); else wave_load<In, VEC>(src, n, nc, nxt);
+    const int nc = c + 1;
+    if (nc < full_chunks) wave_load_full<In, VEC>(src, nc, nxt);
+    else if (nc < nchunks) wave_load<In, VEC>(src, n, nc, nxt);
     const bool partial = c >= full_chunks;  // only the slice's last chunk can be partial
     if (partial) {
 #pragma unroll
@@ -1549,7 +1545,7 @@ __device__ __forceinline__ void flush_head(uint64_t *list, int count, uint32_t *
   wave_lds_sync();
   uint32_t base = 0;
   if (wave_lane() == 0) base = atomicAdd(head_count, (uint32_t)count);
-  base = (uint32_t)__shfl((int)base, 0);
+  base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
   for (int i = wave_lane(); i < count; i += kWaveSize) head[base + i] = list[i];
   wave_lds_sync();
 }

@@ -86,6 +86,29 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v + xor_lane<1>(v);
 }
 
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, xor_lane<32>(v));
+  v = max(v, xor_lane<16>(v));
+  v = max(v, xor_lane<8>(v));
+  v = max(v, xor_lane<4>(v));
+  v = max(v, xor_lane<2>(v));
+  return max(v, xor_lane<1>(v));
+}
+
+// Inclusive prefix sum over the wave's lanes in lane order: DPP row shifts (0 shifted in)
+// within each 16-lane row, then the totals of the rows below from three readlanes.
+__device__ __forceinline__ uint32_t wave_inclusive_scan_u32(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 47);
+  const int row = wave_lane() >> 4;
+  return x + (row == 0 ? 0u : row == 1 ? r0 : row == 2 ? r0 + r1 : r0 + r1 + r2);
+}
+
 // Makes this wave's LDS writes visible to its other lanes (LDS operations of one wave
 // complete in order; waiting for them is all that is needed).
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
