@@ -95,6 +95,22 @@ struct Launch {
   int32_t h_slice_len;
 };
 
+// The (row, slice) of workgroup b of a grid of rows x splits. Workgroup b runs on XCD b % 8
+// (round-robin dispatch over the eight XCDs), and so does the merge's workgroup for row b:
+// when rows is a multiple of 8, row r's slices go to XCD r % 8 too, so that the merge
+// finds their lists and statistics in its own XCD's L2. Otherwise row-major.
+__device__ __forceinline__ void row_slice_of(int b, int rows, int splits, int &row, int &slice) {
+  if (rows % 8 == 0) {
+    const int x = b & 7, i = b >> 3;
+    const int k = i / splits;
+    row = x + 8 * k;
+    slice = i - k * splits;
+  } else {
+    row = b / splits;
+    slice = b - row * splits;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Loads: VEC consecutive elements (16 bytes for the vector forms) widened to f32. f16
 // widening is exact (tests/support.ts:61-74 states the same property for its reference).
@@ -514,9 +530,8 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
   constexpr int ITEMS = kChunkPerLane / VEC;
   __shared__ SliceSmem sm;
 
-  const int splits = L.splits;
-  const int row = (int)blockIdx.x / splits;
-  const int slice = (int)blockIdx.x - row * splits;
+  int row, slice;
+  row_slice_of((int)blockIdx.x, L.rows, L.splits, row, slice);
   const int V = L.vocab;
   const int begin = slice * L.slice_len;
   const int n = min(L.slice_len, V - begin);
@@ -844,9 +859,8 @@ template <typename In, int VEC>
 __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) {
   __shared__ WaveSmem sm;
 
-  const int splits = L.splits;
-  const int row = (int)blockIdx.x / splits;
-  const int slice = (int)blockIdx.x - row * splits;
+  int row, slice;
+  row_slice_of((int)blockIdx.x, L.rows, L.splits, row, slice);
   const int V = L.vocab;
   const int begin = slice * L.slice_len;
   const int n = min(L.slice_len, V - begin);
@@ -1553,9 +1567,8 @@ __device__ __forceinline__ void flush_head(uint64_t *list, int count, uint32_t *
 template <typename In, int VEC>
 __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) {
   __shared__ uint64_t list[kWListCap];
-  const int splits = L.h_splits;
-  const int row = (int)blockIdx.x / splits;
-  const int slice = (int)blockIdx.x - row * splits;
+  int row, slice;
+  row_slice_of((int)blockIdx.x, L.rows, L.h_splits, row, slice);
   const tabby_row_params P = L.params[row];
   if (!is_head_row(P, L)) return;
   const RowState rs = W.row_state[row];
