@@ -13,12 +13,19 @@
 //   sums are m*u + u * (an integer prefix sum of rint(t_j / u)), and an integer prefix sum
 //   has no order dependence.
 //
-//   An event is a term whose addition is a tie, or that takes the integer sum to 2^53 or
-//   beyond (the sum leaves the binade and is rounded with a coarser ulp). That one term is
-//   added with an ordinary f64 add from the exact P before it; then the binade is
-//   recomputed and the scan resumes after it. P only grows (terms are >= 0), so there are at
-//   most a few dozen binade changes; exact ties need terms whose bits end exactly half an
-//   ulp below P, which are rare in practice and are handled correctly when they occur.
+//   A tie (t / u = f + 1/2) rounds to the even one of m + f and m + f + 1, so it adds
+//   f + ((m + f) mod 2) and leaves an even sum. Only the parity of the running m matters, and
+//   it follows a two-state automaton: a non-tie step XORs it with the parity of its increment,
+//   a tie step resets it to 0. Steps compose as maps x -> (x AND k) XOR c, an associative
+//   monoid, so the parity before every term comes from a wave scan too, and ties cost
+//   nothing extra (terms drawn from few distinct values, as with quantised logits, can tie
+//   on most steps).
+//
+//   An event is a term that takes the integer sum to 2^53 or beyond (the sum leaves the
+//   binade and is rounded with a coarser ulp), or the first partial sum that reaches the
+//   stop value. An event term is added with an ordinary f64 add from the exact P before it;
+//   then the binade is recomputed and the scan resumes after it. P only grows (terms are
+//   >= 0), so there are at most a few dozen binade changes.
 //
 // Integers below 2^53 are exact in f64, so the prefix sums are done in f64: every partial
 // sum of non-negative integers is exact while it is below 2^53, and once the true value
@@ -66,6 +73,40 @@ __device__ __forceinline__ double wave_inclusive_scan(double x) {
   const double below = row == 0 ? 0.0 : row == 1 ? r0 : row == 2 ? r0 + r1 : (r0 + r1) + r2;
   return x + below;
 }
+
+// Parity maps x -> (x & k) ^ c on {0, 1}, encoded k | c << 1; kParityId is the identity.
+constexpr uint32_t kParityId = 1u;
+
+// The map "apply lo, then hi".
+__device__ __forceinline__ uint32_t parity_then(uint32_t lo, uint32_t hi) {
+  const uint32_t k = lo & hi & 1u;
+  const uint32_t c = (((lo >> 1) & hi) ^ (hi >> 1)) & 1u;
+  return k | (c << 1);
+}
+
+__device__ __forceinline__ uint32_t parity_apply(uint32_t f, uint32_t x) { return (x & f & 1u) ^ ((f >> 1) & 1u); }
+
+// The composition of the maps of the lanes below this one (exclusive scan in lane order).
+__device__ __forceinline__ uint32_t parity_exclusive_scan(uint32_t f) {
+  uint32_t x = f;
+  x = parity_then((uint32_t)__builtin_amdgcn_update_dpp((int)kParityId, (int)x, 0x111, 0xF, 0xF, false), x);
+  x = parity_then((uint32_t)__builtin_amdgcn_update_dpp((int)kParityId, (int)x, 0x112, 0xF, 0xF, false), x);
+  x = parity_then((uint32_t)__builtin_amdgcn_update_dpp((int)kParityId, (int)x, 0x114, 0xF, 0xF, false), x);
+  x = parity_then((uint32_t)__builtin_amdgcn_update_dpp((int)kParityId, (int)x, 0x118, 0xF, 0xF, false), x);
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 47);
+  const uint32_t b1 = r0, b2 = parity_then(r0, r1), b3 = parity_then(b2, r2);
+  const int lane = wave_lane(), row = lane >> 4;
+  const uint32_t below_row = row == 0 ? kParityId : row == 1 ? b1 : row == 2 ? b2 : b3;
+  const uint32_t incl = parity_then(below_row, x);
+  // Exclusive: the inclusive map of the lane below; a row's first lane takes the rows below.
+  uint32_t e = (uint32_t)__builtin_amdgcn_update_dpp((int)kParityId, (int)incl, 0x111, 0xF, 0xF, false);
+  if ((lane & 15) == 0) e = below_row;
+  return e;
+}
+
+__device__ __forceinline__ uint32_t low_bit(double integral) { return (uint32_t)((uint64_t)integral & 1u); }
 
 struct SeqSum {
   double total;  // the last partial sum computed
@@ -125,15 +166,20 @@ __device__ __forceinline__ SeqSum wave_seq_sum(const double *t, int n, double *o
     const double u = __longlong_as_double((long long)((uint64_t)(E - 52 + 1023) << 52));
     const double scale = __longlong_as_double((long long)((uint64_t)(52 - E + 1023) << 52));
     const double m = P * scale;
-    // Lane L takes term a + L: its rounded increment and whether it is a tie.
+    // Lane L takes term a + L: its rounded increment, a tie rounding to the even sum.
     const int j = a + lane;
     const double q = j < n ? t[j] * scale : 0.0;
-    const double r = __builtin_rint(q);
-    const bool tie = q < kTwo52 && q - __builtin_floor(q) == 0.5;
+    const double fl = __builtin_floor(q);
+    const bool tie = q < kTwo52 && q - fl == 0.5;
+    double r = __builtin_rint(q);
+    if (__ballot(tie)) {  // the parity scan only when some term of this step ties
+      const uint32_t parity_before = parity_apply(parity_exclusive_scan(tie ? 0u : 1u | (low_bit(r) << 1)), low_bit(m));
+      if (tie) r = fl + (double)(parity_before ^ low_bit(fl));
+    }
     const double cum = m + wave_inclusive_scan(r);
     const bool crosses = cum >= kTwo53;
     const bool stops = cum * u >= stop_at;
-    const uint64_t flagged = __ballot(j < n && (tie || crosses || stops));
+    const uint64_t flagged = __ballot(j < n && (crosses || stops));
     const int Lf = flagged ? __ffsll((unsigned long long)flagged) - 1 : kWaveSize;
     // Partial sums before the first flagged term are exact: cum * u.
     if (out && j < n && lane < Lf) out[j] = cum * u;
@@ -144,13 +190,13 @@ __device__ __forceinline__ SeqSum wave_seq_sum(const double *t, int n, double *o
       continue;
     }
     const int jf = a + Lf;
-    const bool plain_stop = (__builtin_amdgcn_readlane((int)(stops && !tie && !crosses), Lf)) != 0;
+    const bool plain_stop = (__builtin_amdgcn_readlane((int)(stops && !crosses), Lf)) != 0;
     if (plain_stop) {  // exact partial sum that reaches stop_at
       const double at = lane_f64(cum, Lf) * u;
       if (out && lane == 0) out[jf] = at;
       return {at, jf + 1};
     }
-    // A tie or a binade change: one ordinary f64 add from the exact partial sum before it.
+    // A binade change: one ordinary f64 add from the exact partial sum before it.
     const double before = (Lf == 0 ? m : lane_f64(cum, Lf - 1)) * u;
     P = before + t[jf];
     if (out && lane == 0) out[jf] = P;
@@ -180,14 +226,32 @@ __device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, doub
     double tv[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) tv[i] = first + i < n ? t[first + i] : 0.0;
+    // Each term's parity map (a tie resets, any other term XORs its increment's parity),
+    // composed along the lane, then scanned across lanes for the parity at the lane's start.
+    double q[kPer];
+    uint32_t tie_bits = 0, lane_map = kParityId;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      q[i] = tv[i] * scale;
+      const bool tie = q[i] < kTwo52 && q[i] - __builtin_floor(q[i]) == 0.5;
+      if (tie) tie_bits |= 1u << i;
+      lane_map = parity_then(lane_map, tie ? 0u : 1u | (low_bit(__builtin_rint(q[i])) << 1));
+    }
+    uint32_t parity = 0u;
+    if (__ballot(tie_bits != 0u)) parity = parity_apply(parity_exclusive_scan(lane_map), low_bit(m));
     double pre[kPer];
-    uint32_t tie_bits = 0;
     double run = 0.0;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const double q = tv[i] * scale;
-      const double r = __builtin_rint(q);
-      if (q < kTwo52 && q - __builtin_floor(q) == 0.5) tie_bits |= 1u << i;
+      double r;
+      if ((tie_bits >> i) & 1u) {
+        const double fl = __builtin_floor(q[i]);
+        r = fl + (double)(parity ^ low_bit(fl));
+        parity = 0u;
+      } else {
+        r = __builtin_rint(q[i]);
+        parity ^= low_bit(r);
+      }
       run += r;
       pre[i] = run;
     }
@@ -201,7 +265,7 @@ __device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, doub
     if (lane == 32) below = i31;
     if (lane == 48) below = i47;
     const double base = m + below;
-    uint32_t ev_bits = tie_bits;
+    uint32_t ev_bits = 0;
     int stop_i = kPer;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {

@@ -48,6 +48,23 @@ def test_exact_half_ulp_ties_round_to_even(wide):
     _check(np.concatenate([[0.75], np.sort(base)[::-1]]), wide=wide)
 
 
+def test_dense_ties_long(wide):
+    # Terms that fall on half an ulp of the running sum on most steps, past the short path.
+    pattern = np.array([2.0 ** -53, 3 * 2.0 ** -53, 2.0 ** -52, 5 * 2.0 ** -54, 2.0 ** -53, 7 * 2.0 ** -54])
+    _check(np.concatenate([[1.0], np.tile(pattern, 600)]), wide=wide)
+    _check(np.concatenate([[1.5], np.tile(pattern[::-1], 500)]), wide=wide)
+
+
+@pytest.mark.parametrize("stop", [np.inf, 0.98])
+def test_quantised_logit_terms(stop, wide):
+    # Weights of logits on a 0.25 grid (few distinct values, many repeats), sorted, as in
+    # BASELINE config 5; the top-p stop variant cuts inside the run.
+    rng = np.random.default_rng(5)
+    levels = np.sort(np.round(rng.normal(0, 2, 1024) * 4) / 4)[::-1]
+    s = np.exp(levels - levels[0])
+    _check(s / s.sum() if np.isfinite(stop) else s, stop, wide)
+
+
 def test_tiny_and_zero_terms(wide):
     _check(np.concatenate([[1.0], np.full(100, 1e-300), np.zeros(200), [5e-324] * 10]), wide=wide)
 
