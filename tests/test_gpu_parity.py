@@ -43,6 +43,22 @@ def test_config5_ties_neg_inf_k1024(oracle):
     _log("config5[128 rows]", compare(w, res, ids, vals, run_oracle(oracle, w, 1024), 1024))
 
 
+def test_config5_sorted_slice_lists(oracle):
+    # 256 rows: 5 slices per row, each leaving its list sorted, merged by merge paths.
+    w = synth.config(5, rows=256)
+    res, ids, vals = run_gpu(w, k_max=1024, topk_cap=1024)
+    _log("config5[256 rows]", compare(w, res, ids, vals, run_oracle(oracle, w, 1024), 1024))
+
+
+def test_large_pool_capacity_mixed_k(oracle):
+    # k_max 1024 sends every row through the 256-lane slices; small and large k mix, with
+    # ties and -inf, on few enough slices per row for the sorted-list merge.
+    w = synth.random_workload(rows=192, vocab=20000, seed=17, ties=True, neg_inf_frac=0.3,
+                              k_choices=(1, 64, 300, 1024))
+    res, ids, vals = run_gpu(w, k_max=1024, topk_cap=1024)
+    _log("k_max 1024 mixed", compare(w, res, ids, vals, run_oracle(oracle, w, 1024), 1024))
+
+
 def test_f16_input_finite_k(oracle):
     w = synth.config(4, rows=16)
     w.top_k[:] = np.array([1, 20, 50, 100] * 4, np.int32)
