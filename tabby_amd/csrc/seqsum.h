@@ -108,6 +108,15 @@ __device__ __forceinline__ uint32_t parity_exclusive_scan(uint32_t f) {
 
 __device__ __forceinline__ uint32_t low_bit(double integral) { return (uint32_t)((uint64_t)integral & 1u); }
 
+// Term arrays are read and written through accessors: a plain pointer (LDS or global), or
+// PaddedLds, an LDS array with one pad word after every 16 entries, so that the wide form's
+// 16 consecutive entries per lane fall on nearly distinct banks (2-way instead of 32-way).
+struct PaddedLds {
+  double *p;
+  __device__ __forceinline__ double &operator[](int j) const { return p[j + (j >> 4)]; }
+  __host__ __device__ static constexpr int words(int n) { return n + (n >> 4) + 1; }
+};
+
 struct SeqSum {
   double total;  // the last partial sum computed
   int count;     // terms added (the sum stopped early if count < n)
@@ -116,8 +125,8 @@ struct SeqSum {
 // Short sums: every lane adds the same terms left to right (broadcast LDS reads, eight ahead
 // of the adds), so the loop is uniform scalar control flow with no per-lane branching; lane
 // 0 alone writes the partial sums. kStop: stop at the first partial sum >= stop_at.
-template <bool kOut, bool kStop>
-__device__ __forceinline__ SeqSum uniform_seq_sum(const double *t, int n, double *out, double stop_at) {
+template <bool kOut, bool kStop, class In, class Out>
+__device__ __forceinline__ SeqSum uniform_seq_sum(In t, int n, Out out, double stop_at) {
   const bool writer = wave_lane() == 0;
   double P = t[0];
   if (kOut && writer) out[0] = P;
@@ -142,10 +151,15 @@ __device__ __forceinline__ SeqSum uniform_seq_sum(const double *t, int n, double
   return {P, n};
 }
 
-__device__ __forceinline__ SeqSum lane_seq_sum(const double *t, int n, double *out, double stop_at) {
+template <class In, class Out>
+__device__ __forceinline__ SeqSum lane_seq_sum(In t, int n, Out out, bool has_out, double stop_at) {
   const bool stop = stop_at < INFINITY;
-  if (out) return stop ? uniform_seq_sum<true, true>(t, n, out, stop_at) : uniform_seq_sum<true, false>(t, n, out, stop_at);
+  if (has_out) return stop ? uniform_seq_sum<true, true>(t, n, out, stop_at) : uniform_seq_sum<true, false>(t, n, out, stop_at);
   return stop ? uniform_seq_sum<false, true>(t, n, out, stop_at) : uniform_seq_sum<false, false>(t, n, out, stop_at);
+}
+
+__device__ __forceinline__ SeqSum lane_seq_sum(const double *t, int n, double *out, double stop_at) {
+  return lane_seq_sum(t, n, out, out != nullptr, stop_at);
 }
 
 // Adds t[0..n) left to right (n >= 1, every t_j >= 0, t[0] > 0, and every partial sum at
@@ -206,15 +220,20 @@ __device__ __forceinline__ SeqSum wave_seq_sum(const double *t, int n, double *o
   return {P, n};
 }
 
-// The same sum for long sequences in global memory: each lane takes 16 consecutive terms
-// (one 128-byte line) per step, so a step covers 1024 terms; an event restarts the step
-// after the event term. Same contract as wave_seq_sum.
-__device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, double *out, double stop_at) {
+// The same sum for long sequences in global memory or padded LDS: each lane takes 16
+// consecutive terms (one 128-byte line) per step, so a step covers 1024 terms; an event
+// restarts the step after the event term. Same contract as wave_seq_sum; out is written
+// only if has_out. settle: the terms are non-increasing, so once a whole step has added
+// only terms below half an ulp of the sum (no event), every later term is too and the sum
+// cannot change again: it returns there (only when nothing is written).
+template <class In, class Out>
+__device__ __forceinline__ SeqSum wave_seq_sum_wide(In t, int n, Out out, bool has_out, double stop_at,
+                                                    bool settle = false) {
   constexpr int kPer = 16, kStep = kWaveSize * kPer;
-  if (n <= kSeqShort) return lane_seq_sum(t, n, out, stop_at);
+  if (n <= kSeqShort) return lane_seq_sum(t, n, out, has_out, stop_at);
   const int lane = wave_lane();
   double P = t[0];
-  if (out && lane == 0) out[0] = P;
+  if (has_out && lane == 0) out[0] = P;
   if (P >= stop_at) return {P, 1};
   int a = 1;
   while (a < n) {
@@ -223,36 +242,40 @@ __device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, doub
     const double scale = __longlong_as_double((long long)((uint64_t)(52 - E + 1023) << 52));
     const double m = P * scale;
     const int first = a + lane * kPer;
-    double tv[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) tv[i] = first + i < n ? t[first + i] : 0.0;
-    // Each term's parity map (a tie resets, any other term XORs its increment's parity),
-    // composed along the lane, then scanned across lanes for the parity at the lane's start.
-    double q[kPer];
-    uint32_t tie_bits = 0, lane_map = kParityId;
+    double q[kPer], r[kPer];
+    uint32_t tie_bits = 0;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      q[i] = tv[i] * scale;
-      const bool tie = q[i] < kTwo52 && q[i] - __builtin_floor(q[i]) == 0.5;
-      if (tie) tie_bits |= 1u << i;
-      lane_map = parity_then(lane_map, tie ? 0u : 1u | (low_bit(__builtin_rint(q[i])) << 1));
+      q[i] = (first + i < n ? t[first + i] : 0.0) * scale;
+      r[i] = __builtin_rint(q[i]);
+      // r - q is exact (the two are within 1/2 of each other), so a tie is |r - q| == 1/2.
+      if (q[i] < kTwo52 && __builtin_fabs(r[i] - q[i]) == 0.5) tie_bits |= 1u << i;
     }
-    uint32_t parity = 0u;
-    if (__ballot(tie_bits != 0u)) parity = parity_apply(parity_exclusive_scan(lane_map), low_bit(m));
+    if (__ballot(tie_bits != 0u)) {
+      // Each term's parity map (a tie resets, any other term XORs its increment's parity),
+      // composed along the lane, then scanned across lanes for the parity at the lane's
+      // start; a tie then adds its floor plus the bit that makes the sum even.
+      uint32_t lane_map = kParityId;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+        lane_map = parity_then(lane_map, ((tie_bits >> i) & 1u) ? 0u : 1u | (low_bit(r[i]) << 1));
+      uint32_t parity = parity_apply(parity_exclusive_scan(lane_map), low_bit(m));
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        if ((tie_bits >> i) & 1u) {
+          const double fl = q[i] - 0.5;
+          r[i] = fl + (double)(parity ^ low_bit(fl));
+          parity = 0u;
+        } else {
+          parity ^= low_bit(r[i]);
+        }
+      }
+    }
     double pre[kPer];
     double run = 0.0;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      double r;
-      if ((tie_bits >> i) & 1u) {
-        const double fl = __builtin_floor(q[i]);
-        r = fl + (double)(parity ^ low_bit(fl));
-        parity = 0u;
-      } else {
-        r = __builtin_rint(q[i]);
-        parity ^= low_bit(r);
-      }
-      run += r;
+      run += r[i];
       pre[i] = run;
     }
     const double incl = wave_inclusive_scan(run);
@@ -265,23 +288,30 @@ __device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, doub
     if (lane == 32) below = i31;
     if (lane == 48) below = i47;
     const double base = m + below;
-    uint32_t ev_bits = 0;
-    int stop_i = kPer;
+    // Partial sums only grow: a lane whose last one neither crosses 2^53 nor reaches the stop
+    // has no event; the others look for their first.
+    const int last_i = min(kPer, n - first) - 1;  // this lane's last term (negative: none)
+    double cum_end = base;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const double cum = base + pre[i];
-      if (first + i < n) {
-        if (cum >= kTwo53) ev_bits |= 1u << i;
-        if (stop_i == kPer && cum * u >= stop_at) stop_i = i;
+    for (int i = 0; i < kPer; ++i)
+      if (i == last_i) cum_end = base + pre[i];
+    int my_first = kPer;
+    bool my_stop = false;
+    if (last_i >= 0 && (cum_end >= kTwo53 || cum_end * u >= stop_at)) {
+#pragma unroll
+      for (int i = kPer - 1; i >= 0; --i) {
+        const double cum = base + pre[i];
+        if (i <= last_i && (cum >= kTwo53 || cum * u >= stop_at)) {
+          my_first = i;
+          my_stop = cum < kTwo53;
+        }
       }
     }
-    const int ev_i = ev_bits ? __builtin_ctz(ev_bits) : kPer;
-    const int my_first = min(ev_i, stop_i);
     const uint64_t has = __ballot(my_first < kPer);
     const int Lf = has ? __ffsll((unsigned long long)has) - 1 : kWaveSize;
     const int fi = Lf < kWaveSize ? __builtin_amdgcn_readlane(my_first, Lf) : 0;
     const int flagged = Lf < kWaveSize ? a + Lf * kPer + fi : n;
-    if (out) {
+    if (has_out) {
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
         const int j = first + i;
@@ -291,16 +321,19 @@ __device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, doub
     if (flagged >= n) {
       const int last = min(n, a + kStep) - 1;
       const int ll = (last - a) / kPer, li = (last - a) % kPer;
-      double cum_last = 0.0;
+      double cum_last = 0.0, q_last = 0.0;
 #pragma unroll
       for (int i = 0; i < kPer; ++i)
-        if (i == li) cum_last = base + pre[i];
+        if (i == li) {
+          cum_last = base + pre[i];
+          q_last = q[i];
+        }
       P = lane_f64(cum_last, ll) * u;
       a = last + 1;
+      if (settle && !has_out && lane_f64(q_last, ll) < 0.5) return {P, n};
       continue;
     }
-    const bool is_stop = __builtin_amdgcn_readlane(stop_i, Lf) == fi &&
-                         !((__builtin_amdgcn_readlane((int)ev_bits, Lf) >> fi) & 1u);
+    const bool is_stop = __builtin_amdgcn_readlane((int)my_stop, Lf) != 0;
     double before_mine = 0.0, at_mine = 0.0;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
@@ -311,15 +344,19 @@ __device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, doub
     }
     if (is_stop) {
       const double at = lane_f64(at_mine, Lf) * u;
-      if (out && lane == 0) out[flagged] = at;
+      if (has_out && lane == 0) out[flagged] = at;
       return {at, flagged + 1};
     }
     P = lane_f64(before_mine, Lf) * u + t[flagged];
-    if (out && lane == 0) out[flagged] = P;
+    if (has_out && lane == 0) out[flagged] = P;
     if (P >= stop_at) return {P, flagged + 1};
     a = flagged + 1;
   }
   return {P, n};
+}
+
+__device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, double *out, double stop_at) {
+  return wave_seq_sum_wide(t, n, out, out != nullptr, stop_at);
 }
 
 // Two independent left-to-right sums over the same length (poolMass and the scaled total):

@@ -973,10 +973,12 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   }
 }
 
-// Smallest key whose scaled logit (l - max)/T in f64 is >= -40 (the max's key when T <= 0:
-// greedy needs only the row's maxima). Anything below has exp(.) < 2^-54 and, added in sorted
-// order, can change neither the scaled total nor a running sum, both of which are >= their
-// first term when it is added.
+// Smallest key whose scaled logit (l - max)/T in f64 is >= -37.5 (the max's key when T <= 0:
+// greedy needs only the row's maxima). Anything below has a weight exp(.) < e^-37.5 < 5.2e-17,
+// below 2^-54 = 5.55e-17, and, added in sorted order, is below half an ulp of both sums it
+// enters: the scaled total, which is >= 1 (its first term is exp(0)), and a running sum of
+// the weights divided by that total, which is >= its first term 1/total while every later
+// weight is < 2^-54/total. So it changes neither, and the draw never reaches it.
 __device__ __forceinline__ uint32_t head_threshold(float row_max, double T) {
   const uint32_t top = key_of(row_max);
   if (!(T > 0.0)) return top;
@@ -984,7 +986,7 @@ __device__ __forceinline__ uint32_t head_threshold(float row_max, double T) {
   while (hi - lo > 1u) {
     const uint32_t mid = lo + (hi - lo) / 2u;
     const double q = ((double)value_of(mid) - (double)row_max) / T;
-    if (q >= -40.0) hi = mid; else lo = mid;
+    if (q >= -37.5) hi = mid; else lo = mid;
   }
   return hi;
 }
@@ -1543,12 +1545,13 @@ __global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace 
 // ---------------------------------------------------------------------------------------
 // Whole-vocabulary rows (top_k = 0, or >= vocab beyond the pool capacity). The pool is the
 // entire row sorted, but only its head matters to sampleFromTopK: with the row max M, an
-// element whose (l - M)/T is below -40 has exp(.) < 2^-54, and it is added -- in sorted
-// order, after every larger term -- to the scaled total (>= 1, the max's own term) or to a
-// running weight sum (>= the first weight), so it cannot change either by rounding. The
-// merge computes head_key, the smallest key with (l - M)/T >= -40 in f64 (or the max's key
-// when T <= 0). head_kernel collects the head; head_finish_kernel sorts it and runs the
-// tail. poolMass takes the head's terms plus the rest of sum-exp.
+// element whose (l - M)/T is below -37.5 has a weight below 2^-54, and it is added -- in
+// sorted order, after every larger term -- to the scaled total (>= 1, the max's own term)
+// or, divided by that total, to a running weight sum (>= the first weight), below half an
+// ulp of either, so it cannot change them (head_threshold). The merge computes head_key, the
+// smallest key with (l - M)/T >= -37.5 in f64 (or the max's key when T <= 0). head_kernel
+// collects the head; the plan, sort and finish kernels sort it and run the tail. poolMass
+// takes the head's terms plus the rest of sum-exp.
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ bool is_head_row(const tabby_row_params &P, const Launch &L) {
   return params_valid(P, L.k_max) && effective_k(P, L.vocab) > L.kcap;
@@ -1800,17 +1803,23 @@ __global__ __launch_bounds__(kBlock) void head_sort_kernel(Launch L, Workspace W
   terms(out);
 }
 
+// Heads up to this many entries run their sums from LDS (padded, 139 KB of the 160 KB a
+// gfx950 workgroup may use); larger ones from global memory.
+constexpr int kHeadLds = 16384;
+
 struct HeadSmem {
   BlockScratch bs;
   double pool, e;
   double scaled_total;
   int cut;
   int chosen;
+  double t[PaddedLds::words(kHeadLds)];  // the head's weights, then their running sums
 };
 
 // First i in [0, n) with target < c[i] (c non-decreasing), or n - 1 when there is none: a
-// 64-ary search by one wave, each step probing 64 evenly spaced entries.
-__device__ __forceinline__ int wave_first_above(const double *c, int n, double target) {
+// 64-ary search by one wave, each step probing 64 evenly spaced entries. C: an accessor.
+template <class C>
+__device__ __forceinline__ int wave_first_above(C c, int n, double target) {
   int lo = 0, hi = n;  // the answer lies in [lo, hi]; hi == n means "none yet"
   while (hi - lo > kWaveSize) {
     const int step = (hi - lo + kWaveSize - 1) / kWaveSize;
@@ -1885,30 +1894,55 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
     res.considered = 1;
     res.pool_exhausted = 0;
   } else {
-    // The scaled total over the sorted head (bit-exact sequential sum, wave 0).
-    if (wave_id() == 0) {
-      const double S = wave_seq_sum_wide(sg, H, nullptr, INFINITY).total;
-      if (lane_id() == 0) sm.scaled_total = S;
-    }
-    __syncthreads();
-    const double S = sm.scaled_total;
-    for (int i = threadIdx.x; i < H; i += kBlock) cg[i] = sg[i] / S;
-    __syncthreads();
-    // Running sums of the weights up to the first that reaches top-p (the cut); without a
-    // cut the whole vocabulary is considered.
+    // The scaled total over the sorted head (bit-exact sequential sum, wave 0), the weights,
+    // and their running sums up to the first that reaches top-p (the cut; without a cut the
+    // whole vocabulary is considered). From LDS when the head fits, else global memory.
     const double top_p = P.top_p;
-    if (wave_id() == 0) {
-      const SeqSum run = wave_seq_sum_wide(cg, H, cg, top_p < 1.0 ? top_p : INFINITY);
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");  // the sums are read by other lanes
-      const bool reached = top_p < 1.0 && run.total >= top_p;
-      const double target = P.uniform * run.total;  // the running sum at the cut: the total
-      const int first = wave_first_above(cg, run.count, target);
-      if (lane_id() == 0) {
-        sm.cut = reached ? run.count : V;
-        sm.chosen = first;
+    const double stop = top_p < 1.0 ? top_p : INFINITY;
+    auto finish = [&](auto t, auto c) {
+      if (wave_id() == 0) {
+        // The weights are non-increasing: the sum may settle before the head's end.
+        const double S = wave_seq_sum_wide(t, H, c, false, INFINITY, true).total;  // c unused
+        if (lane_id() == 0) sm.scaled_total = S;
       }
+      __syncthreads();
+      const double S = sm.scaled_total;
+      for (int i = threadIdx.x; i < H; i += kBlock) c[i] = t[i] / S;
+      __syncthreads();
+      if (wave_id() == 0) {
+        const SeqSum run = wave_seq_sum_wide(c, H, c, true, stop);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");  // the sums are read by other lanes
+        const bool reached = top_p < 1.0 && run.total >= top_p;
+        const double target = P.uniform * run.total;  // the running sum at the cut: the total
+        const int first = wave_first_above(c, run.count, target);
+        if (lane_id() == 0) {
+          sm.cut = reached ? run.count : V;
+          sm.chosen = first;
+        }
+      }
+      __syncthreads();
+    };
+    if (H <= kHeadLds) {
+      const PaddedLds lt{sm.t};
+      constexpr int B = 8;  // loads in flight per lane
+      for (int base = 0; base < H; base += B * kBlock) {
+        double v[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int i = base + u * kBlock + (int)threadIdx.x;
+          v[u] = i < H ? sg[i] : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int i = base + u * kBlock + (int)threadIdx.x;
+          if (i < H) lt[i] = v[u];
+        }
+      }
+      __syncthreads();
+      finish(lt, lt);
+    } else {
+      finish((const double *)sg, cg);
     }
-    __syncthreads();
     chosen = sm.chosen;
     res.considered = (uint32_t)sm.cut;
     res.pool_exhausted = (top_p < 1.0 && pool_mass < top_p) ? 1 : 0;
