@@ -289,12 +289,10 @@ __device__ __forceinline__ SeqSum wave_seq_sum_wide(In t, int n, Out out, bool h
     if (lane == 48) below = i47;
     const double base = m + below;
     // Partial sums only grow: a lane whose last one neither crosses 2^53 nor reaches the stop
-    // has no event; the others look for their first.
+    // has no event; the others look for their first. (Terms past n are 0, so the lane's
+    // last partial sum is base + run.)
     const int last_i = min(kPer, n - first) - 1;  // this lane's last term (negative: none)
-    double cum_end = base;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i)
-      if (i == last_i) cum_end = base + pre[i];
+    const double cum_end = base + run;
     int my_first = kPer;
     bool my_stop = false;
     if (last_i >= 0 && (cum_end >= kTwo53 || cum_end * u >= stop_at)) {
@@ -320,17 +318,10 @@ __device__ __forceinline__ SeqSum wave_seq_sum_wide(In t, int n, Out out, bool h
     }
     if (flagged >= n) {
       const int last = min(n, a + kStep) - 1;
-      const int ll = (last - a) / kPer, li = (last - a) % kPer;
-      double cum_last = 0.0, q_last = 0.0;
-#pragma unroll
-      for (int i = 0; i < kPer; ++i)
-        if (i == li) {
-          cum_last = base + pre[i];
-          q_last = q[i];
-        }
-      P = lane_f64(cum_last, ll) * u;
+      const int ll = (last - a) / kPer;
+      P = lane_f64(cum_end, ll) * u;  // lane ll holds the step's last term
+      if (settle && !has_out && t[last] * scale < 0.5) return {P, n};
       a = last + 1;
-      if (settle && !has_out && lane_f64(q_last, ll) < 0.5) return {P, n};
       continue;
     }
     const bool is_stop = __builtin_amdgcn_readlane((int)my_stop, Lf) != 0;

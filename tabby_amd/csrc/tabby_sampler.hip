@@ -1660,7 +1660,18 @@ __global__ __launch_bounds__(kBlock) void head_plan_kernel(Launch L, Workspace W
   };
   for (int b = threadIdx.x; b < kHeadBuckets; b += kBlock) sm.hist[b] = 0u;
   __syncthreads();
-  for (int i = threadIdx.x; i < H; i += kBlock) atomicAdd(&sm.hist[bucket_of(head[i])], 1u);
+  constexpr int B = 8;  // global loads in flight per lane
+  for (int base0 = 0; base0 < H; base0 += B * kBlock) {
+    uint64_t v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = base0 + u * kBlock + (int)threadIdx.x;
+      v[u] = i < H ? head[i] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (base0 + u * kBlock + (int)threadIdx.x < H) atomicAdd(&sm.hist[bucket_of(v[u])], 1u);
+  }
   __syncthreads();
   // Exclusive scan of the bucket counts: 16 buckets per thread, then across threads.
   constexpr int kPer = kHeadBuckets / kBlock;
@@ -1690,9 +1701,16 @@ __global__ __launch_bounds__(kBlock) void head_plan_kernel(Launch L, Workspace W
   }
   // Scatter into bucket order (unsorted within a bucket).
   __syncthreads();
-  for (int i = threadIdx.x; i < H; i += kBlock) {
-    const uint64_t v = head[i];
-    sorted[atomicAdd(&sm.start[bucket_of(v)], 1u)] = v;
+  for (int base0 = 0; base0 < H; base0 += B * kBlock) {
+    uint64_t v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = base0 + u * kBlock + (int)threadIdx.x;
+      v[u] = i < H ? head[i] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (base0 + u * kBlock + (int)threadIdx.x < H) sorted[atomicAdd(&sm.start[bucket_of(v[u])], 1u)] = v[u];
   }
 }
 
@@ -1732,7 +1750,9 @@ __global__ __launch_bounds__(kBlock) void head_sort_kernel(Launch L, Workspace W
     double pool_part = 0.0, e_part = 0.0;
     for (int i = threadIdx.x; i < n; i += kBlock) {
       const double d = (double)value_of(composite_key(src[i])) - (double)rs.max;
-      const double e = fdlibm_exp(d);
+      // poolMass and the head's share of sum-exp are compared within 1e-5: an f32 exp2 will
+      // do (the exact V8 exp is kept for the weights, which decide the draw).
+      const double e = (double)__builtin_amdgcn_exp2f((float)(d * 1.4426950408889634));
       pool_part += e / rs.sum_exp;
       e_part += e;
       sg[i] = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
