@@ -953,7 +953,9 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   // has to merge sorted lists.
   int keep = 0;
   if (kk > 0) {
-    if (count > 2 * kk || count > 4 * kWaveSize) {
+    // Prune when the list is longer than kk's register class: the sort then stays in the
+    // fewest registers (one for kk <= 64).
+    if (count > kWaveSize * ((kk + kWaveSize - 1) / kWaveSize)) {
       const Pruned pr = wave_prune_any(sm, count, kk, theta_key);
       count = __builtin_amdgcn_readfirstlane(pr.count);
     }
@@ -1264,7 +1266,8 @@ __device__ __forceinline__ RowStats row_stats(const SliceStat *stats, int splits
   double part = 0.0;
 #pragma unroll
   for (int q = 0; q < kMaxSplits / kWaveSize; ++q)
-    if (st[q].max != -INFINITY) part += st[q].sum * fdlibm_exp_inline((double)st[q].max - (double)out.max);
+    if (st[q].max != -INFINITY)  // sum-exp is compared within 1e-5: an f32 exp2 rescale will do
+      part += st[q].sum * (double)__builtin_amdgcn_exp2f((st[q].max - out.max) * kLog2e);
   out.sum_exp = wave_sum(part);
   return out;
 }
