@@ -1194,13 +1194,15 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Kernel 2 for pools of at most 256 (wave_merge_kernel): one wave per row. Every slice left
-// its top min(kk, count) candidates sorted descending, so the row's top-k is a merge of
-// sorted lists: the accumulator (the first list) and each further list, loaded reversed, give
-// max(a_i, b_(n-1-i)) -- the top n of their union as a bitonic sequence -- which a bitonic
-// clean (register strides, then lane strides through DPP / permlane) sorts again. The slice
-// statistics and the head of every list are loaded in one round trip; the f64 tail of
-// sampleFromTopK then runs from LDS, its sequential sums on one lane.
+// Kernel 2 for pools of at most 256 (wave_merge_kernel): one 256-lane workgroup per row.
+// Every slice left its top min(kk, count) candidates sorted descending, so the row's top-k is
+// a merge of sorted lists: the accumulator (the first list) and each further list, loaded
+// reversed, give max(a_i, b_(n-1-i)) -- the top n of their union as a bitonic sequence --
+// which a bitonic clean (register strides, then lane strides through DPP / permlane) sorts
+// again. Each wave merges a quarter of the lists, then a two-level tree through LDS. The
+// slice statistics and the head of every list are loaded in one round trip; the f64 tail of
+// sampleFromTopK then runs from LDS: the two independent sums on two waves, the running sums
+// on one, each evaluated bit-exactly by the whole wave (seqsum.h).
 // ---------------------------------------------------------------------------------------
 struct WaveMergeSmem {
   uint64_t sorted[kWaveKcap];
