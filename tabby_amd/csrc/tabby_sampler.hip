@@ -2050,15 +2050,17 @@ struct Plan {
 };
 
 // Enough slices per row that the batch fills the chip about once: 256 CUs x 5 resident
-// 256-lane workgroups, or x 12 one-wave workgroups for the wave kernel (fewer, longer
-// slices amortize each wave's selection work; the streaming rate is the same). Each
+// 256-lane workgroups, or 256 CUs x 4 SIMDs x 4 one-wave workgroups for the wave kernel
+// (measured at 256 rows: 16 slices per row, 39.9 us per call, beat 12 per row, 41.4 us --
+// the SIMDs issue their oldest wave first and a fourth wave hides more of the others'
+// waits -- and 18 or 20 per row, which no longer fit at once, ~50 us). Each
 // slice is at least one chunk long (two for the wave kernel) and aligned to the vector
 // loads. A row's wave slices are capped at kMaxWaveSplits: with few rows the chip is idle
 // anyway and the latency is one slice's chain plus the merge, whose cost grows with the
 // number of lists (measured on one row: 24 slices of 2048 beat 12 of 4096 and 48 of 1024
 // at vocab 49152; 37 slices of 4096 beat 46 and 74 at vocab 151936).
 constexpr int kTargetGroups = 1280;
-constexpr int kTargetWaves = 3072;
+constexpr int kTargetWaves = 4096;
 constexpr int kMaxWaveSplits = 36;
 
 Plan make_plan(int rows, int vocab, int dtype, const void *logits, bool wave) {
