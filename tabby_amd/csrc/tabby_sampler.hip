@@ -1298,6 +1298,7 @@ struct ListMerger {
   int slice_len;
   int64_t row_stride;
   int s_begin, s_end;
+  bool tree;  // at most 4 lists: loaded alternately descending and reversed for finish_tree
   uint64_t acc[R];
   uint64_t raw[kBatch][R];
 
@@ -1324,7 +1325,44 @@ struct ListMerger {
     if (s_begin < s_end) issue(s_begin, acc, false);
 #pragma unroll
     for (int q = 0; q < kBatch; ++q)
-      if (s_begin + 1 + q < s_end) issue(s_begin + 1 + q, raw[q], true);
+      if (s_begin + 1 + q < s_end) issue(s_begin + 1 + q, raw[q], !tree || (q & 1) == 0);
+  }
+  // The top 64 of at most four lists (R == 1) by a two-level tree: lists 0 and 1, and 2 and
+  // 3, merge side by side (the first pair cleaned descending, the second ascending, so that
+  // the two results again form a bitonic sequence), then the pair results merge.
+  template <class CountOf>
+  __device__ __forceinline__ void finish_tree(CountOf count_of) {
+    static_assert(R == 1, "one register per list");
+    const int n = s_end - s_begin;
+    uint64_t v[4] = {0ull, 0ull, 0ull, 0ull};
+    if (n > 0) {
+      v[0] = acc[0];
+      uint64_t t[1] = {v[0]};
+      mask(count_of(s_begin), t, false);
+      v[0] = t[0];
+    }
+#pragma unroll
+    for (int j = 1; j < 4; ++j) {
+      if (j < n) {
+        uint64_t t[1] = {raw[j - 1][0]};
+        mask(count_of(s_begin + j), t, (j & 1) != 0);
+        v[j] = t[0];
+      }
+    }
+    uint64_t a = tmax(v[0], v[1]), b = tmax(v[2], v[3]);
+    const int lane = wave_lane();
+    if (n > 2) {
+#pragma unroll
+      for (int stride = kWaveSize / 2; stride > 0; stride >>= 1) {
+        const uint64_t oa = xor_lane_by(a, stride), ob = xor_lane_by(b, stride);
+        const bool lower = (lane & stride) == 0;
+        a = lower ? tmax(a, oa) : tmin(a, oa);  // descending
+        b = lower ? tmin(b, ob) : tmax(b, ob);  // ascending
+      }
+      a = tmax(a, b);
+    }
+    acc[0] = a;
+    if (n > 1) bitonic_clean_desc<1>(acc);
   }
   template <class CountOf>
   __device__ __forceinline__ void finish(CountOf count_of) {
@@ -1426,7 +1464,11 @@ template <int R, class CountOf>
 __device__ __forceinline__ void merge_lists_4(WaveMergeSmem &sm, ListMerger<R> &mg, CountOf count_of,
                                               int K) {
   const int w = wave_id(), lane = wave_lane();
-  mg.finish(count_of);
+  if constexpr (R == 1) {
+    if (mg.tree) mg.finish_tree(count_of); else mg.finish(count_of);
+  } else {
+    mg.finish(count_of);
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) sm.part[w][r * kWaveSize + lane] = mg.acc[r];
   __syncthreads();
@@ -1457,6 +1499,7 @@ __device__ __forceinline__ ListMerger<R> lists_of_wave(const uint64_t *lists, co
   mg.row_stride = W.row_cand_stride;
   mg.s_begin = min(wave_id() * per, L.splits);
   mg.s_end = min(mg.s_begin + per, L.splits);
+  mg.tree = R == 1 && per <= 4;
   return mg;
 }
 
