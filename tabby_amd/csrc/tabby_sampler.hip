@@ -855,15 +855,20 @@ __device__ __forceinline__ Pruned wave_prune_any(WaveSmem &sm, int count, int kk
   return wave_prune<8>(sm, count, kk, floor_key);
 }
 
-template <typename In, int VEC>
-__global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) {
-  __shared__ WaveSmem sm;
-
-  int row, slice;
-  row_slice_of((int)blockIdx.x, L.rows, L.splits, row, slice);
+// One wave's share of row `row`: slice `slice` of L.slice_len elements or, when `claim` is
+// given (CLAIM), chunk `slice` of the whole row and then every chunk the wave claims from the
+// LDS counter *claim (shared by the row's waves, starting past their first chunks), so that
+// the row's waves end together however the SIMDs schedule them. Every statistic and list of
+// the wave is independent of which elements it saw: the max, sum-exp to 1e-5, and a
+// superset of the top kk of its elements. The wave's top min(count, kk), sorted descending,
+// go to out[0..keep) as composites (out may be sm.list itself: the list is read into
+// registers before anything is written), its statistics to *stat.
+template <typename In, int VEC, bool CLAIM>
+__device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, int row, int slice, uint64_t *out,
+                                           SliceStat *stat, int *claim) {
   const int V = L.vocab;
-  const int begin = slice * L.slice_len;
-  const int n = min(L.slice_len, V - begin);
+  const int begin = CLAIM ? 0 : slice * L.slice_len;
+  const int n = CLAIM ? V : min(L.slice_len, V - begin);
   const int nchunks = (n + kWChunk - 1) / kWChunk;
   const int full_chunks = n / kWChunk;
   const tabby_row_params P = L.params[row];
@@ -871,7 +876,6 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   const int keff = effective_k(P, V);
   const int kk = slice_keep(valid_params, keff, n, L.kcap, L.head_pass, L.topk_cap);
   const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
-  uint64_t *region = W.cands + (size_t)row * W.row_cand_stride + (size_t)begin;
   const int prune_at = kWListCap - kWaveSize;
 
   float lane_max = -INFINITY;
@@ -880,10 +884,10 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   uint32_t theta_key = kNegInfKey;
   float theta = -INFINITY;  // == value_of(theta_key)
 
-  // Processes chunk c held in `cur` while chunk c + 1, if any, loads into `nxt`. (A load past
-  // the last chunk would be waited for by the end-of-slice prune.)
-  auto step = [&](int c, float (&cur)[kWChunkPerLane], float (&nxt)[kWChunkPerLane]) {
-    const int nc = c + 1;
+  // Processes chunk c held in `cur` while chunk nc, if any, loads into `nxt`. (A load past
+  // the last chunk would be waited for by the end-of-slice prune.) `first`: the wave's first
+  // chunk.
+  auto step = [&](int c, int nc, bool first, float (&cur)[kWChunkPerLane], float (&nxt)[kWChunkPerLane]) {
     if (nc < full_chunks) wave_load_full<In, VEC>(src, nc, nxt);
     else if (nc < nchunks) wave_load<In, VEC>(src, n, nc, nxt);
     const bool partial = c >= full_chunks;  // only the slice's last chunk can be partial
@@ -906,7 +910,7 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
       lane_max = nm;
     }
     if (kk == 0) return;
-    if (c == 0 && kk < n && kk <= kWaveSize) {
+    if (first && kk < n && kk <= kWaveSize) {
       uint32_t k1[1] = {key_of(cm)};
       wave_sort_desc<1>(k1);
       theta_key = min(max((uint32_t)__builtin_amdgcn_readlane((int)k1[0], kk - 1), kNegInfKey), 0xff800000u);
@@ -938,10 +942,30 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   };
 
   float x[kWChunkPerLane], y[kWChunkPerLane];
-  if (full_chunks > 0) wave_load_full<In, VEC>(src, 0, x); else wave_load<In, VEC>(src, n, 0, x);
-  for (int c = 0; c < nchunks; c += 2) {
-    step(c, x, y);
-    if (c + 1 < nchunks) step(c + 1, y, x);
+  if constexpr (CLAIM) {
+    auto next = [&]() {
+      int c = 0;
+      if (wave_lane() == 0) c = atomicAdd(claim, 1);
+      return __builtin_amdgcn_readfirstlane(c);
+    };
+    int a = slice;
+    if (a < full_chunks) wave_load_full<In, VEC>(src, a, x);
+    else if (a < nchunks) wave_load<In, VEC>(src, n, a, x);
+    bool first = true;
+    while (a < nchunks) {
+      const int b = next();
+      step(a, b, first, x, y);
+      first = false;
+      if (b >= nchunks) break;
+      a = next();
+      step(b, a, false, y, x);
+    }
+  } else {
+    if (full_chunks > 0) wave_load_full<In, VEC>(src, 0, x); else wave_load<In, VEC>(src, n, 0, x);
+    for (int c = 0; c < nchunks; c += 2) {
+      step(c, c + 1, c == 0, x, y);
+      if (c + 1 < nchunks) step(c + 1, c + 2, false, y, x);
+    }
   }
 
   const float ms = wave_max(lane_max);
@@ -949,8 +973,8 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
                           ? 0.0
                           : lane_sum * (double)__builtin_amdgcn_exp2f((lane_max - ms) * kLog2e);
   const double ss = wave_sum(term);
-  // The slice's top min(count, kk), sorted descending, go to its region: the merge only
-  // has to merge sorted lists.
+  // The slice's top min(count, kk), sorted descending: the merge only has to merge sorted
+  // lists.
   int keep = 0;
   if (kk > 0) {
     // Prune when the list is longer than kk's register class: the sort then stays in the
@@ -961,18 +985,28 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
     }
     keep = min(count, kk);
     wave_lds_sync();
-    if (count <= kWaveSize) store_sorted_top<1>(sm.list, count, keep, region);
-    else if (count <= 2 * kWaveSize) store_sorted_top<2>(sm.list, count, keep, region);
-    else if (count <= 4 * kWaveSize) store_sorted_top<4>(sm.list, count, keep, region);
-    else store_sorted_top<8>(sm.list, count, keep, region);
+    if (count <= kWaveSize) store_sorted_top<1>(sm.list, count, keep, out);
+    else if (count <= 2 * kWaveSize) store_sorted_top<2>(sm.list, count, keep, out);
+    else if (count <= 4 * kWaveSize) store_sorted_top<4>(sm.list, count, keep, out);
+    else store_sorted_top<8>(sm.list, count, keep, out);
   }
   if (wave_lane() == 0) {
     SliceStat st_out;
     st_out.max = ms;
     st_out.count = (uint32_t)keep;
     st_out.sum = ss;
-    W.stats[(size_t)row * kMaxSplits + slice] = st_out;
+    *stat = st_out;
   }
+}
+
+template <typename In, int VEC>
+__global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) {
+  __shared__ WaveSmem sm;
+  int row, slice;
+  row_slice_of((int)blockIdx.x, L.rows, L.splits, row, slice);
+  wave_slice<In, VEC, false>(sm, L, row, slice,
+                             W.cands + (size_t)row * W.row_cand_stride + (size_t)slice * L.slice_len,
+                             W.stats + (size_t)row * kMaxSplits + slice, nullptr);
 }
 
 // Smallest key whose scaled logit (l - max)/T in f64 is >= -37.5 (the max's key when T <= 0:
@@ -1457,9 +1491,9 @@ __device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch
   }
 }
 
-// The four waves of the workgroup each merge a quarter of the row's lists (their loads
-// issued by the caller); then a two-level tree through LDS merges the four results into
-// sm.sorted[0..K).
+// The first four waves of the workgroup each merge a quarter of the row's lists (their
+// loads issued by the caller); then a two-level tree through LDS merges the four results
+// into sm.sorted[0..K). Further waves only take part in the barriers.
 template <int R, class CountOf>
 __device__ __forceinline__ void merge_lists_4(WaveMergeSmem &sm, ListMerger<R> &mg, CountOf count_of,
                                               int K) {
@@ -1469,8 +1503,10 @@ __device__ __forceinline__ void merge_lists_4(WaveMergeSmem &sm, ListMerger<R> &
   } else {
     mg.finish(count_of);
   }
+  if (w < kWaves) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) sm.part[w][r * kWaveSize + lane] = mg.acc[r];
+    for (int r = 0; r < R; ++r) sm.part[w][r * kWaveSize + lane] = mg.acc[r];
+  }
   __syncthreads();
   if (w == 0 || w == 2) {
     merge_with<R>(mg.acc, sm.part[w + 1]);
@@ -1489,34 +1525,40 @@ __device__ __forceinline__ void merge_lists_4(WaveMergeSmem &sm, ListMerger<R> &
   __syncthreads();
 }
 
+// Where a row's lists lie: list s at base + s * stride, all inside base[0..room).
+struct RowLists {
+  const uint64_t *base;
+  int count;
+  int stride;
+  int64_t room;
+};
+
 template <int R>
-__device__ __forceinline__ ListMerger<R> lists_of_wave(const uint64_t *lists, const Launch &L,
-                                                       const Workspace &W) {
-  const int per = (L.splits + kWaves - 1) / kWaves;
+__device__ __forceinline__ ListMerger<R> lists_of_wave(const RowLists &rl) {
+  const int per = (rl.count + kWaves - 1) / kWaves;
   ListMerger<R> mg;
-  mg.base = lists;
-  mg.slice_len = L.slice_len;
-  mg.row_stride = W.row_cand_stride;
-  mg.s_begin = min(wave_id() * per, L.splits);
-  mg.s_end = min(mg.s_begin + per, L.splits);
+  mg.base = rl.base;
+  mg.slice_len = rl.stride;
+  mg.row_stride = rl.room;
+  mg.s_begin = min(wave_id() * per, rl.count);  // waves past the fourth get no lists
+  mg.s_end = min(mg.s_begin + per, rl.count);
   mg.tree = R == 1 && per <= 4;
   return mg;
 }
 
+// Merges row `row`'s sorted slice lists and statistics and finishes the row (at least four
+// waves; the lists and statistics are in global memory or in LDS).
 template <typename In>
-__global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace W) {
-  __shared__ WaveMergeSmem sm;
-  const int row = (int)blockIdx.x;
+__device__ __forceinline__ void merge_row(WaveMergeSmem &sm, const Launch &L, const Workspace &W, int row,
+                                          const SliceStat *stats, const RowLists &lists) {
   const int lane = wave_lane();
   const int V = L.vocab;
-  const SliceStat *stats = W.stats + (size_t)row * kMaxSplits;
-  const uint64_t *lists = W.cands + (size_t)row * W.row_cand_stride;
   // The lists' first 64 entries are loaded before the parameters are known: pools of at
   // most 64 (the common case) then need no second round trip.
-  ListMerger<1> m1 = lists_of_wave<1>(lists, L, W);
+  ListMerger<1> m1 = lists_of_wave<1>(lists);
   m1.start();
   const tabby_row_params P = L.params[row];
-  const RowStats rs = row_stats(stats, L.splits);
+  const RowStats rs = row_stats(stats, lists.count);
   auto count_of = [&](int s) { return list_count(rs, s); };
   const bool valid_params = params_valid(P, L.k_max);
   const int keff = effective_k(P, V);
@@ -1528,11 +1570,11 @@ __global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace 
     if (K <= kWaveSize) {
       merge_lists_4<1>(sm, m1, count_of, K);
     } else if (K <= 2 * kWaveSize) {
-      ListMerger<2> m2 = lists_of_wave<2>(lists, L, W);
+      ListMerger<2> m2 = lists_of_wave<2>(lists);
       m2.start();
       merge_lists_4<2>(sm, m2, count_of, K);
     } else {
-      ListMerger<4> m4 = lists_of_wave<4>(lists, L, W);
+      ListMerger<4> m4 = lists_of_wave<4>(lists);
       m4.start();
       merge_lists_4<4>(sm, m4, count_of, K);
     }
@@ -1588,6 +1630,46 @@ __global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace 
     return;
   }
   wave_tail<In>(sm, K, L, row, row_src, row_max, sum_exp, P);
+}
+
+template <typename In>
+__global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace W) {
+  __shared__ WaveMergeSmem sm;
+  const int row = (int)blockIdx.x;
+  const RowLists lists{W.cands + (size_t)row * W.row_cand_stride, L.splits, L.slice_len, W.row_cand_stride};
+  merge_row<In>(sm, L, W, row, W.stats + (size_t)row * kMaxSplits, lists);
+}
+
+// ---------------------------------------------------------------------------------------
+// Batches of at least as many rows as the chip has CUs (pools of at most 256): one
+// workgroup per row of L.splits <= kRowWaves waves, which take the row's chunks from an LDS
+// counter (wave_slice with CLAIM) and leave their sorted lists and statistics in LDS; after
+// one barrier the workgroup merges them as wave_merge_kernel does. Nothing goes through
+// global memory between the two halves, the row finishes as soon as its own chunks are done
+// instead of after every row's, and its waves end within about a chunk of each other (with
+// fixed slices, the SIMDs' oldest-first issue left the youngest waves ~8 us behind).
+// ---------------------------------------------------------------------------------------
+constexpr int kRowWaves = 16;
+
+struct RowSmem {
+  WaveSmem wave[kRowWaves];
+  SliceStat stats[kRowWaves];
+  WaveMergeSmem merge;
+  int next_chunk;
+};
+
+template <typename In, int VEC>
+__global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Workspace W) {
+  __shared__ RowSmem sm;
+  const int row = (int)blockIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  if (threadIdx.x == 0) sm.next_chunk = L.splits;  // chunk w is wave w's first
+  __syncthreads();
+  wave_slice<In, VEC, true>(sm.wave[w], L, row, w, sm.wave[w].list, &sm.stats[w], &sm.next_chunk);
+  __syncthreads();
+  constexpr int stride = (int)(sizeof(WaveSmem) / sizeof(uint64_t));
+  const RowLists lists{sm.wave[0].list, L.splits, stride, (int64_t)L.splits * stride};
+  merge_row<In>(sm.merge, L, W, row, sm.stats, lists);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2053,6 +2135,7 @@ using namespace tabby;
 
 struct tabby_sampler {
   int device = 0;
+  int cus = 0;  // compute units of the device
   int32_t vocab_max = 0, rows_max = 0, k_max = 0;
   Workspace ws{};
   void *ws_base = nullptr;
@@ -2122,10 +2205,16 @@ Plan make_plan(int rows, int vocab, int dtype, const void *logits, bool wave) {
   return p;
 }
 
+// One workgroup per row (row_kernel) once the rows alone fill the CUs and a row's slices
+// fit one workgroup.
+bool per_row_launch(const Launch &L, int cus) { return L.kcap <= kWaveKcap && L.rows >= cus && L.splits <= kRowWaves; }
+
 template <typename In, int VEC>
-hipError_t launch_pair(const Launch &L, const Workspace &W, hipStream_t stream) {
+hipError_t launch_pair(const Launch &L, const Workspace &W, int cus, hipStream_t stream) {
   const dim3 slices((unsigned)(L.rows * L.splits)), rows((unsigned)L.rows);
-  if (L.kcap <= kWaveKcap) {
+  if (per_row_launch(L, cus)) {
+    hipLaunchKernelGGL((row_kernel<In, VEC>), rows, dim3((unsigned)(L.splits * kWaveSize)), 0, stream, L, W);
+  } else if (L.kcap <= kWaveKcap) {
     hipLaunchKernelGGL((wave_kernel<In, VEC>), slices, dim3(kWaveSize), 0, stream, L, W);
     hipLaunchKernelGGL((wave_merge_kernel<In>), rows, dim3(kBlock), 0, stream, L, W);
   } else {
@@ -2146,14 +2235,14 @@ hipError_t launch_head(const Launch &L, const Workspace &W, hipStream_t stream) 
   return hipGetLastError();
 }
 
-hipError_t dispatch(int dtype, const Plan &p, const Launch &L, const Workspace &W, hipStream_t s) {
+hipError_t dispatch(int dtype, const Plan &p, const Launch &L, const Workspace &W, int cus, hipStream_t s) {
   hipError_t e;
   if (dtype == TABBY_F32) {
-    e = p.vec == 4 ? launch_pair<float, 4>(L, W, s) : launch_pair<float, 1>(L, W, s);
+    e = p.vec == 4 ? launch_pair<float, 4>(L, W, cus, s) : launch_pair<float, 1>(L, W, cus, s);
     if (e == hipSuccess && L.head_pass) e = p.vec == 4 ? launch_head<float, 4>(L, W, s) : launch_head<float, 1>(L, W, s);
     return e;
   }
-  e = p.vec == 8 ? launch_pair<uint16_t, 8>(L, W, s) : launch_pair<uint16_t, 1>(L, W, s);
+  e = p.vec == 8 ? launch_pair<uint16_t, 8>(L, W, cus, s) : launch_pair<uint16_t, 1>(L, W, cus, s);
   if (e == hipSuccess && L.head_pass) e = p.vec == 8 ? launch_head<uint16_t, 8>(L, W, s) : launch_head<uint16_t, 1>(L, W, s);
   return e;
 }
@@ -2189,9 +2278,12 @@ int tabby_sampler_create(int device, int32_t vocab_max, int32_t rows_max, int32_
   if (k_max < 1 || k_max > kKcapLarge)
     return fail(TABBY_ECAPACITY, "k_max must be between 1 and " + std::to_string(kKcapLarge));
   HIP_TRY(hipSetDevice(device));
+  int cus = 0;
+  HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
 
   tabby_sampler *h = new tabby_sampler();
   h->device = device;
+  h->cus = cus;
   h->vocab_max = vocab_max;
   h->rows_max = rows_max;
   h->k_max = k_max;
@@ -2309,7 +2401,7 @@ int tabby_sampler_sample_device(tabby_sampler *h, const void *logits_dev, int32_
   L.h_splits = hp.splits;
   L.h_slice_len = hp.slice_len;
   HIP_TRY(hipSetDevice(h->device));
-  HIP_TRY(dispatch(dtype, p, L, h->ws, (hipStream_t)stream));
+  HIP_TRY(dispatch(dtype, p, L, h->ws, h->cus, (hipStream_t)stream));
   return TABBY_OK;
 }
 
