@@ -864,14 +864,13 @@ __device__ __forceinline__ Pruned wave_prune_any(WaveSmem &sm, int count, int kk
 // go to out[0..keep) as composites (out may be sm.list itself: the list is read into
 // registers before anything is written), its statistics to *stat.
 template <typename In, int VEC, bool CLAIM>
-__device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, int row, int slice, uint64_t *out,
-                                           SliceStat *stat, int *claim) {
+__device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const tabby_row_params &P, int row,
+                                           int slice, uint64_t *out, SliceStat *stat, int *claim) {
   const int V = L.vocab;
   const int begin = CLAIM ? 0 : slice * L.slice_len;
   const int n = CLAIM ? V : min(L.slice_len, V - begin);
   const int nchunks = (n + kWChunk - 1) / kWChunk;
   const int full_chunks = n / kWChunk;
-  const tabby_row_params P = L.params[row];
   const bool valid_params = params_valid(P, L.k_max);
   const int keff = effective_k(P, V);
   const int kk = slice_keep(valid_params, keff, n, L.kcap, L.head_pass, L.topk_cap);
@@ -1004,7 +1003,8 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   __shared__ WaveSmem sm;
   int row, slice;
   row_slice_of((int)blockIdx.x, L.rows, L.splits, row, slice);
-  wave_slice<In, VEC, false>(sm, L, row, slice,
+  const tabby_row_params P = L.params[row];
+  wave_slice<In, VEC, false>(sm, L, P, row, slice,
                              W.cands + (size_t)row * W.row_cand_stride + (size_t)slice * L.slice_len,
                              W.stats + (size_t)row * kMaxSplits + slice, nullptr);
 }
@@ -1266,8 +1266,7 @@ __device__ __forceinline__ void bitonic_clean_desc(uint64_t (&a)[R]) {
   for (int stride = kWaveSize / 2; stride > 0; stride >>= 1) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint64_t o = xor_lane_by(a[r], stride);
-      a[r] = (lane & stride) == 0 ? tmax(a[r], o) : tmin(a[r], o);
+      a[r] = cmpx(a[r], xor_lane_by(a[r], stride), (lane & stride) == 0);
     }
   }
 }
@@ -1390,8 +1389,8 @@ struct ListMerger {
       for (int stride = kWaveSize / 2; stride > 0; stride >>= 1) {
         const uint64_t oa = xor_lane_by(a, stride), ob = xor_lane_by(b, stride);
         const bool lower = (lane & stride) == 0;
-        a = lower ? tmax(a, oa) : tmin(a, oa);  // descending
-        b = lower ? tmin(b, ob) : tmax(b, ob);  // ascending
+        a = cmpx(a, oa, lower);   // descending
+        b = cmpx(b, ob, !lower);  // ascending
       }
       a = tmax(a, b);
     }
@@ -1546,26 +1545,42 @@ __device__ __forceinline__ ListMerger<R> lists_of_wave(const RowLists &rl) {
   return mg;
 }
 
+// The pool a row's merge builds: its top-k, or for a whole-vocabulary row the caller's
+// top-k list (finished later by the head kernels).
+struct RowPool {
+  bool valid;   // parameters valid
+  bool finite;  // the pool is the row's top-k (not a whole-vocabulary row)
+  int K;        // pool entries to merge
+};
+
+__device__ __forceinline__ RowPool row_pool(const Launch &L, const tabby_row_params &P) {
+  RowPool rp;
+  rp.valid = params_valid(P, L.k_max);
+  const int keff = effective_k(P, L.vocab);
+  rp.finite = rp.valid && keff <= L.kcap;
+  rp.K = !rp.valid ? 0 : rp.finite ? keff : L.head_pass ? min(L.topk_cap, L.vocab) : 0;
+  return rp;
+}
+
+template <typename In>
+__device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, const Workspace &W, int row,
+                                            const tabby_row_params &P, const RowPool &rp, float row_max,
+                                            double sum_exp);
+
 // Merges row `row`'s sorted slice lists and statistics and finishes the row (at least four
-// waves; the lists and statistics are in global memory or in LDS).
+// waves; the lists and statistics are in global memory or in LDS; P is the row's parameters).
 template <typename In>
 __device__ __forceinline__ void merge_row(WaveMergeSmem &sm, const Launch &L, const Workspace &W, int row,
-                                          const SliceStat *stats, const RowLists &lists) {
-  const int lane = wave_lane();
-  const int V = L.vocab;
-  // The lists' first 64 entries are loaded before the parameters are known: pools of at
-  // most 64 (the common case) then need no second round trip.
+                                          const tabby_row_params &P, const SliceStat *stats,
+                                          const RowLists &lists) {
+  // The lists' first 64 entries are loaded before the pool size is known: pools of at most
+  // 64 (the common case) then need no second round trip.
   ListMerger<1> m1 = lists_of_wave<1>(lists);
   m1.start();
-  const tabby_row_params P = L.params[row];
   const RowStats rs = row_stats(stats, lists.count);
   auto count_of = [&](int s) { return list_count(rs, s); };
-  const bool valid_params = params_valid(P, L.k_max);
-  const int keff = effective_k(P, V);
-  const bool finite = valid_params && keff <= L.kcap;
-  const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V;
-  // Pool to merge: the row's top-k, or for a whole-vocabulary row the caller's top-k list.
-  const int K = !valid_params ? 0 : finite ? keff : L.head_pass ? min(L.topk_cap, V) : 0;
+  const RowPool rp = row_pool(L, P);
+  const int K = rp.K;
   if (K > 0) {
     if (K <= kWaveSize) {
       merge_lists_4<1>(sm, m1, count_of, K);
@@ -1579,8 +1594,20 @@ __device__ __forceinline__ void merge_row(WaveMergeSmem &sm, const Launch &L, co
       merge_lists_4<4>(sm, m4, count_of, K);
     }
   }
-  const float row_max = rs.max;
-  const double sum_exp = rs.sum_exp;
+  finish_pool<In>(sm, L, W, row, P, rp, rs.max, rs.sum_exp);
+}
+
+// The rest of a row once its pool, sm.sorted[0..K), and its max and sum-exp are known: the
+// f64 tail of sampleFromTopK, the hand-over to the head kernels, or an error status. Wave 0
+// and wave 1 work; every wave of the workgroup must call it.
+template <typename In>
+__device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, const Workspace &W, int row,
+                                            const tabby_row_params &P, const RowPool &rp, float row_max,
+                                            double sum_exp) {
+  const int lane = wave_lane();
+  const int K = rp.K;
+  const bool valid_params = rp.valid, finite = rp.finite;
+  const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * L.vocab;
   const bool in_domain = (row_max > -INFINITY) && (row_max < INFINITY) && (sum_exp > 0.0) &&
                          (sum_exp < INFINITY);
   if (valid_params && in_domain && finite) {
@@ -1637,7 +1664,8 @@ __global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace 
   __shared__ WaveMergeSmem sm;
   const int row = (int)blockIdx.x;
   const RowLists lists{W.cands + (size_t)row * W.row_cand_stride, L.splits, L.slice_len, W.row_cand_stride};
-  merge_row<In>(sm, L, W, row, W.stats + (size_t)row * kMaxSplits, lists);
+  const tabby_row_params P = L.params[row];
+  merge_row<In>(sm, L, W, row, P, W.stats + (size_t)row * kMaxSplits, lists);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1648,6 +1676,9 @@ __global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace 
 // global memory between the two halves, the row finishes as soon as its own chunks are done
 // instead of after every row's, and its waves end within about a chunk of each other (with
 // fixed slices, the SIMDs' oldest-first issue left the youngest waves ~8 us behind).
+// (A tournament -- each finished wave merging with its sibling through an LDS counter, so
+// that the lower levels overlap the last waves' streaming -- was measured slower: each level
+// is a chain of dependent LDS round trips before its merge.)
 // ---------------------------------------------------------------------------------------
 constexpr int kRowWaves = 16;
 
@@ -1663,13 +1694,14 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   __shared__ RowSmem sm;
   const int row = (int)blockIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const tabby_row_params P = L.params[row];  // kept in registers for the merge
   if (threadIdx.x == 0) sm.next_chunk = L.splits;  // chunk w is wave w's first
   __syncthreads();
-  wave_slice<In, VEC, true>(sm.wave[w], L, row, w, sm.wave[w].list, &sm.stats[w], &sm.next_chunk);
+  wave_slice<In, VEC, true>(sm.wave[w], L, P, row, w, sm.wave[w].list, &sm.stats[w], &sm.next_chunk);
   __syncthreads();
   constexpr int stride = (int)(sizeof(WaveSmem) / sizeof(uint64_t));
   const RowLists lists{sm.wave[0].list, L.splits, stride, (int64_t)L.splits * stride};
-  merge_row<In>(sm.merge, L, W, row, sm.stats, lists);
+  merge_row<In>(sm.merge, L, W, row, P, sm.stats, lists);
 }
 
 // ---------------------------------------------------------------------------------------

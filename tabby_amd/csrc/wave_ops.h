@@ -118,6 +118,12 @@ __device__ __forceinline__ T tmax(T a, T b) { return a > b ? a : b; }
 template <typename T>
 __device__ __forceinline__ T tmin(T a, T b) { return a < b ? a : b; }
 
+// One compare-exchange of a lane exchange: the larger of v and its partner's o where
+// keep_max, else the smaller. One compare and one select: for the lanes keeping the smaller
+// value the compare's lane mask is inverted (a scalar XOR; o == v needs no swap either way).
+template <typename T>
+__device__ __forceinline__ T cmpx(T v, T o, bool keep_max) { return ((o > v) == keep_max) ? o : v; }
+
 // The bitonic network's stages for one `size` over strides below 64*R, on the 64*R values
 // v[r] at global indices base + r*64 + lane (base a multiple of 64*R); the direction of each
 // pair is descending where (index & size) == 0, as in a descending sort of the whole array.
@@ -147,7 +153,7 @@ __device__ __forceinline__ void wave_bitonic_stages(T (&v)[R], int base, int siz
         const T o = xor_lane_by(v[r], stride);
         const bool lower = (lane & stride) == 0;
         const bool desc = ((base + r * kWaveSize + lane) & size) == 0;
-        v[r] = (lower == desc) ? tmax(v[r], o) : tmin(v[r], o);
+        v[r] = cmpx(v[r], o, lower == desc);
       }
     }
   }
@@ -180,7 +186,7 @@ __device__ __forceinline__ void wave_sort_desc(T (&v)[R]) {
           const T o = xor_lane_by(v[r], stride);
           const bool lower = (lane & stride) == 0;
           const bool desc = (((r * kWaveSize) | lane) & size) == 0;
-          v[r] = (lower == desc) ? tmax(v[r], o) : tmin(v[r], o);
+          v[r] = cmpx(v[r], o, lower == desc);
         }
       }
     }
