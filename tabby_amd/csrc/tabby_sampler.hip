@@ -567,9 +567,15 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
     const float nm = fmaxf(lane_max, cm);
     if (nm != -INFINITY) {
       const float ml = nm * kLog2e;
-      float part = 0.0f;
+      float t[kChunkPerLane];  // summed pairwise, as in the wave kernel
 #pragma unroll
-      for (int e = 0; e < kChunkPerLane; ++e) part += __builtin_amdgcn_exp2f(fmaf(x[e], kLog2e, -ml));
+      for (int e = 0; e < kChunkPerLane; ++e) t[e] = __builtin_amdgcn_exp2f(fmaf(x[e], kLog2e, -ml));
+#pragma unroll
+      for (int h = kChunkPerLane / 2; h > 0; h >>= 1) {
+#pragma unroll
+        for (int e = 0; e < h; ++e) t[e] += t[e + h];
+      }
+      const float part = t[0];
       const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f((lane_max - nm) * kLog2e);
       lane_sum = lane_sum * rescale + (double)part;
       lane_max = nm;
@@ -901,9 +907,17 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
     const float nm = fmaxf(lane_max, cm);
     if (nm != -INFINITY) {
       const float ml = nm * kLog2e;
-      float part = 0.0f;
+      // Pairwise sum: independent adds interleave with the exps (a running sum made one
+      // dependent chain of 16 exp-add pairs per chunk).
+      float t[kWChunkPerLane];
 #pragma unroll
-      for (int e = 0; e < kWChunkPerLane; ++e) part += __builtin_amdgcn_exp2f(fmaf(cur[e], kLog2e, -ml));
+      for (int e = 0; e < kWChunkPerLane; ++e) t[e] = __builtin_amdgcn_exp2f(fmaf(cur[e], kLog2e, -ml));
+#pragma unroll
+      for (int h = kWChunkPerLane / 2; h > 0; h >>= 1) {
+#pragma unroll
+        for (int e = 0; e < h; ++e) t[e] += t[e + h];
+      }
+      const float part = t[0];
       const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f((lane_max - nm) * kLog2e);
       lane_sum = lane_sum * rescale + (double)part;
       lane_max = nm;
