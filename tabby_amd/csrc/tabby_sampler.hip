@@ -866,12 +866,14 @@ __device__ __forceinline__ Pruned wave_prune_any(WaveSmem &sm, int count, int kk
 // LDS counter *claim (shared by the row's waves, starting past their first chunks), so that
 // the row's waves end together however the SIMDs schedule them. Every statistic and list of
 // the wave is independent of which elements it saw: the max, sum-exp to 1e-5, and a
-// superset of the top kk of its elements. The wave's top min(count, kk), sorted descending,
+// superset of the top kk of its elements. With CLAIM the row's waves also agree on a first
+// bound through *row_theta (an LDS word holding 0xffffffff before the call) and one barrier. The wave's top min(count, kk), sorted descending,
 // go to out[0..keep) as composites (out may be sm.list itself: the list is read into
 // registers before anything is written), its statistics to *stat.
 template <typename In, int VEC, bool CLAIM>
 __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const tabby_row_params &P, int row,
-                                           int slice, uint64_t *out, SliceStat *stat, int *claim) {
+                                           int slice, uint64_t *out, SliceStat *stat, int *claim,
+                                           uint32_t *row_theta) {
   const int V = L.vocab;
   const int begin = CLAIM ? 0 : slice * L.slice_len;
   const int n = CLAIM ? V : min(L.slice_len, V - begin);
@@ -961,17 +963,45 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
       if (wave_lane() == 0) c = atomicAdd(claim, 1);
       return __builtin_amdgcn_readfirstlane(c);
     };
-    int a = slice;
+    const int a = slice;
     if (a < full_chunks) wave_load_full<In, VEC>(src, a, x);
     else if (a < nchunks) wave_load<In, VEC>(src, n, a, x);
-    bool first = true;
-    while (a < nchunks) {
-      const int b = next();
-      step(a, b, first, x, y);
-      first = false;
-      if (b >= nchunks) break;
-      a = next();
-      step(b, a, false, y, x);
+    int b = next();
+    if (b < full_chunks) wave_load_full<In, VEC>(src, b, y);
+    else if (b < nchunks) wave_load<In, VEC>(src, n, b, y);
+    // The row's first bound, shared by its L.splits waves: wave w offers the kw-th largest of
+    // its first chunk's lane maxima, kw = ceil(kk / L.splits) -- kw distinct elements at or
+    // above it -- and the smallest offer has at least kk elements of the row at or above
+    // it, so it never exceeds the row's kk-th largest. (A wave alone could only offer the
+    // kk-th largest of its 64 lane maxima.) Every wave passes the barrier once.
+    {
+      const int kw = (kk + L.splits - 1) / L.splits;
+      uint32_t offer = kNegInfKey;
+      if (kk > 0 && kw <= kWaveSize && a < nchunks) {
+        if (a >= full_chunks) {
+#pragma unroll
+          for (int e = 0; e < kWChunkPerLane; ++e)
+            if (wave_local<VEC>(a, e) >= n) x[e] = -INFINITY;
+        }
+        float cm = x[0];
+#pragma unroll
+        for (int e = 1; e < kWChunkPerLane; ++e) cm = fmaxf(cm, x[e]);
+        uint32_t k1[1] = {key_of(cm)};
+        wave_sort_desc<1>(k1);
+        offer = min(max((uint32_t)__builtin_amdgcn_readlane((int)k1[0], kw - 1), kNegInfKey), 0xff800000u);
+      }
+      if (wave_lane() == 0) atomicMin(row_theta, offer);
+      __syncthreads();
+      theta_key = max(theta_key, (uint32_t)__builtin_amdgcn_readfirstlane((int)*row_theta));
+      theta = value_of(theta_key);
+    }
+    if (a < nchunks) step(a, nchunks, false, x, y);  // chunk b is already in flight
+    while (b < nchunks) {
+      const int c = next();
+      step(b, c, false, y, x);
+      if (c >= nchunks) break;
+      b = next();
+      step(c, b, false, x, y);
     }
   } else {
     if (full_chunks > 0) wave_load_full<In, VEC>(src, 0, x); else wave_load<In, VEC>(src, n, 0, x);
@@ -1020,7 +1050,7 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   const tabby_row_params P = L.params[row];
   wave_slice<In, VEC, false>(sm, L, P, row, slice,
                              W.cands + (size_t)row * W.row_cand_stride + (size_t)slice * L.slice_len,
-                             W.stats + (size_t)row * kMaxSplits + slice, nullptr);
+                             W.stats + (size_t)row * kMaxSplits + slice, nullptr, nullptr);
 }
 
 // Smallest key whose scaled logit (l - max)/T in f64 is >= -37.5 (the max's key when T <= 0:
@@ -1701,6 +1731,7 @@ struct RowSmem {
   SliceStat stats[kRowWaves];
   WaveMergeSmem merge;
   int next_chunk;
+  uint32_t row_theta;
 };
 
 template <typename In, int VEC>
@@ -1709,9 +1740,13 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   const int row = (int)blockIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
   const tabby_row_params P = L.params[row];  // kept in registers for the merge
-  if (threadIdx.x == 0) sm.next_chunk = L.splits;  // chunk w is wave w's first
+  if (threadIdx.x == 0) {
+    sm.next_chunk = L.splits;  // chunk w is wave w's first
+    sm.row_theta = 0xffffffffu;
+  }
   __syncthreads();
-  wave_slice<In, VEC, true>(sm.wave[w], L, P, row, w, sm.wave[w].list, &sm.stats[w], &sm.next_chunk);
+  wave_slice<In, VEC, true>(sm.wave[w], L, P, row, w, sm.wave[w].list, &sm.stats[w], &sm.next_chunk,
+                            &sm.row_theta);
   __syncthreads();
   constexpr int stride = (int)(sizeof(WaveSmem) / sizeof(uint64_t));
   const RowLists lists{sm.wave[0].list, L.splits, stride, (int64_t)L.splits * stride};
