@@ -228,9 +228,10 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": ("one tabby_sampler_sample_device call = wave_kernel (streaming: max, "
-                       "sum-exp, candidates) + wave_merge_kernel (exact top-k, top-p, draw); "
-                       "duration = HIP-event time of the back-to-back timed calls / steps"),
+            "kernel": ("one tabby_sampler_sample_device call = row_kernel, one workgroup per "
+                       "row (streaming: max, sum-exp, candidates; then in LDS the exact top-k, "
+                       "top-p and draw); duration = HIP-event time of the back-to-back timed "
+                       "calls / steps"),
             "bytes_per_launch": bytes_per_launch,
             "duration_us": round(avg_ms * 1000, 2),
         },

@@ -6,7 +6,10 @@
 // (src/shaders/topk_partial.wgsl, topk_select.wgsl), orchestrated by encodeSampling
 // (src/engine/forward.ts:522-601); the f64 tail runs on the CPU (src/engine/sampler.ts:147-212).
 //
-// Here one call samples a whole batch with two kernels on the caller's stream:
+// Here one call samples a whole batch on the caller's stream. A batch of at least as many
+// rows as the device has CUs (pools up to 256) takes one kernel, row_kernel: one workgroup
+// per row, whose waves stream the row and then merge in LDS what the two kernels below
+// exchange through global memory. Smaller batches, and pools above 256, take two kernels:
 //   * wave_kernel (slice_kernel for pools above 256): grid = rows x splits; each wave
 //     (workgroup) owns one slice of one row and reads it from HBM exactly once with 16-byte
 //     nontemporal loads into registers. From registers it keeps the slice max, the slice sum
@@ -866,14 +869,15 @@ __device__ __forceinline__ Pruned wave_prune_any(WaveSmem &sm, int count, int kk
 // LDS counter *claim (shared by the row's waves, starting past their first chunks), so that
 // the row's waves end together however the SIMDs schedule them. Every statistic and list of
 // the wave is independent of which elements it saw: the max, sum-exp to 1e-5, and a
-// superset of the top kk of its elements. With CLAIM the row's waves also agree on a first
-// bound through *row_theta (an LDS word holding 0xffffffff before the call) and one barrier. The wave's top min(count, kk), sorted descending,
+// superset of the top kk of its elements. With CLAIM the row's `waves` waves (all of the
+// workgroup, *claim starting at `waves`) also agree on a first bound through *row_theta (an
+// LDS word holding 0xffffffff before the call) and one barrier. The wave's top min(count, kk), sorted descending,
 // go to out[0..keep) as composites (out may be sm.list itself: the list is read into
 // registers before anything is written), its statistics to *stat.
 template <typename In, int VEC, bool CLAIM>
 __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const tabby_row_params &P, int row,
                                            int slice, uint64_t *out, SliceStat *stat, int *claim,
-                                           uint32_t *row_theta) {
+                                           uint32_t *row_theta, int waves) {
   const int V = L.vocab;
   const int begin = CLAIM ? 0 : slice * L.slice_len;
   const int n = CLAIM ? V : min(L.slice_len, V - begin);
@@ -969,13 +973,13 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
     int b = next();
     if (b < full_chunks) wave_load_full<In, VEC>(src, b, y);
     else if (b < nchunks) wave_load<In, VEC>(src, n, b, y);
-    // The row's first bound, shared by its L.splits waves: wave w offers the kw-th largest of
-    // its first chunk's lane maxima, kw = ceil(kk / L.splits) -- kw distinct elements at or
-    // above it -- and the smallest offer has at least kk elements of the row at or above
-    // it, so it never exceeds the row's kk-th largest. (A wave alone could only offer the
-    // kk-th largest of its 64 lane maxima.) Every wave passes the barrier once.
+    // The row's first bound, shared by its waves: wave w offers the kw-th largest of its
+    // first chunk's lane maxima, kw = ceil(kk / waves) -- kw distinct elements at or above
+    // it -- and the smallest offer has at least kk elements of the row at or above it, so it
+    // never exceeds the row's kk-th largest. (A wave alone could only offer the kk-th
+    // largest of its 64 lane maxima.) Every wave passes the barrier once.
     {
-      const int kw = (kk + L.splits - 1) / L.splits;
+      const int kw = (kk + waves - 1) / waves;
       uint32_t offer = kNegInfKey;
       if (kk > 0 && kw <= kWaveSize && a < nchunks) {
         if (a >= full_chunks) {
@@ -1050,7 +1054,7 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   const tabby_row_params P = L.params[row];
   wave_slice<In, VEC, false>(sm, L, P, row, slice,
                              W.cands + (size_t)row * W.row_cand_stride + (size_t)slice * L.slice_len,
-                             W.stats + (size_t)row * kMaxSplits + slice, nullptr, nullptr);
+                             W.stats + (size_t)row * kMaxSplits + slice, nullptr, nullptr, 0);
 }
 
 // Smallest key whose scaled logit (l - max)/T in f64 is >= -37.5 (the max's key when T <= 0:
@@ -1714,7 +1718,8 @@ __global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace 
 
 // ---------------------------------------------------------------------------------------
 // Batches of at least as many rows as the chip has CUs (pools of at most 256): one
-// workgroup per row of L.splits <= kRowWaves waves, which take the row's chunks from an LDS
+// workgroup per row of max(L.splits, kWaves) <= kRowWaves waves (the merge below needs
+// four), which take the row's chunks from an LDS
 // counter (wave_slice with CLAIM) and leave their sorted lists and statistics in LDS; after
 // one barrier the workgroup merges them as wave_merge_kernel does. Nothing goes through
 // global memory between the two halves, the row finishes as soon as its own chunks are done
@@ -1739,17 +1744,18 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   __shared__ RowSmem sm;
   const int row = (int)blockIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int nw = (int)(blockDim.x / kWaveSize);  // the row's waves, >= kWaves
   const tabby_row_params P = L.params[row];  // kept in registers for the merge
   if (threadIdx.x == 0) {
-    sm.next_chunk = L.splits;  // chunk w is wave w's first
+    sm.next_chunk = nw;  // chunk w is wave w's first
     sm.row_theta = 0xffffffffu;
   }
   __syncthreads();
   wave_slice<In, VEC, true>(sm.wave[w], L, P, row, w, sm.wave[w].list, &sm.stats[w], &sm.next_chunk,
-                            &sm.row_theta);
+                            &sm.row_theta, nw);
   __syncthreads();
   constexpr int stride = (int)(sizeof(WaveSmem) / sizeof(uint64_t));
-  const RowLists lists{sm.wave[0].list, L.splits, stride, (int64_t)L.splits * stride};
+  const RowLists lists{sm.wave[0].list, nw, stride, (int64_t)nw * stride};
   merge_row<In>(sm.merge, L, W, row, P, sm.stats, lists);
 }
 
@@ -2294,7 +2300,9 @@ template <typename In, int VEC>
 hipError_t launch_pair(const Launch &L, const Workspace &W, int cus, hipStream_t stream) {
   const dim3 slices((unsigned)(L.rows * L.splits)), rows((unsigned)L.rows);
   if (per_row_launch(L, cus)) {
-    hipLaunchKernelGGL((row_kernel<In, VEC>), rows, dim3((unsigned)(L.splits * kWaveSize)), 0, stream, L, W);
+    // At least kWaves waves: the merge's list tree and its two f64 sums take four.
+    hipLaunchKernelGGL((row_kernel<In, VEC>), rows, dim3((unsigned)(std::max(L.splits, kWaves) * kWaveSize)), 0,
+                       stream, L, W);
   } else if (L.kcap <= kWaveKcap) {
     hipLaunchKernelGGL((wave_kernel<In, VEC>), slices, dim3(kWaveSize), 0, stream, L, W);
     hipLaunchKernelGGL((wave_merge_kernel<In>), rows, dim3(kBlock), 0, stream, L, W);

@@ -244,3 +244,59 @@ def test_full_vocab_rejects_list_above_k_max():
         p = S.make_params(S.SamplingParams(0.7, 0, 0.9), 1, 0.5)
         with pytest.raises(S.SamplingError, match="topk_cap"):
             g.sample_params(x, p, topk_cap=65)
+
+
+# ---- batches of at least as many rows as CUs: the per-row kernel -------------------------
+# (row_kernel: one workgroup per row, chunks claimed from an LDS counter, a first bound
+# shared by the row's waves, lists merged in LDS.)
+
+def test_row_kernel_mixed_k_ties_neg_inf(oracle):
+    # 264 rows of 20,000: ten waves per row (not a power of two), pools up to 256 (four
+    # registers per list), ties and -inf, greedy and sampled rows.
+    w = synth.random_workload(rows=264, vocab=20000, seed=53, ties=True, neg_inf_frac=0.3,
+                              k_choices=(1, 5, 50, 64, 65, 100, 200, 256))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=256)
+    _log("row kernel mixed k", compare(w, res, ids, vals, run_oracle(oracle, w, 256), 256))
+
+
+def test_row_kernel_f16_finite_k(oracle):
+    w = synth.config(4, rows=256, vocab=40000)
+    w.top_k[:] = np.array([1, 20, 50, 100] * 64, np.int32)
+    w.temperature[:] = np.array([0.0, 0.3, 0.7, 1.0] * 64)
+    res, ids, vals = run_gpu(w, k_max=128, topk_cap=100)
+    _log("row kernel f16", compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100))
+
+
+@pytest.mark.parametrize("vocab", [1, 3, 1000, 2049, 4096])
+def test_row_kernel_small_vocab(oracle, vocab):
+    # One or two waves per row; rows shorter than their k; a row's first chunk partial.
+    w = synth.random_workload(rows=256, vocab=vocab, seed=61 + vocab, k_choices=(1, 2, 40, 64, 256))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=64)
+    _log(f"row kernel vocab {vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
+def test_row_kernel_with_full_vocab_rows(oracle):
+    # Whole-vocabulary rows among finite ones: the per-row kernel hands them to the head
+    # kernels.
+    w = synth.random_workload(rows=256, vocab=12000, seed=71, k_choices=(0, 1, 50, 256),
+                              temperatures=(0.0, 0.3, 1.0), top_ps=(0.9, 0.95, 1.0))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=64)
+    _log("row kernel + full vocab", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
+def test_row_kernel_rows_outside_contract():
+    import torch
+    rows = 256
+    x = torch.randn(rows, 3000, device="cuda")
+    x[5] = float("-inf")
+    x[77, 1234] = float("nan")
+    x[200, 9] = float("inf")
+    with S.GpuSampler(vocab_max=3000, rows_max=rows, k_max=64) as g:
+        p = S.make_params(S.SamplingParams(0.7, 40, 0.9), rows, 0.25)
+        pd = torch.from_numpy(p.view(np.uint8).copy()).cuda()
+        rd = torch.zeros(rows * S.RESULT_DTYPE.itemsize, dtype=torch.uint8, device="cuda")
+        g.sample_device(x, pd, rd)
+        res = rd.cpu().numpy().view(S.RESULT_DTYPE)
+    bad = {5, 77, 200}
+    for r in range(rows):
+        assert res["status"][r] == (S.TABBY_EDOMAIN if r in bad else 0), f"row {r}"
