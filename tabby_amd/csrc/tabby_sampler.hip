@@ -1292,7 +1292,10 @@ struct WaveMergeSmem {
   double b[kWaveKcap];  // exp((l - max) / T), then the weights
   double c[kWaveKcap];  // running sums of the weights
   uint64_t part[kWaves][kWaveKcap];  // each wave's merged lists
-  double pool, scaled;               // poolMass and the scaled total
+  double pool;                       // poolMass
+  int cut, chosen;                   // consideredCount and the drawn position
+  float row_max;                     // row statistics, when a separate wave combines them
+  double row_sum;
 };
 
 // Bitonic clean of 64*R values (index r*64 + lane) into descending order.
@@ -1480,18 +1483,46 @@ __device__ __forceinline__ void merge_with(uint64_t (&acc)[R], const uint64_t *o
   bitonic_clean_desc<R>(acc);
 }
 
-// sampleFromTopK (src/engine/sampler.ts:147-212) over sm.sorted[0..K), K >= 1, in the
-// reference's order of f64 operations. The caller has left the terms exp(x - max)/sum_exp in
-// sm.a with their sum in sm.pool (poolMass) and the weights exp(x/T) in sm.b with their sum
-// in sm.scaled. The running sums of the normalised weights (the top-p cumulative sums) are
-// left-to-right sums evaluated bit-exactly by the whole wave (wave_seq_sum).
+// The draw of sampleFromTopK (src/engine/sampler.ts:170-203) over sm.sorted[0..K), K >= 1,
+// by the wave that has just left the weights exp(x/T) in sm.b with their left-to-right sum
+// `scaled`: the normalised weights, their running sums (the top-p cumulative sums, evaluated
+// bit-exactly by the whole wave: wave_seq_sum) up to the first that reaches top-p -- the
+// cut -- and the first running sum above uniform * total. Leaves sm.cut and sm.chosen.
+__device__ __forceinline__ void wave_draw(WaveMergeSmem &sm, int K, const tabby_row_params &P, double scaled) {
+  const int lane = wave_lane();
+  for (int i = lane; i < K; i += kWaveSize) sm.b[i] = sm.b[i] / scaled;
+  wave_lds_sync();
+  const double top_p = P.top_p;
+  const SeqSum run = wave_seq_sum(sm.b, K, sm.c, top_p < 1.0 ? top_p : INFINITY);
+  wave_lds_sync();
+  const int cut = run.count;
+  const double total = run.total;  // the running sum at cut - 1: the reference's total
+  const double target = P.uniform * total;
+  int chosen = cut - 1;
+  for (int base = 0; base < cut; base += kWaveSize) {
+    const int i = base + lane;
+    const uint64_t hit = __ballot(i < cut && target < sm.c[min(i, cut - 1)]);
+    if (hit) {
+      chosen = base + __ffsll((unsigned long long)hit) - 1;
+      break;
+    }
+  }
+  if (lane == 0) {
+    sm.cut = cut;
+    sm.chosen = chosen;
+  }
+}
+
+// The row's result (src/engine/sampler.ts:147-212) once the other passes are done: the exact
+// terms exp(x - max)/sum_exp in sm.a with their sum in sm.pool (poolMass) and, for T > 0,
+// the draw's sm.cut and sm.chosen (wave_draw); T <= 0 is greedy (sampler.ts:159-167).
 template <typename In>
 __device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch &L, int row,
                                           const In *row_src, float max_logit, double sum_exp,
                                           const tabby_row_params &P) {
   const int lane = wave_lane();
   const double T = P.temperature;
-  const double pool = sm.pool, scaled = sm.scaled;
+  const double pool = sm.pool;
   tabby_row_result res;
   res.max_logit = max_logit;
   res.sum_exp = sum_exp;
@@ -1499,30 +1530,13 @@ __device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch
   res.status = TABBY_OK;
   res.topk_count = min(K, L.topk_cap);
   int chosen = 0;
-  if (!(T > 0.0)) {  // sampler.ts:159-167: greedy, the uniform unused
+  if (!(T > 0.0)) {  // greedy, the uniform unused
     res.considered = 1;
     res.pool_exhausted = 0;
   } else {
-    for (int i = lane; i < K; i += kWaveSize) sm.b[i] = sm.b[i] / scaled;
-    wave_lds_sync();
-    // The running sums of the weights, stopping at the first that reaches top-p: the cut.
-    const double top_p = P.top_p;
-    const SeqSum run = wave_seq_sum(sm.b, K, sm.c, top_p < 1.0 ? top_p : INFINITY);
-    wave_lds_sync();
-    const int cut = run.count;
-    const double total = run.total;  // the running sum at cut - 1: the reference's total
-    const double target = P.uniform * total;
-    chosen = cut - 1;
-    for (int base = 0; base < cut; base += kWaveSize) {
-      const int i = base + lane;
-      const uint64_t hit = __ballot(i < cut && target < sm.c[min(i, cut - 1)]);
-      if (hit) {
-        chosen = base + __ffsll((unsigned long long)hit) - 1;
-        break;
-      }
-    }
-    res.considered = (uint32_t)cut;
-    res.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
+    chosen = sm.chosen;
+    res.considered = (uint32_t)sm.cut;
+    res.pool_exhausted = (P.top_p < 1.0 && pool < P.top_p) ? 1 : 0;
   }
   const uint64_t cv = sm.sorted[chosen];
   res.id = (int32_t)composite_index(cv);
@@ -1615,6 +1629,26 @@ __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, 
                                             const tabby_row_params &P, const RowPool &rp, float row_max,
                                             double sum_exp);
 
+// The row's top K, sorted, into sm.sorted[0..K) from its sorted lists (merge_lists_4 in the
+// register class of K; m1: the first 64 entries' loads, already issued). No barrier when
+// K == 0.
+template <class CountOf>
+__device__ __forceinline__ void merge_pool(WaveMergeSmem &sm, const RowLists &lists, ListMerger<1> &m1,
+                                           CountOf count_of, int K) {
+  if (K <= 0) return;
+  if (K <= kWaveSize) {
+    merge_lists_4<1>(sm, m1, count_of, K);
+  } else if (K <= 2 * kWaveSize) {
+    ListMerger<2> m2 = lists_of_wave<2>(lists);
+    m2.start();
+    merge_lists_4<2>(sm, m2, count_of, K);
+  } else {
+    ListMerger<4> m4 = lists_of_wave<4>(lists);
+    m4.start();
+    merge_lists_4<4>(sm, m4, count_of, K);
+  }
+}
+
 // Merges row `row`'s sorted slice lists and statistics and finishes the row (at least four
 // waves; the lists and statistics are in global memory or in LDS; P is the row's parameters).
 template <typename In>
@@ -1628,20 +1662,7 @@ __device__ __forceinline__ void merge_row(WaveMergeSmem &sm, const Launch &L, co
   const RowStats rs = row_stats(stats, lists.count);
   auto count_of = [&](int s) { return list_count(rs, s); };
   const RowPool rp = row_pool(L, P);
-  const int K = rp.K;
-  if (K > 0) {
-    if (K <= kWaveSize) {
-      merge_lists_4<1>(sm, m1, count_of, K);
-    } else if (K <= 2 * kWaveSize) {
-      ListMerger<2> m2 = lists_of_wave<2>(lists);
-      m2.start();
-      merge_lists_4<2>(sm, m2, count_of, K);
-    } else {
-      ListMerger<4> m4 = lists_of_wave<4>(lists);
-      m4.start();
-      merge_lists_4<4>(sm, m4, count_of, K);
-    }
-  }
+  merge_pool(sm, lists, m1, count_of, rp.K);
   finish_pool<In>(sm, L, W, row, P, rp, rs.max, rs.sum_exp);
 }
 
@@ -1661,7 +1682,7 @@ __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, 
   if (valid_params && in_domain && finite) {
     // sampleFromTopK's two independent passes over the pool (sampler.ts:156-157, 170-172)
     // on two waves: wave 0 the exact terms and poolMass, wave 1 the scaled terms and their
-    // total, each a left-to-right sum.
+    // total, each a left-to-right sum; wave 1 goes on to the draw.
     const int w = wave_id();
     const double M = (double)row_max, T = P.temperature;
     if (w == 0) {
@@ -1674,8 +1695,7 @@ __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, 
       for (int i = lane; i < K; i += kWaveSize)
         sm.b[i] = T > 0.0 ? fdlibm_exp_inline(((double)value_of(composite_key(sm.sorted[i])) - M) / T) : 0.0;
       wave_lds_sync();
-      const double scaled = T > 0.0 ? wave_seq_sum(sm.b, K, nullptr, INFINITY).total : 0.0;
-      if (lane == 0) sm.scaled = scaled;
+      if (T > 0.0) wave_draw(sm, K, P, wave_seq_sum(sm.b, K, nullptr, INFINITY).total);
     }
     __syncthreads();
   }
@@ -1718,10 +1738,11 @@ __global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace 
 
 // ---------------------------------------------------------------------------------------
 // Batches of at least as many rows as the chip has CUs (pools of at most 256): one
-// workgroup per row of max(L.splits, kWaves) <= kRowWaves waves (the merge below needs
-// four), which take the row's chunks from an LDS
+// workgroup per row of max(L.splits, kRowMinWaves) <= kRowWaves waves (the merge below
+// uses five), which take the row's chunks from an LDS
 // counter (wave_slice with CLAIM) and leave their sorted lists and statistics in LDS; after
-// one barrier the workgroup merges them as wave_merge_kernel does. Nothing goes through
+// one barrier the first four waves merge the lists as wave_merge_kernel does, reading their
+// lengths from LDS, while the fifth combines the statistics. Nothing goes through
 // global memory between the two halves, the row finishes as soon as its own chunks are done
 // instead of after every row's, and its waves end within about a chunk of each other (with
 // fixed slices, the SIMDs' oldest-first issue left the youngest waves ~8 us behind).
@@ -1730,6 +1751,7 @@ __global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace 
 // is a chain of dependent LDS round trips before its merge.)
 // ---------------------------------------------------------------------------------------
 constexpr int kRowWaves = 16;
+constexpr int kRowMinWaves = kWaves + 1;  // four merge the lists, one the statistics
 
 struct RowSmem {
   WaveSmem wave[kRowWaves];
@@ -1744,7 +1766,7 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   __shared__ RowSmem sm;
   const int row = (int)blockIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
-  const int nw = (int)(blockDim.x / kWaveSize);  // the row's waves, >= kWaves
+  const int nw = (int)(blockDim.x / kWaveSize);  // the row's waves, >= kRowMinWaves
   const tabby_row_params P = L.params[row];  // kept in registers for the merge
   if (threadIdx.x == 0) {
     sm.next_chunk = nw;  // chunk w is wave w's first
@@ -1756,7 +1778,19 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   __syncthreads();
   constexpr int stride = (int)(sizeof(WaveSmem) / sizeof(uint64_t));
   const RowLists lists{sm.wave[0].list, nw, stride, (int64_t)nw * stride};
-  merge_row<In>(sm.merge, L, W, row, P, sm.stats, lists);
+  ListMerger<1> m1 = lists_of_wave<1>(lists);
+  m1.start();
+  const RowPool rp = row_pool(L, P);
+  if (w == kWaves) {
+    const RowStats rs = row_stats(sm.stats, nw);
+    if (wave_lane() == 0) {
+      sm.merge.row_max = rs.max;
+      sm.merge.row_sum = rs.sum_exp;
+    }
+  }
+  merge_pool(sm.merge, lists, m1, [&](int s) { return (int)sm.stats[s].count; }, rp.K);
+  __syncthreads();
+  finish_pool<In>(sm.merge, L, W, row, P, rp, sm.merge.row_max, sm.merge.row_sum);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2300,9 +2334,9 @@ template <typename In, int VEC>
 hipError_t launch_pair(const Launch &L, const Workspace &W, int cus, hipStream_t stream) {
   const dim3 slices((unsigned)(L.rows * L.splits)), rows((unsigned)L.rows);
   if (per_row_launch(L, cus)) {
-    // At least kWaves waves: the merge's list tree and its two f64 sums take four.
-    hipLaunchKernelGGL((row_kernel<In, VEC>), rows, dim3((unsigned)(std::max(L.splits, kWaves) * kWaveSize)), 0,
-                       stream, L, W);
+    // At least kRowMinWaves waves: the merge uses five.
+    hipLaunchKernelGGL((row_kernel<In, VEC>), rows, dim3((unsigned)(std::max(L.splits, kRowMinWaves) * kWaveSize)),
+                       0, stream, L, W);
   } else if (L.kcap <= kWaveKcap) {
     hipLaunchKernelGGL((wave_kernel<In, VEC>), slices, dim3(kWaveSize), 0, stream, L, W);
     hipLaunchKernelGGL((wave_merge_kernel<In>), rows, dim3(kBlock), 0, stream, L, W);
