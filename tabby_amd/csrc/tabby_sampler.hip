@@ -2299,8 +2299,10 @@ struct Plan {
   int vec;
 };
 
-// Enough slices per row that the batch fills the chip about once: 256 CUs x 5 resident
-// 256-lane workgroups, or 256 CUs x 4 SIMDs x 4 one-wave workgroups for the wave kernel
+// Enough slices per row that the batch fills the chip about once: 256 CUs x 3 resident
+// 256-lane workgroups of the slice kernel (its 41.5 KB of LDS leaves room for three; a
+// larger grid ran in two rounds -- config 5, 512 rows: 3 slices per row took 225 us, one
+// 200 us), rounded down, or 256 CUs x 4 SIMDs x 4 one-wave workgroups for the wave kernel
 // (measured at 256 rows: 16 slices per row, 39.9 us per call, beat 12 per row, 41.4 us --
 // the SIMDs issue their oldest wave first and a fourth wave hides more of the others'
 // waits -- and 18 or 20 per row, which no longer fit at once, ~50 us). Each
@@ -2309,7 +2311,7 @@ struct Plan {
 // anyway and the latency is one slice's chain plus the merge, whose cost grows with the
 // number of lists (measured on one row: 24 slices of 2048 beat 12 of 4096 and 48 of 1024
 // at vocab 49152; 37 slices of 4096 beat 46 and 74 at vocab 151936).
-constexpr int kTargetGroups = 1280;
+constexpr int kTargetGroups = 768;
 constexpr int kTargetWaves = 4096;
 constexpr int kMaxWaveSplits = 36;
 
@@ -2321,7 +2323,7 @@ Plan make_plan(int rows, int vocab, int dtype, const void *logits, bool wave) {
   const int chunk = wave ? 2 * kWChunk : kChunk;
   const int target = wave ? kTargetWaves : kTargetGroups;
   const int most = std::min(wave ? kMaxWaveSplits : kMaxSplits, (vocab + chunk - 1) / chunk);
-  const int want = std::max(1, std::min(most, (target + rows - 1) / rows));
+  const int want = std::max(1, std::min(most, wave ? (target + rows - 1) / rows : target / rows));
   const int granule = (wave ? kWaveSize : kBlock) * p.vec;
   const int per = (vocab + want - 1) / want;
   p.slice_len = (per + granule - 1) / granule * granule;

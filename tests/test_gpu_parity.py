@@ -44,7 +44,7 @@ def test_config5_ties_neg_inf_k1024(oracle):
 
 
 def test_config5_sorted_slice_lists(oracle):
-    # 256 rows: 5 slices per row, each leaving its list sorted, merged by merge paths.
+    # 256 rows: three slices per row of the 256-lane slice kernel.
     w = synth.config(5, rows=256)
     res, ids, vals = run_gpu(w, k_max=1024, topk_cap=1024)
     _log("config5[256 rows]", compare(w, res, ids, vals, run_oracle(oracle, w, 1024), 1024))
