@@ -300,3 +300,20 @@ def test_row_kernel_rows_outside_contract():
     bad = {5, 77, 200}
     for r in range(rows):
         assert res["status"][r] == (S.TABBY_EDOMAIN if r in bad else 0), f"row {r}"
+
+
+def test_row_kernel_f16_unaligned_vocab(oracle):
+    # f16 rows whose length is not a multiple of 8: element loads instead of 16-byte vectors.
+    w = synth.config(4, rows=256, vocab=4097)
+    w.top_k[:] = np.array([1, 7, 64, 200] * 64, np.int32)
+    w.temperature[:] = np.array([0.0, 0.5, 1.0, 2.0] * 64)
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=200)
+    _log("row kernel f16 vocab 4097", compare(w, res, ids, vals, run_oracle(oracle, w, 200), 200))
+
+
+def test_row_kernel_300_rows(oracle):
+    # More rows than CUs, not a multiple of 8, with -inf and ties.
+    w = synth.random_workload(rows=300, vocab=30000, seed=83, ties=True, neg_inf_frac=0.1,
+                              k_choices=(1, 50, 128))
+    res, ids, vals = run_gpu(w, k_max=128, topk_cap=128)
+    _log("row kernel 300 rows", compare(w, res, ids, vals, run_oracle(oracle, w, 128), 128))
