@@ -350,6 +350,205 @@ __device__ __forceinline__ SeqSum wave_seq_sum_wide(const double *t, int n, doub
   return wave_seq_sum_wide(t, n, out, out != nullptr, stop_at);
 }
 
+// LDS words through which the NW waves of block_seq_sum_wide combine a step.
+template <int NW>
+struct SeqScratch {
+  uint32_t map[NW];    // each wave's parity map over its terms
+  uint32_t tie[NW];    // whether the wave holds a tie
+  double total[NW];    // each wave's integer increment
+  int flag[NW];        // each wave's first event (n: none)
+  uint32_t stop[NW];   // that event is a plain stop
+  double before[NW];   // the integer partial sum before it, and at it
+  double at[NW];
+  double last[NW];     // the integer partial sum at the wave's last term
+  SeqSum result;
+};
+
+// wave_seq_sum_wide by a whole workgroup of NW waves: a step covers NW * 1024 terms, wave w
+// the w-th 1024. The waves' integer increments are added in wave order (exact, as in one
+// wave); a tie needs the parity of the running sum before it, so when a step holds a tie the
+// waves' parity maps are composed in wave order (a wave without ties just XORs its terms'
+// low bits: one ballot). The step's first event, from the first wave that has one, decides
+// as in one wave. Three barriers per step, four with a tie. Same contract as
+// wave_seq_sum_wide; every thread of the workgroup calls it and gets the result.
+template <int NW, class In, class Out>
+__device__ __forceinline__ SeqSum block_seq_sum_wide(In t, int n, Out out, bool has_out, double stop_at,
+                                                     bool settle, SeqScratch<NW> &sc) {
+  constexpr int kPer = 16, kStep = kWaveSize * kPer, kBlockStep = NW * kStep;
+  const int lane = wave_lane(), w = (int)(threadIdx.x >> 6);
+  if (n <= kSeqShort) {
+    if (w == 0) {
+      const SeqSum r = lane_seq_sum(t, n, out, has_out, stop_at);
+      if (lane == 0) sc.result = r;
+    }
+    __syncthreads();
+    const SeqSum r = sc.result;
+    __syncthreads();  // sc is free again when the call returns
+    return r;
+  }
+  double P = t[0];
+  if (has_out && threadIdx.x == 0) out[0] = P;
+  if (P >= stop_at) return {P, 1};
+  int a = 1;
+  while (a < n) {
+    const int E = ((int)((uint64_t)__double_as_longlong(P) >> 52) & 0x7ff) - 1023;
+    const double u = __longlong_as_double((long long)((uint64_t)(E - 52 + 1023) << 52));
+    const double scale = __longlong_as_double((long long)((uint64_t)(52 - E + 1023) << 52));
+    const double m = P * scale;
+    const int wfirst = a + w * kStep;
+    const int first = wfirst + lane * kPer;
+    double q[kPer], r[kPer];
+    uint32_t tie_bits = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      q[i] = (first + i < n ? t[first + i] : 0.0) * scale;
+      r[i] = __builtin_rint(q[i]);
+      if (q[i] < kTwo52 && __builtin_fabs(r[i] - q[i]) == 0.5) tie_bits |= 1u << i;
+    }
+    const bool wtie = __ballot(tie_bits != 0u) != 0ull;
+    uint32_t lane_map = kParityId, excl = kParityId, wave_map;
+    if (wtie) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+        lane_map = parity_then(lane_map, ((tie_bits >> i) & 1u) ? 0u : 1u | (low_bit(r[i]) << 1));
+      excl = parity_exclusive_scan(lane_map);
+      wave_map = (uint32_t)__builtin_amdgcn_readlane((int)parity_then(excl, lane_map), kWaveSize - 1);
+    } else {
+      uint32_t par = 0u;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) par ^= low_bit(r[i]);
+      wave_map = 1u | ((uint32_t)(__popcll(__ballot(par != 0u)) & 1) << 1);  // x -> x ^ parity
+    }
+    auto totals = [&](double (&pre)[kPer], double &run, double &incl) {
+      run = 0.0;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        run += r[i];
+        pre[i] = run;
+      }
+      incl = wave_inclusive_scan(run);
+    };
+    double pre[kPer], run, incl;
+    totals(pre, run, incl);
+    if (lane == 0) {
+      sc.map[w] = wave_map;
+      sc.tie[w] = wtie ? 1u : 0u;
+    }
+    if (lane == kWaveSize - 1) sc.total[w] = incl;
+    __syncthreads();
+    bool any_tie = false;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) any_tie |= sc.tie[k] != 0u;
+    if (any_tie) {
+      if (wtie) {
+        uint32_t prefix = kParityId;
+        for (int k = 0; k < w; ++k) prefix = parity_then(prefix, sc.map[k]);
+        uint32_t parity = parity_apply(parity_then(prefix, excl), low_bit(m));
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          if ((tie_bits >> i) & 1u) {
+            const double fl = q[i] - 0.5;
+            r[i] = fl + (double)(parity ^ low_bit(fl));
+            parity = 0u;
+          } else {
+            parity ^= low_bit(r[i]);
+          }
+        }
+        totals(pre, run, incl);
+      }
+      __syncthreads();  // every wave has read the first totals
+      if (lane == kWaveSize - 1) sc.total[w] = incl;
+      __syncthreads();
+    }
+    double wave_prefix = 0.0;
+    for (int k = 0; k < w; ++k) wave_prefix += sc.total[k];
+    double below = row_shift_up<1>(incl);
+    const double i15 = lane_f64(incl, 15), i31 = lane_f64(incl, 31), i47 = lane_f64(incl, 47);
+    if (lane == 16) below = i15;
+    if (lane == 32) below = i31;
+    if (lane == 48) below = i47;
+    const double base = m + wave_prefix + below;
+    const int last_i = min(kPer, n - first) - 1;
+    const double cum_end = base + run;
+    int my_first = kPer;
+    bool my_stop = false;
+    if (last_i >= 0 && (cum_end >= kTwo53 || cum_end * u >= stop_at)) {
+#pragma unroll
+      for (int i = kPer - 1; i >= 0; --i) {
+        const double cum = base + pre[i];
+        if (i <= last_i && (cum >= kTwo53 || cum * u >= stop_at)) {
+          my_first = i;
+          my_stop = cum < kTwo53;
+        }
+      }
+    }
+    const uint64_t has = __ballot(my_first < kPer);
+    const int Lf = has ? __ffsll((unsigned long long)has) - 1 : kWaveSize;
+    const int fi = Lf < kWaveSize ? __builtin_amdgcn_readlane(my_first, Lf) : 0;
+    double before_mine = 0.0, at_mine = 0.0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      if (i == fi) {
+        before_mine = i == 0 ? base : base + pre[i - 1];
+        at_mine = base + pre[i];
+      }
+    }
+    const int wlast = min(n, wfirst + kStep) - 1;  // the wave's last term (< wfirst: none)
+    const int ll = wlast >= wfirst ? (wlast - wfirst) / kPer : 0;
+    const double last_cum = lane_f64(cum_end, ll);
+    if (Lf < kWaveSize) {
+      const double bf = lane_f64(before_mine, Lf), at = lane_f64(at_mine, Lf);
+      const int st = __builtin_amdgcn_readlane((int)my_stop, Lf);
+      if (lane == 0) {
+        sc.flag[w] = wfirst + Lf * kPer + fi;
+        sc.stop[w] = (uint32_t)st;
+        sc.before[w] = bf;
+        sc.at[w] = at;
+      }
+    } else if (lane == 0) {
+      sc.flag[w] = n;
+    }
+    if (lane == 0) sc.last[w] = last_cum;
+    __syncthreads();
+    int flagged = n, fw = 0;
+    for (int k = NW - 1; k >= 0; --k) {
+      if (sc.flag[k] < n) {
+        flagged = sc.flag[k];
+        fw = k;
+      }
+    }
+    if (has_out) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int j = first + i;
+        if (j < n && j < flagged) out[j] = (base + pre[i]) * u;
+      }
+    }
+    if (flagged >= n) {
+      const int last = min(n, a + kBlockStep) - 1;
+      P = sc.last[(last - a) / kStep] * u;  // the wave holding the step's last term
+      const bool settled = settle && !has_out && t[last] * scale < 0.5;
+      a = last + 1;
+      __syncthreads();  // sc is reused by the next step
+      if (settled) return {P, n};
+      continue;
+    }
+    const bool is_stop = sc.stop[fw] != 0u;
+    const double before = sc.before[fw], at = sc.at[fw];
+    __syncthreads();  // sc is reused by the next step
+    if (is_stop) {
+      const double v = at * u;
+      if (has_out && threadIdx.x == 0) out[flagged] = v;
+      return {v, flagged + 1};
+    }
+    P = before * u + t[flagged];
+    if (has_out && threadIdx.x == 0) out[flagged] = P;
+    if (P >= stop_at) return {P, flagged + 1};
+    a = flagged + 1;
+  }
+  return {P, n};
+}
+
 // Two independent left-to-right sums over the same length (poolMass and the scaled total):
 // short ones interleave on lane 0, long ones use the wave scan for each. The second is
 // skipped (0) when want_b is false.

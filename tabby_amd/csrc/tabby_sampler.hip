@@ -2081,10 +2081,12 @@ __global__ __launch_bounds__(kBlock) void head_sort_kernel(Launch L, Workspace W
 // gfx950 workgroup may use); larger ones from global memory.
 constexpr int kHeadLds = 16384;
 
+constexpr int kFinishThreads = 512;  // eight waves: the sums take 8,192 terms per step
+
 struct HeadSmem {
   BlockScratch bs;
+  SeqScratch<kFinishThreads / kWaveSize> ss;
   double pool, e;
-  double scaled_total;
   int cut;
   int chosen;
   double t[PaddedLds::words(kHeadLds)];  // the head's weights, then their running sums
@@ -2118,7 +2120,7 @@ __device__ __forceinline__ int wave_first_above(C c, int n, double target) {
 // sampleFromTopK over the sorted head (see the comment on head_kernel): the head's terms,
 // the scaled total and the running sums (bit-exact sequential sums), the cut and the draw.
 template <typename In>
-__global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace W) {
+__global__ __launch_bounds__(kFinishThreads) void head_finish_kernel(Launch L, Workspace W) {
   __shared__ HeadSmem sm;
   const int row = (int)blockIdx.x;
   const tabby_row_params P = L.params[row];
@@ -2174,18 +2176,14 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
     const double top_p = P.top_p;
     const double stop = top_p < 1.0 ? top_p : INFINITY;
     auto finish = [&](auto t, auto c) {
-      if (wave_id() == 0) {
-        // The weights are non-increasing: the sum may settle before the head's end.
-        const double S = wave_seq_sum_wide(t, H, c, false, INFINITY, true).total;  // c unused
-        if (lane_id() == 0) sm.scaled_total = S;
-      }
+      // The weights are non-increasing: the sum may settle before the head's end. Both sums
+      // are taken by the whole workgroup (block_seq_sum_wide: 8,192 terms per step).
+      const double S = block_seq_sum_wide<kFinishThreads / kWaveSize>(t, H, c, false, INFINITY, true, sm.ss).total;
+      for (int i = threadIdx.x; i < H; i += kFinishThreads) c[i] = t[i] / S;
       __syncthreads();
-      const double S = sm.scaled_total;
-      for (int i = threadIdx.x; i < H; i += kBlock) c[i] = t[i] / S;
-      __syncthreads();
+      const SeqSum run = block_seq_sum_wide<kFinishThreads / kWaveSize>(c, H, c, true, stop, false, sm.ss);
+      __syncthreads();  // every running sum is written
       if (wave_id() == 0) {
-        const SeqSum run = wave_seq_sum_wide(c, H, c, true, stop);
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");  // the sums are read by other lanes
         const bool reached = top_p < 1.0 && run.total >= top_p;
         const double target = P.uniform * run.total;  // the running sum at the cut: the total
         const int first = wave_first_above(c, run.count, target);
@@ -2199,16 +2197,16 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
     if (H <= kHeadLds) {
       const PaddedLds lt{sm.t};
       constexpr int B = 8;  // loads in flight per lane
-      for (int base = 0; base < H; base += B * kBlock) {
+      for (int base = 0; base < H; base += B * kFinishThreads) {
         double v[B];
 #pragma unroll
         for (int u = 0; u < B; ++u) {
-          const int i = base + u * kBlock + (int)threadIdx.x;
+          const int i = base + u * kFinishThreads + (int)threadIdx.x;
           v[u] = i < H ? sg[i] : 0.0;
         }
 #pragma unroll
         for (int u = 0; u < B; ++u) {
-          const int i = base + u * kBlock + (int)threadIdx.x;
+          const int i = base + u * kFinishThreads + (int)threadIdx.x;
           if (i < H) lt[i] = v[u];
         }
       }
@@ -2227,7 +2225,7 @@ __global__ __launch_bounds__(kBlock) void head_finish_kernel(Launch L, Workspace
   if (threadIdx.x == 0) L.results[row] = res;
   if (L.topk_cap > 0) {
     const int m = min(H, L.topk_cap);
-    for (int i = threadIdx.x; i < m; i += kBlock) {
+    for (int i = threadIdx.x; i < m; i += kFinishThreads) {
       const uint32_t idx = composite_index(sorted[i]);
       L.topk_ids[(size_t)row * L.topk_cap + i] = (int32_t)idx;
       L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(V - 1)));
@@ -2243,6 +2241,14 @@ __global__ __launch_bounds__(kWaveSize) void seq_sum_kernel(const double *t, int
                                                            double *out, int32_t *count, int32_t wide) {
   const SeqSum r = wide ? wave_seq_sum_wide(t, n, out, stop_at) : wave_seq_sum(t, n, out, stop_at);
   if (wave_lane() == 0) *count = r.count;
+}
+
+// The same by a 256-lane workgroup (block_seq_sum_wide).
+__global__ __launch_bounds__(kBlock) void seq_sum_block_kernel(const double *t, int32_t n, double stop_at,
+                                                              double *out, int32_t *count) {
+  __shared__ SeqScratch<kWaves> sc;
+  const SeqSum r = block_seq_sum_wide<kWaves>(t, n, out, true, stop_at, false, sc);
+  if (threadIdx.x == 0) *count = r.count;
 }
 
 __global__ void exp_kernel(const double *x, double *y, int64_t n) {
@@ -2359,7 +2365,7 @@ hipError_t launch_head(const Launch &L, const Workspace &W, hipStream_t stream) 
   hipLaunchKernelGGL(head_plan_kernel, dim3((unsigned)L.rows), dim3(kBlock), 0, stream, L, W);
   hipLaunchKernelGGL(head_sort_kernel, dim3((unsigned)(L.rows * (W.plan_stride - 2))), dim3(kBlock), 0,
                      stream, L, W);
-  hipLaunchKernelGGL((head_finish_kernel<In>), dim3((unsigned)L.rows), dim3(kBlock), 0, stream, L, W);
+  hipLaunchKernelGGL((head_finish_kernel<In>), dim3((unsigned)L.rows), dim3(kFinishThreads), 0, stream, L, W);
   return hipGetLastError();
 }
 
@@ -2596,8 +2602,12 @@ int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double stop_at, doub
                         int32_t *count_dev, int32_t wide, void *stream) {
   if (!terms_dev || !prefix_dev || !count_dev) return fail(TABBY_EINVAL, "null pointer");
   if (n < 1) return fail(TABBY_EINVAL, "n must be >= 1");
-  hipLaunchKernelGGL(seq_sum_kernel, dim3(1), dim3(kWaveSize), 0, (hipStream_t)stream, terms_dev, n,
-                     stop_at, prefix_dev, count_dev, wide);
+  if (wide == 2)
+    hipLaunchKernelGGL(seq_sum_block_kernel, dim3(1), dim3(kBlock), 0, (hipStream_t)stream, terms_dev, n, stop_at,
+                       prefix_dev, count_dev);
+  else
+    hipLaunchKernelGGL(seq_sum_kernel, dim3(1), dim3(kWaveSize), 0, (hipStream_t)stream, terms_dev, n,
+                       stop_at, prefix_dev, count_dev, wide);
   HIP_TRY(hipGetLastError());
   return TABBY_OK;
 }

@@ -300,10 +300,11 @@ def device_exp(x) -> "object":
     return y
 
 
-def device_seq_sum(terms, stop_at: float = float("inf"), wide: bool = False):
+def device_seq_sum(terms, stop_at: float = float("inf"), wide: int = 0):
     """The device's sequential f64 partial sums of a CUDA float64 tensor (diagnostic):
-    returns (prefix sums actually written, as a CUDA tensor, count). ``wide`` selects the
-    16-terms-per-lane form used for long sums in global memory."""
+    returns (prefix sums actually written, as a CUDA tensor, count). ``wide``: 0 the
+    one-term-per-lane form, 1 the 16-terms-per-lane form used for long sums, 2 that form
+    taken by a four-wave workgroup."""
     import torch
     t = terms.contiguous()
     out = torch.zeros_like(t)

@@ -8,12 +8,12 @@ from tabby_amd import sampler as S
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=[False, True], ids=["lds", "wide"])
+@pytest.fixture(params=[0, 1, 2], ids=["lds", "wide", "block"])
 def wide(request):
     return request.param
 
 
-def _check(terms, stop_at=np.inf, wide=False):
+def _check(terms, stop_at=np.inf, wide=0):
     import torch
     terms = np.ascontiguousarray(terms, dtype=np.float64)
     prefix, n = S.device_seq_sum(torch.from_numpy(terms).cuda(), stop_at, wide)
@@ -26,7 +26,7 @@ def _check(terms, stop_at=np.inf, wide=False):
     assert bad.size == 0, f"{bad.size} differ, first at {bad[0]}: {got[bad[0]]!r} vs {expected[bad[0]]!r}"
 
 
-@pytest.mark.parametrize("n", [1, 2, 15, 16, 17, 63, 64, 65, 1023, 1024, 1025, 4097, 20000])
+@pytest.mark.parametrize("n", [1, 2, 15, 16, 17, 63, 64, 65, 1023, 1024, 1025, 4096, 4097, 8193, 20000])
 def test_sorted_exponential_terms(n, wide):
     rng = np.random.default_rng(n)
     l = np.sort(rng.normal(0, 3, n))[::-1]
