@@ -1886,13 +1886,15 @@ constexpr int kHeadBatch = 4096;
 // [1] = head size, [2 + g] = start offset of segment g, or ~0u if no segment starts there.
 __host__ __device__ __forceinline__ int plan_slots(int vocab_max) { return vocab_max / kSegCap + 2; }
 
+constexpr int kPlanThreads = 1024;  // a 13 K-entry head took 24.5 us on 256 lanes
+
 struct PlanSmem {
-  BlockScratch bs;
+  uint32_t wave_total[kPlanThreads / kWaveSize];
   uint32_t hist[kHeadBuckets];
   uint32_t start[kHeadBuckets];
 };
 
-__global__ __launch_bounds__(kBlock) void head_plan_kernel(Launch L, Workspace W) {
+__global__ __launch_bounds__(kPlanThreads) void head_plan_kernel(Launch L, Workspace W) {
   __shared__ PlanSmem sm;
   const int row = (int)blockIdx.x;
   uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
@@ -1912,39 +1914,43 @@ __global__ __launch_bounds__(kBlock) void head_plan_kernel(Launch L, Workspace W
   auto bucket_of = [&](uint64_t v) {
     return min((kmax - min(composite_key(v), kmax)) >> shift, (uint32_t)(kHeadBuckets - 1));
   };
-  for (int b = threadIdx.x; b < kHeadBuckets; b += kBlock) sm.hist[b] = 0u;
+  for (int b = threadIdx.x; b < kHeadBuckets; b += kPlanThreads) sm.hist[b] = 0u;
   __syncthreads();
   constexpr int B = 8;  // global loads in flight per lane
-  for (int base0 = 0; base0 < H; base0 += B * kBlock) {
+  for (int base0 = 0; base0 < H; base0 += B * kPlanThreads) {
     uint64_t v[B];
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-      const int i = base0 + u * kBlock + (int)threadIdx.x;
+      const int i = base0 + u * kPlanThreads + (int)threadIdx.x;
       v[u] = i < H ? head[i] : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < B; ++u)
-      if (base0 + u * kBlock + (int)threadIdx.x < H) atomicAdd(&sm.hist[bucket_of(v[u])], 1u);
+      if (base0 + u * kPlanThreads + (int)threadIdx.x < H) atomicAdd(&sm.hist[bucket_of(v[u])], 1u);
   }
   __syncthreads();
   // Exclusive scan of the bucket counts: 16 buckets per thread, then across threads.
-  constexpr int kPer = kHeadBuckets / kBlock;
+  constexpr int kPer = kHeadBuckets / kPlanThreads;
   uint32_t local[kPer], run = 0;
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     local[q] = run;
     run += sm.hist[threadIdx.x * kPer + q];
   }
-  uint32_t total;
-  const uint32_t base = block_exclusive_scan(run, sm.bs, &total);
+  // Across the workgroup: wave scans, then the totals of the waves below.
+  const uint32_t inc = wave_inclusive_scan_u32(run);
+  if (wave_lane() == kWaveSize - 1) sm.wave_total[wave_id()] = inc;
+  __syncthreads();
+  uint32_t base = inc - run;
+  for (int k = 0; k < wave_id(); ++k) base += sm.wave_total[k];
 #pragma unroll
   for (int q = 0; q < kPer; ++q) sm.start[threadIdx.x * kPer + q] = base + local[q];
   __syncthreads();
   const int slots = min((int)((uint32_t)H / kSegCap) + 1, W.plan_stride - 2);
-  for (int g = threadIdx.x; g < slots; g += kBlock) plan[2 + g] = g == 0 ? 0u : ~0u;
+  for (int g = threadIdx.x; g < slots; g += kPlanThreads) plan[2 + g] = g == 0 ? 0u : ~0u;
   __syncthreads();
   // Segment starts: a bucket whose start reaches a new multiple of kSegCap.
-  for (int b = 1 + (int)threadIdx.x; b < kHeadBuckets; b += kBlock) {
+  for (int b = 1 + (int)threadIdx.x; b < kHeadBuckets; b += kPlanThreads) {
     const uint32_t st = sm.start[b];
     const uint32_t g = st / kSegCap, gp = sm.start[b - 1] / kSegCap;
     if (g != gp && st < (uint32_t)H && (int)g < slots) plan[2 + g] = st;
@@ -1955,16 +1961,16 @@ __global__ __launch_bounds__(kBlock) void head_plan_kernel(Launch L, Workspace W
   }
   // Scatter into bucket order (unsorted within a bucket).
   __syncthreads();
-  for (int base0 = 0; base0 < H; base0 += B * kBlock) {
+  for (int base0 = 0; base0 < H; base0 += B * kPlanThreads) {
     uint64_t v[B];
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-      const int i = base0 + u * kBlock + (int)threadIdx.x;
+      const int i = base0 + u * kPlanThreads + (int)threadIdx.x;
       v[u] = i < H ? head[i] : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < B; ++u)
-      if (base0 + u * kBlock + (int)threadIdx.x < H) sorted[atomicAdd(&sm.start[bucket_of(v[u])], 1u)] = v[u];
+      if (base0 + u * kPlanThreads + (int)threadIdx.x < H) sorted[atomicAdd(&sm.start[bucket_of(v[u])], 1u)] = v[u];
   }
 }
 
@@ -2362,7 +2368,7 @@ template <typename In, int VEC>
 hipError_t launch_head(const Launch &L, const Workspace &W, hipStream_t stream) {
   hipLaunchKernelGGL((head_kernel<In, VEC>), dim3((unsigned)(L.rows * L.h_splits)), dim3(kWaveSize), 0,
                      stream, L, W);
-  hipLaunchKernelGGL(head_plan_kernel, dim3((unsigned)L.rows), dim3(kBlock), 0, stream, L, W);
+  hipLaunchKernelGGL(head_plan_kernel, dim3((unsigned)L.rows), dim3(kPlanThreads), 0, stream, L, W);
   hipLaunchKernelGGL(head_sort_kernel, dim3((unsigned)(L.rows * (W.plan_stride - 2))), dim3(kBlock), 0,
                      stream, L, W);
   hipLaunchKernelGGL((head_finish_kernel<In>), dim3((unsigned)L.rows), dim3(kFinishThreads), 0, stream, L, W);
