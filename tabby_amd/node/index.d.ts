@@ -65,3 +65,10 @@ export declare class Sampler {
 }
 
 export declare function version(): string;
+
+/** A TopKResult as the sample block of forward.ts:127-157: f32 words [maxLogit, sumExp,
+ *  (value, index) * k], each index a u32 in its word. k defaults to all candidates. */
+export declare function encodeSampleBlock(top: TopKResult, k?: number): ArrayBuffer;
+
+/** forward.ts:142-157: the first k candidates of a sample block. */
+export declare function decodeSampleBlock(raw: ArrayBuffer, k: number): TopKResult;

@@ -13,6 +13,9 @@
  *                      sampleFromTopK (forward.ts:243-248, 442-451, 522-601;
  *                      sampler.ts:147-212), one launch for a batch of rows
  *   sample(logits, params, rng)   the one-row call of inference.worker.ts:162-168
+ *   encodeSampleBlock / decodeSampleBlock   the sample block a decode step reads back
+ *                      (forward.ts:127-157): [maxLogit, sumExp, (value, index) * k] as
+ *                      f32 words, each index a u32 in its word's bytes
  *
  * Every sampling computation runs on the GPU. There is no JavaScript fallback: if the
  * addon or the library is missing, require() throws.
@@ -206,8 +209,51 @@ class Sampler {
   }
 }
 
+// The reference's sample block (forward.ts:127-129, 142-157): f32 words [maxLogit, sumExp,
+// then (value, index) per candidate], the index written as a u32 into its word.
+const SAMPLE_HEADER_FLOATS = 2;
+
+/** A TopKResult as a sample block of k slots (default: all of its candidates). */
+function encodeSampleBlock(top, k) {
+  const n = k === undefined ? top.ids.length : k;
+  if (!(n >= 0) || n > top.ids.length || top.logits.length !== top.ids.length) {
+    throw new Error('encodeSampleBlock: k must be within the result\'s ' + top.ids.length + ' candidates');
+  }
+  const raw = new ArrayBuffer((SAMPLE_HEADER_FLOATS + 2 * n) * 4);
+  const asFloat = new Float32Array(raw);
+  const asUint = new Uint32Array(raw);
+  asFloat[0] = top.maxLogit;
+  asFloat[1] = top.sumExp;
+  for (let i = 0; i < n; i++) {
+    const slot = SAMPLE_HEADER_FLOATS + i * 2;
+    asFloat[slot] = top.logits[i];
+    asUint[slot + 1] = top.ids[i] >>> 0;
+  }
+  return raw;
+}
+
+/** The first k candidates of a sample block, as a TopKResult. */
+function decodeSampleBlock(raw, k) {
+  const asFloat = new Float32Array(raw);
+  const asUint = new Uint32Array(raw);
+  if (SAMPLE_HEADER_FLOATS + 2 * k > asFloat.length) {
+    throw new Error('decodeSampleBlock: the block holds ' + ((asFloat.length - SAMPLE_HEADER_FLOATS) >> 1) +
+                    ' candidates, asked for ' + k);
+  }
+  const ids = [];
+  const logits = [];
+  for (let i = 0; i < k; i++) {
+    const slot = SAMPLE_HEADER_FLOATS + i * 2;
+    ids.push(asUint[slot + 1]);
+    logits.push(asFloat[slot]);
+  }
+  return { maxLogit: asFloat[0], sumExp: asFloat[1], ids, logits };
+}
+
 module.exports = {
   Sampler,
+  encodeSampleBlock,
+  decodeSampleBlock,
   DeviceLogits,
   SeededRandom,
   DEFAULT_SAMPLING,

@@ -142,6 +142,37 @@ class TopKResult:
     logits: List[float] = field(default_factory=list)
 
 
+SAMPLE_HEADER_FLOATS = 2  # forward.ts:127-129: [maxLogit, sumExp, (value, index) * k]
+
+
+def encode_sample_block(top: TopKResult, k: Optional[int] = None) -> bytes:
+    """A TopKResult as the sample block a decode step reads back (forward.ts:127-157): f32
+    words [maxLogit, sumExp, then (value, index) per candidate], each index a u32 written
+    into its word. ``k`` defaults to all of the result's candidates."""
+    n = len(top.ids) if k is None else int(k)
+    if not 0 <= n <= len(top.ids) or len(top.logits) != len(top.ids):
+        raise ValueError(f"encode_sample_block: k must be within the result's {len(top.ids)} candidates")
+    block = np.zeros(SAMPLE_HEADER_FLOATS + 2 * n, dtype=np.float32)
+    block[0] = top.maxLogit
+    block[1] = top.sumExp
+    block[SAMPLE_HEADER_FLOATS::2] = np.asarray(top.logits[:n], dtype=np.float32)
+    block.view(np.uint32)[SAMPLE_HEADER_FLOATS + 1::2] = np.asarray(top.ids[:n], dtype=np.uint32)
+    return block.tobytes()
+
+
+def decode_sample_block(raw: bytes, k: int) -> TopKResult:
+    """forward.ts:142-157: the first k candidates of a sample block, read through an f32 and
+    a u32 view of the same bytes."""
+    as_float = np.frombuffer(raw, dtype=np.float32)
+    as_uint = np.frombuffer(raw, dtype=np.uint32)
+    if SAMPLE_HEADER_FLOATS + 2 * k > as_float.size:
+        raise ValueError(f"decode_sample_block: the block holds {(as_float.size - SAMPLE_HEADER_FLOATS) // 2} "
+                         f"candidates, asked for {k}")
+    slots = SAMPLE_HEADER_FLOATS + 2 * np.arange(k)
+    return TopKResult(float(as_float[0]), float(as_float[1]),
+                      [int(v) for v in as_uint[slots + 1]], [float(v) for v in as_float[slots]])
+
+
 def outcome_of(rec) -> SampleOutcome:
     return SampleOutcome(id=int(rec["id"]), probability=float(rec["probability"]),
                          consideredCount=int(rec["considered"]), poolMass=float(rec["pool_mass"]),

@@ -5,6 +5,8 @@
  *   node node_host.js sample SPEC.json     -> writes SPEC.out: one outcome per row, sampled
  *                                             through Sampler.sampleBatch in one launch
  *   node node_host.js api                  -> exercises sample()/SeededRandom/errors, prints JSON
+ *   node node_host.js wire JSON            -> {top, k, block64}: the encoded block of `top` (base64)
+ *                                             and the decoding of block64 with k candidates
  * SPEC.json: {logits: path, dtype: "f32"|"f16", rows, vocab, topK[], temperature[], topP[],
  *             uniform[], topkCap, kMax, out}
  */
@@ -16,6 +18,12 @@ function main() {
   const cmd = process.argv[2];
   if (cmd === 'load') {
     console.log(JSON.stringify({ version: tabby.version() }));
+  } else if (cmd === 'wire') {
+    const spec = JSON.parse(process.argv[3]);
+    const enc = Buffer.from(tabby.encodeSampleBlock(spec.top, spec.k)).toString('base64');
+    const b = Buffer.from(spec.block64, 'base64');
+    const raw = b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength);
+    console.log(JSON.stringify({ encoded: enc, decoded: tabby.decodeSampleBlock(raw, spec.k) }));
   } else if (cmd === 'sample') {
     const spec = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
     const buf = fs.readFileSync(spec.logits);
