@@ -549,44 +549,4 @@ __device__ __forceinline__ SeqSum block_seq_sum_wide(In t, int n, Out out, bool 
   return {P, n};
 }
 
-// Two independent left-to-right sums over the same length (poolMass and the scaled total):
-// short ones interleave on lane 0, long ones use the wave scan for each. The second is
-// skipped (0) when want_b is false.
-__device__ __forceinline__ void wave_seq_sum2(const double *a, const double *b, int n, bool want_b,
-                                              double *sum_a, double *sum_b) {
-  if (n > kSeqShort) {
-    *sum_a = wave_seq_sum(a, n, nullptr, INFINITY).total;
-    *sum_b = want_b ? wave_seq_sum(b, n, nullptr, INFINITY).total : 0.0;
-    return;
-  }
-  // Both chains on every lane, interleaved (uniform control flow, see uniform_seq_sum).
-  double pa = a[0], pb = b[0];
-  int i = 1;
-  for (; i + 8 <= n; i += 8) {
-    double va[8], vb[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      va[q] = a[i + q];
-      vb[q] = b[i + q];
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      pa += va[q];
-      pb += vb[q];
-    }
-  }
-  for (; i < n; ++i) {
-    pa += a[i];
-    pb += b[i];
-  }
-  auto bcast = [](double v) {
-    const uint64_t bits = (uint64_t)__double_as_longlong(v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bits);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bits >> 32));
-    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-  };
-  *sum_a = bcast(pa);
-  *sum_b = want_b ? bcast(pb) : 0.0;
-}
-
 }  // namespace tabby

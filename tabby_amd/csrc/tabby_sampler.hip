@@ -209,14 +209,15 @@ __device__ void finish_row(Smem &sm, const Launch &L, int row, const In *row_src
     w[i] = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
   }
   __syncthreads();
-  // Sequential sums (bit-exact, computed by wave 0; see seqsum.h).
+  // Sequential sums (bit-exact; see seqsum.h): poolMass on wave 0 and the scaled total on
+  // wave 1 at the same time. (The 16-terms-per-lane form reads 16 consecutive entries per
+  // lane, which these unpadded LDS arrays serve with bank conflicts: slower here.)
   if (wave_id() == 0) {
-    double pool, scaled;
-    wave_seq_sum2(exact, w, count, T > 0.0, &pool, &scaled);
-    if (lane_id() == 0) {
-      sm.pool_mass = pool;
-      sm.scaled_total = scaled;
-    }
+    const double pool = wave_seq_sum(exact, count, nullptr, INFINITY).total;
+    if (lane_id() == 0) sm.pool_mass = pool;
+  } else if (wave_id() == 1) {
+    const double scaled = T > 0.0 ? wave_seq_sum(w, count, nullptr, INFINITY).total : 0.0;
+    if (lane_id() == 0) sm.scaled_total = scaled;
   }
   __syncthreads();
   const double pool_mass = sm.pool_mass;
