@@ -39,6 +39,10 @@ def parse_args():
     ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5], default=None,
                     help="run BASELINE.json's configs[N-1] exactly as generated (parameters, "
                          "dtype and shape) instead of the headline; a secondary measurement")
+    ap.add_argument("--host-params", action="store_true",
+                    help="time the host-parameter entry (tabby_sampler_sample: parameters uploaded "
+                         "and results read back every call, synchronously) instead of the "
+                         "device-resident one; a secondary, PCIe-inclusive measurement")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -144,7 +148,15 @@ def main() -> int:
     whole = bool(np.any((w.top_k <= 0) | (w.top_k >= w.vocab))) and w.vocab > kcap
     flags = S.TABBY_FLAG_FULL_VOCAB if whole else 0
 
+    hparams = [np.roll(params, (b * 61) % w.rows) for b in range(ROTATE)]
+
     def step(i: int) -> None:
+        if args.host_params:
+            res_h, _, _ = sampler.sample_params(buffers[i % ROTATE], hparams[i % ROTATE],
+                                                stream=stream)
+            if res_h["status"].any():
+                raise RuntimeError("bench: a row returned a nonzero status")
+            return
         sampler.sample_device(buffers[i % ROTATE], pbufs[i % ROTATE], results, flags=flags,
                               stream=stream)
 
@@ -178,7 +190,8 @@ def main() -> int:
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "sample_kernel_config3_traffic.json")
-    headline = args.config is None and args.dtype == "f32" and not args.mixed_params
+    headline = (args.config is None and args.dtype == "f32" and not args.mixed_params
+                and not args.host_params)
     if os.path.exists(tpath) and headline:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -189,7 +202,8 @@ def main() -> int:
     if args.config is None:
         metric = "sampled rows/sec + achieved HBM GB/s, 256x151936 fp32 logits, top-k50/top-p0.9"
         config = {
-            "workload": "config3-headline" if not args.mixed_params else "config3-mixed",
+            "workload": ("config3-mixed" if args.mixed_params else "config3-headline")
+                        + ("-host-params" if args.host_params else ""),
             "rows": w.rows, "vocab": w.vocab,
             "top_k": "per-row {1,20,50,100}" if args.mixed_params else args.top_k,
             "top_p": "per-row {0.8,0.95,1.0}" if args.mixed_params else args.top_p,
@@ -205,6 +219,10 @@ def main() -> int:
                   "top_p": sorted(set(float(p) for p in w.top_p)),
                   "temperature": sorted(set(float(t) for t in w.temperature)),
                   "parallelism": "single GPU"}
+    if args.host_params:
+        metric += "; host-parameter entry, PCIe-inclusive (upload, sample, read back, sync)"
+        if args.config is not None:
+            config["workload"] += "-host-params"
     out = {
         "metric": metric,
         "value": round(rows_per_s, 1),
@@ -231,7 +249,9 @@ def main() -> int:
             "kernel": ("one tabby_sampler_sample_device call = row_kernel, one workgroup per "
                        "row (streaming: max, sum-exp, candidates; then in LDS the exact top-k, "
                        "top-p and draw); duration = HIP-event time of the back-to-back timed "
-                       "calls / steps"),
+                       "calls / steps") if not args.host_params else
+                      ("one synchronous tabby_sampler_sample call (parameter upload, the "
+                       "sampling kernels, result read-back); duration = HIP-event time / steps"),
             "bytes_per_launch": bytes_per_launch,
             "duration_us": round(avg_ms * 1000, 2),
         },

@@ -865,20 +865,47 @@ __device__ __forceinline__ Pruned wave_prune_any(WaveSmem &sm, int count, int kk
   return wave_prune<8>(sm, count, kk, floor_key);
 }
 
+// Registers per lane (1, 2, 4 or 8) for the union of the row's published lane-maximum keys:
+// each of `waves` waves publishes m = min(64, 64 * regs / waves) keys, and the union must hold
+// at least kk of them (kk <= 256 here; 8 always suffices for 5 to 16 waves).
+__device__ __forceinline__ int bound_regs(int kk, int waves) {
+  for (int r = 1; r < 8; r *= 2)
+    if (waves * min(kWaveSize, kWaveSize * r / waves) >= kk) return r;
+  return 8;
+}
+
+// The kk-th largest (1 <= kk <= total <= 64 * R) of keys[0..total), on every lane.
+template <int R>
+__device__ __forceinline__ uint32_t union_kth(const uint32_t *keys, int total, int kk) {
+  uint32_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + wave_lane();
+    v[r] = i < total ? keys[i] : 0u;
+  }
+  wave_sort_desc<R>(v);
+  const int p = kk - 1;
+  uint32_t t = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (r == p / kWaveSize) t = (uint32_t)__builtin_amdgcn_readlane((int)v[r], p % kWaveSize);
+  return t;
+}
+
 // One wave's share of row `row`: slice `slice` of L.slice_len elements or, when `claim` is
 // given (CLAIM), chunk `slice` of the whole row and then every chunk the wave claims from the
 // LDS counter *claim (shared by the row's waves, starting past their first chunks), so that
 // the row's waves end together however the SIMDs schedule them. Every statistic and list of
 // the wave is independent of which elements it saw: the max, sum-exp to 1e-5, and a
 // superset of the top kk of its elements. With CLAIM the row's `waves` waves (all of the
-// workgroup, *claim starting at `waves`) also agree on a first bound through *row_theta (an
-// LDS word holding 0xffffffff before the call) and one barrier. The wave's top min(count, kk), sorted descending,
+// workgroup, *claim starting at `waves`) also agree on a first bound through bound_keys (LDS
+// room for 8 x 64 keys) and one barrier. The wave's top min(count, kk), sorted descending,
 // go to out[0..keep) as composites (out may be sm.list itself: the list is read into
 // registers before anything is written), its statistics to *stat.
 template <typename In, int VEC, bool CLAIM>
 __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const tabby_row_params &P, int row,
                                            int slice, uint64_t *out, SliceStat *stat, int *claim,
-                                           uint32_t *row_theta, int waves) {
+                                           uint32_t *bound_keys, int waves) {
   const int V = L.vocab;
   const int begin = CLAIM ? 0 : slice * L.slice_len;
   const int n = CLAIM ? V : min(L.slice_len, V - begin);
@@ -974,31 +1001,49 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
     int b = next();
     if (b < full_chunks) wave_load_full<In, VEC>(src, b, y);
     else if (b < nchunks) wave_load<In, VEC>(src, n, b, y);
-    // The row's first bound, shared by its waves: wave w offers the kw-th largest of its
-    // first chunk's lane maxima, kw = ceil(kk / waves) -- kw distinct elements at or above
-    // it -- and the smallest offer has at least kk elements of the row at or above it, so it
-    // never exceeds the row's kk-th largest. (A wave alone could only offer the kk-th
-    // largest of its 64 lane maxima.) Every wave passes the barrier once.
-    {
-      const int kw = (kk + waves - 1) / waves;
-      uint32_t offer = kNegInfKey;
-      if (kk > 0 && kw <= kWaveSize && a < nchunks) {
+    // The row's first bound, shared by its waves. A wave's 64 lane maxima over its first two
+    // chunks are 64 distinct elements of the row; each wave publishes its m largest, and the
+    // kk-th largest of the union (waves * m >= kk keys) has kk distinct elements at or above
+    // it, so it never exceeds the row's kk-th largest. (The union is much tighter than any
+    // one wave's offer: the row's top lane maxima are spread over the waves.) Every wave
+    // passes the barrier once and computes the same bound.
+    if (kk > 0) {
+      const int regs = bound_regs(kk, waves);
+      const int m = min(kWaveSize, kWaveSize * regs / waves);
+      float cm = -INFINITY;
+      if (a < nchunks) {
         if (a >= full_chunks) {
 #pragma unroll
           for (int e = 0; e < kWChunkPerLane; ++e)
             if (wave_local<VEC>(a, e) >= n) x[e] = -INFINITY;
         }
-        float cm = x[0];
 #pragma unroll
-        for (int e = 1; e < kWChunkPerLane; ++e) cm = fmaxf(cm, x[e]);
-        uint32_t k1[1] = {key_of(cm)};
-        wave_sort_desc<1>(k1);
-        offer = min(max((uint32_t)__builtin_amdgcn_readlane((int)k1[0], kw - 1), kNegInfKey), 0xff800000u);
+        for (int e = 0; e < kWChunkPerLane; ++e) cm = fmaxf(cm, x[e]);
       }
-      if (wave_lane() == 0) atomicMin(row_theta, offer);
+      if (b < nchunks) {
+        if (b >= full_chunks) {
+#pragma unroll
+          for (int e = 0; e < kWChunkPerLane; ++e)
+            if (wave_local<VEC>(b, e) >= n) y[e] = -INFINITY;
+        }
+#pragma unroll
+        for (int e = 0; e < kWChunkPerLane; ++e) cm = fmaxf(cm, y[e]);
+      }
+      uint32_t k1[1] = {key_of(cm)};
+      wave_sort_desc<1>(k1);
+      if (wave_lane() < m) bound_keys[slice * m + wave_lane()] = min(max(k1[0], kNegInfKey), 0xff800000u);
       __syncthreads();
-      theta_key = max(theta_key, (uint32_t)__builtin_amdgcn_readfirstlane((int)*row_theta));
+      uint32_t t;
+      switch (regs) {
+        case 1: t = union_kth<1>(bound_keys, waves * m, kk); break;
+        case 2: t = union_kth<2>(bound_keys, waves * m, kk); break;
+        case 4: t = union_kth<4>(bound_keys, waves * m, kk); break;
+        default: t = union_kth<8>(bound_keys, waves * m, kk); break;
+      }
+      theta_key = max(theta_key, t);
       theta = value_of(theta_key);
+    } else {
+      __syncthreads();
     }
     if (a < nchunks) step(a, nchunks, false, x, y);  // chunk b is already in flight
     while (b < nchunks) {
@@ -1759,7 +1804,7 @@ struct RowSmem {
   SliceStat stats[kRowWaves];
   WaveMergeSmem merge;
   int next_chunk;
-  uint32_t row_theta;
+  uint32_t bound_keys[8 * kWaveSize];
 };
 
 template <typename In, int VEC>
@@ -1771,11 +1816,10 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   const tabby_row_params P = L.params[row];  // kept in registers for the merge
   if (threadIdx.x == 0) {
     sm.next_chunk = nw;  // chunk w is wave w's first
-    sm.row_theta = 0xffffffffu;
   }
   __syncthreads();
   wave_slice<In, VEC, true>(sm.wave[w], L, P, row, w, sm.wave[w].list, &sm.stats[w], &sm.next_chunk,
-                            &sm.row_theta, nw);
+                            sm.bound_keys, nw);
   __syncthreads();
   constexpr int stride = (int)(sizeof(WaveSmem) / sizeof(uint64_t));
   const RowLists lists{sm.wave[0].list, nw, stride, (int64_t)nw * stride};
