@@ -317,3 +317,29 @@ def test_row_kernel_300_rows(oracle):
                               k_choices=(1, 50, 128))
     res, ids, vals = run_gpu(w, k_max=128, topk_cap=128)
     _log("row kernel 300 rows", compare(w, res, ids, vals, run_oracle(oracle, w, 128), 128))
+
+
+def test_row_kernel_shared_bound_adversarial(oracle):
+    # The row kernel's first bound is the k-th largest of the union of the waves' top lane
+    # maxima over their first two chunks. Rows built against it, 16 waves per row: the top
+    # of the row inside wave 0's first chunk; the top packed into one lane of every chunk (a
+    # lane maximum stands for one of its 16 elements); ascending rows (every first chunk is
+    # the smallest); the top in the last chunks only (claimed last).
+    V = 60000
+    w = synth.random_workload(rows=256, vocab=V, seed=97, ties=False,
+                              k_choices=(1, 50, 64, 65, 128, 129, 200, 256), sigma=1.0)
+    rng = np.random.default_rng(97)
+    pos = np.arange(V)
+    one_lane = ((pos % 1024) % 256) // 4 == 0  # lane 0 of every 1,024-element chunk
+    for r in range(256):
+        kind = r % 4
+        if kind == 0:
+            w.logits[r, :1024] = (12.0 + rng.standard_normal(1024)).astype(np.float32)
+        elif kind == 1:
+            w.logits[r, one_lane] = (12.0 + rng.standard_normal(int(one_lane.sum()))).astype(np.float32)
+        elif kind == 2:
+            w.logits[r] = np.sort(w.logits[r])
+        else:
+            w.logits[r, V - 4096:] = (12.0 + rng.standard_normal(4096)).astype(np.float32)
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=256)
+    _log("row kernel shared bound", compare(w, res, ids, vals, run_oracle(oracle, w, 256), 256))
