@@ -126,12 +126,23 @@ def test_k_at_least_vocab_takes_whole_row(oracle):
     compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100)
 
 
-def test_repeatable_bit_for_bit():
-    w = synth.config(3, rows=32)
-    a = run_gpu(w, k_max=128, topk_cap=100)
-    b = run_gpu(w, k_max=128, topk_cap=100)
-    assert a[0].tobytes() == b[0].tobytes()
+def assert_same_result(a, b):
+    """Two runs of the same rows: ids, counts, flags, max and the top-k lists bit for bit.
+    The row kernel's waves claim chunks in whatever order they run and keep sum-exp as f32
+    terms relative to each lane's running max, so sum-exp -- and the probability and poolMass
+    divided by it -- repeat to those terms' rounding (~1e-9 relative; the contract's
+    tolerance is 1e-5)."""
+    for f in ("id", "considered", "max_logit", "status", "topk_count"):
+        assert a[0][f].tobytes() == b[0][f].tobytes(), f
+    for f in ("probability", "pool_mass", "sum_exp"):
+        np.testing.assert_allclose(a[0][f], b[0][f], rtol=1e-6, atol=0, err_msg=f)
     assert np.array_equal(a[1], b[1]) and np.array_equal(a[2].view(np.uint32), b[2].view(np.uint32))
+
+
+@pytest.mark.parametrize("rows", [1, 32, 256])
+def test_repeatable(rows):
+    w = synth.config(3, rows=rows)
+    assert_same_result(run_gpu(w, k_max=128, topk_cap=100), run_gpu(w, k_max=128, topk_cap=100))
 
 
 def test_reuse_handle_across_calls(oracle):
@@ -140,7 +151,7 @@ def test_reuse_handle_across_calls(oracle):
     with S.GpuSampler(vocab_max=30000, rows_max=8, k_max=64) as g:
         first = run_gpu(w, sampler=g, topk_cap=64)
         second = run_gpu(w, sampler=g, topk_cap=64)
-    assert first[0].tobytes() == second[0].tobytes()
+    assert_same_result(first, second)
     compare(w, *first, run_oracle(oracle, w, 64), 64)
 
 
@@ -343,3 +354,23 @@ def test_row_kernel_shared_bound_adversarial(oracle):
             w.logits[r, V - 4096:] = (12.0 + rng.standard_normal(4096)).astype(np.float32)
     res, ids, vals = run_gpu(w, k_max=256, topk_cap=256)
     _log("row kernel shared bound", compare(w, res, ids, vals, run_oracle(oracle, w, 256), 256))
+
+
+@pytest.mark.parametrize("rows", [1, 5, 17, 64])
+def test_row_kernel_parts(oracle, rows):
+    # Fewer rows than half the CUs: each row is split into parts of one 16-wave workgroup
+    # each (seven parts of 100,000 here, four at 64 rows), and a second kernel merges the
+    # parts' sorted lists; ties, -inf, pools up to 256, greedy and whole-vocabulary rows.
+    w = synth.random_workload(rows=rows, vocab=100000, seed=101 + rows, ties=True, neg_inf_frac=0.2,
+                              k_choices=(0, 1, 50, 64, 65, 256), temperatures=(0.0, 0.3, 1.0))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=64)
+    _log(f"row kernel parts, {rows} rows", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
+@pytest.mark.parametrize("vocab", [33000, 49152])
+def test_row_kernel_one_workgroup_few_rows(oracle, vocab):
+    # Rows of two or three parts' length with few rows: one 16-wave workgroup per row
+    # streams and finishes it alone.
+    w = synth.random_workload(rows=3, vocab=vocab, seed=7 + vocab, k_choices=(1, 40, 256))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=40)
+    _log(f"row kernel one workgroup, vocab {vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 40), 40))
