@@ -9,7 +9,9 @@
 // Here one call samples a whole batch on the caller's stream. A batch of at least as many
 // rows as the device has CUs (pools up to 256) takes one kernel, row_kernel: one workgroup
 // per row, whose waves stream the row and then merge in LDS what the two kernels below
-// exchange through global memory. Smaller batches, and pools above 256, take two kernels:
+// exchange through global memory. A batch of fewer rows than half the CUs runs row_kernel on
+// parts of each row (one workgroup per part) and merges the parts' lists with
+// wave_merge_kernel. Other batches, and pools above 256, take two kernels:
 //   * wave_kernel (slice_kernel for pools above 256): grid = rows x splits; each wave
 //     (workgroup) owns one slice of one row and reads it from HBM exactly once with 16-byte
 //     nontemporal loads into registers. From registers it keeps the slice max, the slice sum
