@@ -9,9 +9,10 @@
 // Here one call samples a whole batch on the caller's stream. A batch of at least as many
 // rows as the device has CUs (pools up to 256) takes one kernel, row_kernel: one workgroup
 // per row, whose waves stream the row and then merge in LDS what the two kernels below
-// exchange through global memory. A batch of fewer rows than half the CUs runs row_kernel on
-// parts of each row (one workgroup per part) and merges the parts' lists with
-// wave_merge_kernel. Other batches, and pools above 256, take two kernels:
+// exchange through global memory. A batch of up to half as many rows as CUs runs row_kernel
+// on parts of each row (one workgroup per part) and merges the parts' lists with
+// wave_merge_kernel, or, where that would give two or three parts, one workgroup per row.
+// Other batches, and pools above 256, take two kernels:
 //   * wave_kernel (slice_kernel for pools above 256): grid = rows x splits; each wave
 //     (workgroup) owns one slice of one row and reads it from HBM exactly once with 16-byte
 //     nontemporal loads into registers. From registers it keeps the slice max, the slice sum
@@ -2419,7 +2420,7 @@ Plan make_plan(int rows, int vocab, int dtype, const void *logits, bool wave) {
 // fit one workgroup.
 bool per_row_launch(const Launch &L, int cus) { return L.kcap <= kWaveKcap && L.rows >= cus && L.splits <= kRowWaves; }
 
-// Fewer rows than half the CUs (pools <= 256): each row is cut into parts of at least
+// Up to half as many rows as CUs (pools <= 256): each row is cut into parts of at least
 // kMinPart elements, one 16-wave row_kernel workgroup each, about one workgroup per CU in all;
 // wave_merge_kernel then merges the parts' sorted lists (one row of 151,936: 14.8 us in ten
 // parts against 18.8 us in 37 one-wave slices; 32 rows: 17.2 against 22.9 us). Returns the
