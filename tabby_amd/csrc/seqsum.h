@@ -167,13 +167,28 @@ __device__ __forceinline__ SeqSum lane_seq_sum(const double *t, int n, double *o
 // If out is non-null, out[j] receives the j-th partial sum (out may be t itself). The sum
 // stops at the first j whose partial sum is >= stop_at (INFINITY: none); count is then
 // j + 1. t and out live in LDS or global memory; all 64 lanes call this together.
+// A short sum with a stop (top-p's running sums) takes its first kSeqStopSerial terms one by
+// one -- peaked rows stop among them -- and the rest by the scan below: one by one, each term
+// waits on the previous add, its compare and a branch (config 1's flat rows run all 40).
+constexpr int kSeqStopSerial = 8;
+
 __device__ __forceinline__ SeqSum wave_seq_sum(const double *t, int n, double *out, double stop_at) {
-  if (n <= kSeqShort) return lane_seq_sum(t, n, out, stop_at);
+  const bool stop = stop_at < INFINITY;
+  if (n <= kSeqShort && (!stop || n <= kSeqStopSerial)) return lane_seq_sum(t, n, out, stop_at);
   const int lane = wave_lane();
-  double P = t[0];
-  if (out && lane == 0) out[0] = P;
-  if (P >= stop_at) return {P, 1};
-  int a = 1;
+  double P;
+  int a;
+  if (n <= kSeqShort) {
+    const SeqSum head = lane_seq_sum(t, kSeqStopSerial, out, stop_at);
+    if (head.count < kSeqStopSerial || head.total >= stop_at) return head;
+    P = head.total;
+    a = kSeqStopSerial;
+  } else {
+    P = t[0];
+    if (out && lane == 0) out[0] = P;
+    if (P >= stop_at) return {P, 1};
+    a = 1;
+  }
   while (a < n) {
     // The binade of P: P = m * u with m in [2^52, 2^53).
     const int E = ((int)((uint64_t)__double_as_longlong(P) >> 52) & 0x7ff) - 1023;
