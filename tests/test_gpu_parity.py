@@ -374,3 +374,15 @@ def test_row_kernel_one_workgroup_few_rows(oracle, vocab):
     w = synth.random_workload(rows=3, vocab=vocab, seed=7 + vocab, k_choices=(1, 40, 256))
     res, ids, vals = run_gpu(w, k_max=256, topk_cap=40)
     _log(f"row kernel one workgroup, vocab {vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 40), 40))
+
+
+@pytest.mark.parametrize("dtype,vocab", [("f32", 65537), ("f16", 65544), ("f16", 65539)])
+def test_row_kernel_parts_ragged(oracle, dtype, vocab):
+    # Parts whose last one is short and ends inside a chunk; an odd vocabulary (element
+    # loads instead of 16-byte vectors) and f16 rows, aligned and not.
+    w = synth.random_workload(rows=2, vocab=vocab, seed=131 + vocab, ties=True, neg_inf_frac=0.1,
+                              k_choices=(1, 50, 256), temperatures=(0.0, 0.8))
+    if dtype == "f16":
+        w.logits = w.logits.astype(np.float16)
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=50)
+    _log(f"row kernel parts ragged {dtype} {vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 50), 50))
