@@ -386,3 +386,17 @@ def test_row_kernel_parts_ragged(oracle, dtype, vocab):
         w.logits = w.logits.astype(np.float16)
     res, ids, vals = run_gpu(w, k_max=256, topk_cap=50)
     _log(f"row kernel parts ragged {dtype} {vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 50), 50))
+
+
+@pytest.mark.xfail(strict=False, reason="known: a whole-vocabulary row with a 90 K-entry head of "
+                   "quantised logits at T = 2 draws one position late inside a run of 3,573 ties "
+                   "(the eight-wave running sums of head_finish_kernel are the suspect)")
+def test_full_vocab_huge_tied_head_draw(oracle):
+    # Found by a randomized sweep: row 6 (k = 0, T = 2.0, top-p 0.9, u = 0.753) of this
+    # workload; consideredCount agrees (36,932), the id does not (16,128 vs 16,106, adjacent
+    # positions 13,294 / 13,293 of a tie run at 3.0).
+    w = synth.random_workload(rows=200, vocab=100000, seed=770792225, ties=True, neg_inf_frac=0.1,
+                              k_choices=(2, 0, 0), temperatures=(0.0, 0.3, 0.7, 1.0, 2.0),
+                              top_ps=(0.5, 0.9, 0.95, 1.0))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=40)
+    compare(w, res, ids, vals, run_oracle(oracle, w, 40), 40)
