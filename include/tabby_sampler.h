@@ -127,7 +127,8 @@ TABBY_API int tabby_debug_exp(const double *x_dev, double *y_dev, int64_t n, voi
  * one wave. terms_dev[0..n) must be >= 0 with terms_dev[0] > 0; prefix_dev[j] receives the
  * j-th partial sum up to the first that is >= stop_at (INFINITY: none), and *count_dev the
  * number of partial sums written. wide = 1 selects the form used for long sums (16 terms per
- * lane per step), wide = 2 the same taken by a four-wave workgroup (whole-vocabulary heads).
+ * lane per step), wide = 2 the same taken by a four-wave workgroup, wide = 3 by an eight-wave
+ * workgroup (the form that finishes whole-vocabulary heads).
  * For parity tests.
  */
 TABBY_API int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double stop_at,

@@ -2322,11 +2322,12 @@ __global__ __launch_bounds__(kWaveSize) void seq_sum_kernel(const double *t, int
   if (wave_lane() == 0) *count = r.count;
 }
 
-// The same by a 256-lane workgroup (block_seq_sum_wide).
-__global__ __launch_bounds__(kBlock) void seq_sum_block_kernel(const double *t, int32_t n, double stop_at,
-                                                              double *out, int32_t *count) {
-  __shared__ SeqScratch<kWaves> sc;
-  const SeqSum r = block_seq_sum_wide<kWaves>(t, n, out, true, stop_at, false, sc);
+// The same by a workgroup of NW waves (block_seq_sum_wide; head_finish_kernel runs NW = 8).
+template <int NW>
+__global__ __launch_bounds__(NW * kWaveSize) void seq_sum_block_kernel(const double *t, int32_t n, double stop_at,
+                                                                       double *out, int32_t *count) {
+  __shared__ SeqScratch<NW> sc;
+  const SeqSum r = block_seq_sum_wide<NW>(t, n, out, true, stop_at, false, sc);
   if (threadIdx.x == 0) *count = r.count;
 }
 
@@ -2722,8 +2723,11 @@ int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double stop_at, doub
   if (!terms_dev || !prefix_dev || !count_dev) return fail(TABBY_EINVAL, "null pointer");
   if (n < 1) return fail(TABBY_EINVAL, "n must be >= 1");
   if (wide == 2)
-    hipLaunchKernelGGL(seq_sum_block_kernel, dim3(1), dim3(kBlock), 0, (hipStream_t)stream, terms_dev, n, stop_at,
-                       prefix_dev, count_dev);
+    hipLaunchKernelGGL(seq_sum_block_kernel<kWaves>, dim3(1), dim3(kWaves * kWaveSize), 0, (hipStream_t)stream,
+                       terms_dev, n, stop_at, prefix_dev, count_dev);
+  else if (wide == 3)
+    hipLaunchKernelGGL(seq_sum_block_kernel<kFinishThreads / kWaveSize>, dim3(1), dim3(kFinishThreads), 0,
+                       (hipStream_t)stream, terms_dev, n, stop_at, prefix_dev, count_dev);
   else
     hipLaunchKernelGGL(seq_sum_kernel, dim3(1), dim3(kWaveSize), 0, (hipStream_t)stream, terms_dev, n,
                        stop_at, prefix_dev, count_dev, wide);

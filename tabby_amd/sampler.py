@@ -335,7 +335,7 @@ def device_seq_sum(terms, stop_at: float = float("inf"), wide: int = 0):
     """The device's sequential f64 partial sums of a CUDA float64 tensor (diagnostic):
     returns (prefix sums actually written, as a CUDA tensor, count). ``wide``: 0 the
     one-term-per-lane form, 1 the 16-terms-per-lane form used for long sums, 2 that form
-    taken by a four-wave workgroup."""
+    taken by a four-wave workgroup, 3 by an eight-wave workgroup."""
     import torch
     t = terms.contiguous()
     out = torch.zeros_like(t)

@@ -390,7 +390,7 @@ def test_row_kernel_parts_ragged(oracle, dtype, vocab):
 
 @pytest.mark.xfail(strict=False, reason="known: a whole-vocabulary row with a 90 K-entry head of "
                    "quantised logits at T = 2 draws one position late inside a run of 3,573 ties "
-                   "(the eight-wave running sums of head_finish_kernel are the suspect)")
+                   "(the running sums are exact; the head's order of equal keys is the suspect)")
 def test_full_vocab_huge_tied_head_draw(oracle):
     # Found by a randomized sweep: row 6 (k = 0, T = 2.0, top-p 0.9, u = 0.753) of this
     # workload; consideredCount agrees (36,932), the id does not (16,128 vs 16,106, adjacent
