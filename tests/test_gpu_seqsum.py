@@ -8,7 +8,7 @@ from tabby_amd import sampler as S
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=[0, 1, 2], ids=["lds", "wide", "block"])
+@pytest.fixture(params=[0, 1, 2, 3], ids=["lds", "wide", "block", "block8"])
 def wide(request):
     return request.param
 
