@@ -66,11 +66,39 @@ def copy_calibration() -> int:
     return 0
 
 
+def _oracle():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle  # test infrastructure: the CPU leg only (checker and baseline)
+    return oracle
+
+
+def oracle_check(w, res, rows_to_check: int = 16) -> dict:
+    """The CPU leg's checker: the C oracle on a sample of the batch's rows against the GPU's
+    results for them (ids, consideredCount and maxLogit exact; probability, poolMass and
+    sumExp within 1e-5 relative). Outside the timed region."""
+    import numpy as np
+    oracle = _oracle()
+    pick = np.unique(np.linspace(0, w.rows - 1, min(rows_to_check, w.rows)).astype(int))
+    logits = w.logits_f32()
+    bad = []
+    for r in pick:
+        o = oracle.sample_row(logits[r], int(w.top_k[r]), float(w.temperature[r]),
+                              float(w.top_p[r]), float(w.uniform[r]))
+        g = res[r]
+        ok = (int(g["status"]) == o["status"] == 0 and int(g["id"]) == o["id"]
+              and int(g["considered"]) == o["considered"]
+              and np.float32(g["max_logit"]) == np.float32(o["max_logit"]))
+        for f in ("probability", "pool_mass", "sum_exp"):
+            ok = ok and abs(float(g[f]) - o[f]) <= 1e-5 * abs(o[f])
+        if not ok:
+            bad.append(int(r))
+    return {"rows_checked": int(pick.size), "mismatched_rows": bad}
+
+
 def cpu_baseline(w, seconds: float) -> dict | None:
     """The Node restatement of the reference CPU sampler (topK sort + sampleFromTopK) on a
     bounded sample of the same rows, single-threaded and across all host cores."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle  # test infrastructure: the baseline leg only
+    oracle = _oracle()
 
     if not oracle.node_available():
         return None
@@ -186,7 +214,18 @@ def main() -> int:
     ms_per_step = 1000.0 * wall / args.steps
     rows_per_s = w.rows * args.steps / wall
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+
+    # The answer of a timed call, checked after the timed region: batch 0 is the workload's
+    # own row order (the others are rotations of it).
+    if args.host_params:
+        res, _, _ = sampler.sample_params(buffers[0], hparams[0], stream=stream)
+    else:
+        results.zero_()
+        sampler.sample_device(buffers[0], pbufs[0], results, flags=flags, stream=stream)
+        torch.cuda.synchronize()
+        res = results.cpu().numpy().view(S.RESULT_DTYPE)
     sampler.close()
+    check = oracle_check(w, res)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "sample_kernel_config3_traffic.json")
@@ -256,8 +295,12 @@ def main() -> int:
             "duration_us": round(avg_ms * 1000, 2),
         },
         "cpu_baseline": cpu,
+        "parity": check,
     }
     print(json.dumps(out), flush=True)
+    if check["mismatched_rows"]:
+        print(f"bench: rows {check['mismatched_rows']} differ from the CPU oracle", file=sys.stderr)
+        return 1
     return 0
 
 

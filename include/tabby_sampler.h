@@ -128,12 +128,22 @@ TABBY_API int tabby_debug_exp(const double *x_dev, double *y_dev, int64_t n, voi
  * j-th partial sum up to the first that is >= stop_at (INFINITY: none), and *count_dev the
  * number of partial sums written. wide = 1 selects the form used for long sums (16 terms per
  * lane per step), wide = 2 the same taken by a four-wave workgroup, wide = 3 by an eight-wave
- * workgroup (the form that finishes whole-vocabulary heads).
+ * workgroup (the form that finishes whole-vocabulary heads). prefix_dev may be terms_dev
+ * itself (the sums are then written over their terms, as whole-vocabulary heads run them).
  * For parity tests.
  */
 TABBY_API int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double stop_at,
                                   double *prefix_dev, int32_t *count_dev, int32_t wide,
                                   void *stream);
+
+/*
+ * Diagnostic: the draw of sampleFromTopK (sampler.ts:195-203) as whole-vocabulary rows run
+ * it, a 64-ary search by one wave: for each of the m targets, out_dev[j] = the first i in
+ * [0, n) with targets_dev[j] < c_dev[i] (c non-decreasing), or n - 1 when there is none.
+ * For parity tests.
+ */
+TABBY_API int tabby_debug_first_above(const double *c_dev, int32_t n, const double *targets_dev,
+                                      int32_t m, int32_t *out_dev, void *stream);
 
 #ifdef __cplusplus
 }

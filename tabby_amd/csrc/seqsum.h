@@ -550,13 +550,16 @@ __device__ __forceinline__ SeqSum block_seq_sum_wide(In t, int n, Out out, bool 
     }
     const bool is_stop = sc.stop[fw] != 0u;
     const double before = sc.before[fw], at = sc.at[fw];
-    __syncthreads();  // sc is reused by the next step
+    // The event term is read by every wave before the barrier: with out == t, thread 0
+    // overwrites it with the partial sum right after.
+    const double t_flagged = is_stop ? 0.0 : t[flagged];
+    __syncthreads();  // sc is reused by the next step; every wave holds t[flagged]
     if (is_stop) {
       const double v = at * u;
       if (has_out && threadIdx.x == 0) out[flagged] = v;
       return {v, flagged + 1};
     }
-    P = before * u + t[flagged];
+    P = before * u + t_flagged;
     if (has_out && threadIdx.x == 0) out[flagged] = P;
     if (P >= stop_at) return {P, flagged + 1};
     a = flagged + 1;

@@ -49,6 +49,16 @@ namespace tabby {
 
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr int kMaxSplits = kBlock;  // one merge lane per slice
+
+// A lane's sum-exp is kept as the sum of 2^(x*L - ml) (L = kLog2e) against its own
+// reference ml = fl(lane_max * L). Rebased on a max m it is sum * 2^(ml - m*L), with m*L
+// formed exactly in f64 (two 24-bit significands): the exponent difference has no error
+// proportional to |m|, so the sum's accuracy does not depend on where the logits sit.
+__device__ __forceinline__ double rebase_sum(double sum, float lane_max, float ml, float m) {
+  if (lane_max == -INFINITY) return 0.0;
+  const double d = (double)ml - (double)m * (double)kLog2e;
+  return sum * (double)__builtin_amdgcn_exp2f((float)d);
+}
 constexpr int kKcapSmall = 256;
 constexpr int kKcapLarge = 1024;
 
@@ -562,7 +572,8 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
   }
   __syncthreads();
   float lane_max = -INFINITY;
-  double lane_sum = 0.0;  // sum of exp(x - lane_max) over this lane's elements so far
+  float lane_ml = 0.0f;   // fl(lane_max * L): the reference of lane_sum's terms (rebase_sum)
+  double lane_sum = 0.0;  // sum of 2^(x*L - lane_ml) over this lane's elements so far
 
   float x[kChunkPerLane], y[kChunkPerLane];
   load_chunk<In, VEC>(src, n, 0, x);
@@ -586,9 +597,10 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
         for (int e = 0; e < h; ++e) t[e] += t[e + h];
       }
       const float part = t[0];
-      const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f((lane_max - nm) * kLog2e);
+      const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f(lane_ml - ml);
       lane_sum = lane_sum * rescale + (double)part;
       lane_max = nm;
+      lane_ml = ml;
     }
 
     if (kk > 0) {
@@ -658,10 +670,7 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
 
   // Slice statistics (their barriers also publish `committed`).
   const float ms = block_max(lane_max, sm.bs);
-  const double term = lane_max == -INFINITY
-                          ? 0.0
-                          : lane_sum * (double)__builtin_amdgcn_exp2f((lane_max - ms) * kLog2e);
-  const double ss = block_sum(term, sm.bs);
+  const double ss = block_sum(rebase_sum(lane_sum, lane_max, lane_ml, ms), sm.bs);
   uint32_t total = 0;
   if (kk > 0) {
     uint32_t have = sm.committed;
@@ -926,7 +935,8 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
   const int prune_at = kWListCap - kWaveSize;
 
   float lane_max = -INFINITY;
-  double lane_sum = 0.0;  // sum of exp(x - lane_max) over this lane's elements so far
+  float lane_ml = 0.0f;   // fl(lane_max * L): the reference of lane_sum's terms
+  double lane_sum = 0.0;  // sum of 2^(x*L - lane_ml) over this lane's elements so far
   int count = 0;          // entries in the list; wave-uniform (readfirstlane keeps it scalar)
   uint32_t theta_key = kNegInfKey;
   float theta = -INFINITY;  // == value_of(theta_key)
@@ -948,6 +958,11 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
     for (int e = 1; e < kWChunkPerLane; ++e) cm = fmaxf(cm, cur[e]);
     const float nm = fmaxf(lane_max, cm);
     if (nm != -INFINITY) {
+      // The lane's terms are 2^(x*L - ml) with ml = fl(nm*L) (L = log2 e in f32), the
+      // product x*L exact inside the fma; ml itself is the reference the sum is kept
+      // against (lane_ml), so that its rounding -- about |nm| * 2^-24 -- does not scale the
+      // terms: rescales subtract references, and the end of the slice subtracts the exact
+      // product ms*L in f64. Errors then depend on x - max only, not on the max.
       const float ml = nm * kLog2e;
       // Pairwise sum: independent adds interleave with the exps (a running sum made one
       // dependent chain of 16 exp-add pairs per chunk).
@@ -960,9 +975,10 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
         for (int e = 0; e < h; ++e) t[e] += t[e + h];
       }
       const float part = t[0];
-      const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f((lane_max - nm) * kLog2e);
+      const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f(lane_ml - ml);
       lane_sum = lane_sum * rescale + (double)part;
       lane_max = nm;
+      lane_ml = ml;
     }
     if (kk == 0) return;
     if (first && kk < n && kk <= kWaveSize) {
@@ -1070,10 +1086,7 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
   }
 
   const float ms = wave_max(lane_max);
-  const double term = lane_max == -INFINITY
-                          ? 0.0
-                          : lane_sum * (double)__builtin_amdgcn_exp2f((lane_max - ms) * kLog2e);
-  const double ss = wave_sum(term);
+  const double ss = wave_sum(rebase_sum(lane_sum, lane_max, lane_ml, ms));
   // The slice's top min(count, kk), sorted descending: the merge only has to merge sorted
   // lists.
   int keep = 0;
@@ -2181,8 +2194,10 @@ __device__ __forceinline__ int wave_first_above(C c, int n, double target) {
     const int probe = lo + wave_lane() * step;
     const uint64_t hit = __ballot(probe < hi && target < c[min(probe, n - 1)]);
     if (!hit) {
-      lo = lo + (kWaveSize - 1) * step + 1;
-      lo = min(lo, hi);
+      // Every valid probe (those below hi) is at or below target: the answer lies past the
+      // last of them, lo + floor((hi - 1 - lo) / step) * step, which is lane 63's probe only
+      // when all 64 probes are valid.
+      lo = lo + min(kWaveSize - 1, (hi - 1 - lo) / step) * step + 1;
     } else {
       const int f = __ffsll((unsigned long long)hit) - 1;
       const int new_hi = lo + f * step;
@@ -2329,6 +2344,14 @@ __global__ __launch_bounds__(NW * kWaveSize) void seq_sum_block_kernel(const dou
   __shared__ SeqScratch<NW> sc;
   const SeqSum r = block_seq_sum_wide<NW>(t, n, out, true, stop_at, false, sc);
   if (threadIdx.x == 0) *count = r.count;
+}
+
+// Diagnostic kernel: the draw search of head_finish_kernel (wave_first_above), one wave per
+// target, over the non-decreasing c[0..n).
+__global__ __launch_bounds__(kWaveSize) void first_above_kernel(const double *c, int32_t n, const double *targets,
+                                                                int32_t *out) {
+  const int r = wave_first_above(c, n, targets[blockIdx.x]);
+  if (wave_lane() == 0) out[blockIdx.x] = r;
 }
 
 __global__ void exp_kernel(const double *x, double *y, int64_t n) {
@@ -2731,6 +2754,16 @@ int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double stop_at, doub
   else
     hipLaunchKernelGGL(seq_sum_kernel, dim3(1), dim3(kWaveSize), 0, (hipStream_t)stream, terms_dev, n,
                        stop_at, prefix_dev, count_dev, wide);
+  HIP_TRY(hipGetLastError());
+  return TABBY_OK;
+}
+
+int tabby_debug_first_above(const double *c_dev, int32_t n, const double *targets_dev, int32_t m,
+                            int32_t *out_dev, void *stream) {
+  if (!c_dev || !targets_dev || !out_dev) return fail(TABBY_EINVAL, "null pointer");
+  if (n < 1 || m < 1 || m > (1 << 24)) return fail(TABBY_EINVAL, "n must be >= 1 and m in [1, 2^24]");
+  hipLaunchKernelGGL(first_above_kernel, dim3((unsigned)m), dim3(kWaveSize), 0, (hipStream_t)stream, c_dev, n,
+                     targets_dev, out_dev);
   HIP_TRY(hipGetLastError());
   return TABBY_OK;
 }

@@ -45,7 +45,7 @@ assert PARAMS_DTYPE.itemsize == 32 and RESULT_DTYPE.itemsize == 48
 EXPORTED_SYMBOLS = (
     "tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
     "tabby_sampler_sample", "tabby_last_error", "tabby_version", "tabby_debug_exp",
-    "tabby_debug_seq_sum",
+    "tabby_debug_seq_sum", "tabby_debug_first_above",
 )
 
 
@@ -77,8 +77,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     L.tabby_version.restype = ctypes.c_char_p
     L.tabby_debug_exp.argtypes = [vp, vp, i64, vp]
     L.tabby_debug_seq_sum.argtypes = [vp, i32, ctypes.c_double, vp, vp, i32, vp]
+    L.tabby_debug_first_above.argtypes = [vp, i32, vp, i32, vp, vp]
     for name in ("tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
-                 "tabby_sampler_sample", "tabby_debug_exp", "tabby_debug_seq_sum"):
+                 "tabby_sampler_sample", "tabby_debug_exp", "tabby_debug_seq_sum",
+                 "tabby_debug_first_above"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -331,14 +333,15 @@ def device_exp(x) -> "object":
     return y
 
 
-def device_seq_sum(terms, stop_at: float = float("inf"), wide: int = 0):
+def device_seq_sum(terms, stop_at: float = float("inf"), wide: int = 0, in_place: bool = False):
     """The device's sequential f64 partial sums of a CUDA float64 tensor (diagnostic):
     returns (prefix sums actually written, as a CUDA tensor, count). ``wide``: 0 the
     one-term-per-lane form, 1 the 16-terms-per-lane form used for long sums, 2 that form
-    taken by a four-wave workgroup, 3 by an eight-wave workgroup."""
+    taken by a four-wave workgroup, 3 by an eight-wave workgroup. ``in_place``: the sums
+    are written over (a copy of) the terms."""
     import torch
-    t = terms.contiguous()
-    out = torch.zeros_like(t)
+    t = terms.contiguous().clone() if in_place else terms.contiguous()
+    out = t if in_place else torch.zeros_like(t)
     cnt = torch.zeros(1, dtype=torch.int32, device=t.device)
     stream = torch.cuda.current_stream()
     _check(load_library().tabby_debug_seq_sum(ctypes.c_void_p(t.data_ptr()), int(t.numel()),
@@ -347,3 +350,17 @@ def device_seq_sum(terms, stop_at: float = float("inf"), wide: int = 0):
                                               ctypes.c_void_p(stream.cuda_stream)))
     n = int(cnt.item())
     return out[:n], n
+
+
+def device_first_above(c, targets):
+    """The device's draw search over a non-decreasing CUDA float64 tensor ``c`` (diagnostic):
+    for each target, the first i with target < c[i], or len(c) - 1 when there is none."""
+    import torch
+    c = c.contiguous()
+    t = targets.contiguous()
+    out = torch.empty(t.numel(), dtype=torch.int32, device=c.device)
+    _check(load_library().tabby_debug_first_above(ctypes.c_void_p(c.data_ptr()), int(c.numel()),
+                                                  ctypes.c_void_p(t.data_ptr()), int(t.numel()),
+                                                  ctypes.c_void_p(out.data_ptr()),
+                                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    return out

@@ -388,15 +388,80 @@ def test_row_kernel_parts_ragged(oracle, dtype, vocab):
     _log(f"row kernel parts ragged {dtype} {vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 50), 50))
 
 
-@pytest.mark.xfail(strict=False, reason="known: a whole-vocabulary row with a 90 K-entry head of "
-                   "quantised logits at T = 2 draws one position late inside a run of 3,573 ties "
-                   "(the running sums are exact; the head's order of equal keys is the suspect)")
 def test_full_vocab_huge_tied_head_draw(oracle):
     # Found by a randomized sweep: row 6 (k = 0, T = 2.0, top-p 0.9, u = 0.753) of this
-    # workload; consideredCount agrees (36,932), the id does not (16,128 vs 16,106, adjacent
-    # positions 13,294 / 13,293 of a tie run at 3.0).
+    # workload has a 90 K-entry head of quantised logits, and its draw lands inside a run of
+    # 3,573 tied values (positions 13,293 / 13,294). The 64-ary draw search skipped the
+    # entries between its last valid probe and its upper bound and drew one position late.
     w = synth.random_workload(rows=200, vocab=100000, seed=770792225, ties=True, neg_inf_frac=0.1,
                               k_choices=(2, 0, 0), temperatures=(0.0, 0.3, 0.7, 1.0, 2.0),
                               top_ps=(0.5, 0.9, 0.95, 1.0))
     res, ids, vals = run_gpu(w, k_max=256, topk_cap=40)
-    compare(w, res, ids, vals, run_oracle(oracle, w, 40), 40)
+    _log("huge tied head", compare(w, res, ids, vals, run_oracle(oracle, w, 40), 40))
+
+
+U_GRID = (0.0, 0.001, 0.1, 0.25, 0.5, 0.6180339887, 0.75, 0.9, 0.999, 0.9999999998)
+
+
+@pytest.mark.parametrize("vocab,ties", [(12000, False), (12000, True), (60000, False), (60000, True)])
+def test_full_vocab_long_cuts_draw_grid(oracle, vocab, ties):
+    # Whole-vocabulary rows whose cut is long (hot temperatures, top-p near 1): heads below
+    # 16,384 entries (sums and draw from LDS) and above (from global memory), with and without
+    # long tie runs, every row drawn at each point of a grid of uniforms.
+    temps, tops = (1.0, 2.0, 50.0), (0.9, 0.99)
+    combos = [(t, p, u) for t in temps for p in tops for u in U_GRID]
+    w = synth.random_workload(rows=len(combos), vocab=vocab, seed=vocab + int(ties), ties=ties,
+                              neg_inf_frac=0.05 if ties else 0.0, k_choices=(0,))
+    for r, (t, p, u) in enumerate(combos):
+        w.temperature[r], w.top_p[r], w.uniform[r] = t, p, u
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=16)
+    _log(f"full vocab long cuts V={vocab} ties={ties}",
+         compare(w, res, ids, vals, run_oracle(oracle, w, 16), 16))
+
+
+@pytest.mark.parametrize("offset", [-500.0, 100.0, 300.0, 1000.0])
+def test_sum_exp_shift_invariant(oracle, offset):
+    # Logits far from 0: sum-exp, poolMass and the probabilities are relative to the row max
+    # (sampler.ts:156-157; tests/sampling.test.ts:73-77), so their accuracy must not depend on
+    # where the row sits. Pools of 1, 50, 256 and the whole vocabulary; three kernel paths
+    # (the per-row kernel at 256 rows, parts at 8 rows, the two-kernel path at 130 rows).
+    for rows in (256, 8, 130):
+        w = synth.config(3, rows=rows, vocab=30000 if rows == 256 else 151936)
+        w.logits = (w.logits.astype(np.float64) + offset).astype(np.float32)
+        w.top_k[:] = np.resize(np.array([1, 50, 256, 0], np.int32), rows)
+        res, ids, vals = run_gpu(w, k_max=256, topk_cap=50)
+        _log(f"shift {offset:+} rows {rows}", compare(w, res, ids, vals, run_oracle(oracle, w, 50), 50))
+
+
+def test_config5_full_512_rows(oracle):
+    # BASELINE config 5 at its stated size: one slice per row of the 256-lane slice kernel.
+    w = synth.config(5)
+    assert w.rows == 512
+    res, ids, vals = run_gpu(w, k_max=1024, topk_cap=1024)
+    _log("config5[512 rows]", compare(w, res, ids, vals, run_oracle(oracle, w, 1024), 1024))
+
+
+@pytest.mark.parametrize("rows", [192, 197])
+def test_wave_kernel_batches_between_half_and_all_cus(oracle, rows):
+    # 129-255 rows with pools up to 256 take the one-wave slice kernel and its merge kernel;
+    # 192 rows (a multiple of 8) place each row's slices on the XCD of its merge, 197 do not.
+    w = synth.config(3, rows=rows)
+    w.top_k[:] = np.resize(np.array([1, 20, 50, 100, 256], np.int32), rows)
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=100)
+    _log(f"wave kernel {rows} rows", compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100))
+
+
+def test_headline_workload_device_form(oracle):
+    # The bench's headline exactly: 256 x 151,936 f32, k 50 and top-p 0.9 on every row, k_max
+    # 64, device-resident parameters and results, no top-k output.
+    import torch
+    w = synth.config(3)
+    w.top_k[:] = 50
+    w.top_p[:] = 0.9
+    x = torch.from_numpy(w.logits).cuda()
+    pd = torch.from_numpy(params_of(w).view(np.uint8).copy()).cuda()
+    rd = torch.zeros(w.rows * S.RESULT_DTYPE.itemsize, dtype=torch.uint8, device="cuda")
+    with S.GpuSampler(vocab_max=w.vocab, rows_max=w.rows, k_max=64) as g:
+        g.sample_device(x, pd, rd)
+        res = rd.cpu().numpy().view(S.RESULT_DTYPE)
+    _log("headline device form", compare(w, res, None, None, run_oracle(oracle, w, 0), 0))

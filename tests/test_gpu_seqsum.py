@@ -76,3 +76,89 @@ def test_stop_at_threshold(stop, wide):
     s = np.exp(l - l[0])
     w = s / s.sum()
     _check(w, stop, wide)
+
+
+def _check_in_place(terms, stop_at=np.inf, wide=0):
+    """The same sums written over their own terms (whole-vocabulary heads run the running
+    sums that way): every partial sum up to the stop bit for bit."""
+    import torch
+    terms = np.ascontiguousarray(terms, dtype=np.float64)
+    prefix, n = S.device_seq_sum(torch.from_numpy(terms).cuda(), stop_at, wide, in_place=True)
+    expected = np.cumsum(terms)
+    hits = np.nonzero(expected >= stop_at)[0]
+    want_n = int(hits[0]) + 1 if hits.size else terms.size
+    assert n == want_n, (n, want_n)
+    got = prefix.cpu().numpy()
+    bad = np.nonzero(got.view(np.uint64) != expected[:n].view(np.uint64))[0]
+    assert bad.size == 0, f"{bad.size} differ, first at {bad[0]}: {got[bad[0]]!r} vs {expected[bad[0]]!r}"
+
+
+@pytest.mark.parametrize("n", [300, 16385, 40000])
+@pytest.mark.parametrize("stop", [np.inf, 0.9, 0.999])
+def test_in_place_with_binade_events(n, stop, wide):
+    # Normalised weights of a flat, tied head (many binade crossings below 1: every event
+    # restarts a step after thread 0 has rewritten the event's term) and integer-valued terms
+    # (a crossing at each power of two).
+    rng = np.random.default_rng(n)
+    levels = np.sort(np.round(rng.normal(0, 1, n) * 4) / 4)[::-1]
+    s = np.exp((levels - levels[0]) / 2.0)
+    _check_in_place(s / s.sum(), stop, wide)
+    if not np.isfinite(stop):
+        _check_in_place(np.ones(n), stop, wide)
+
+
+def _stop_terms(n, seed):
+    rng = np.random.default_rng(seed)
+    l = np.sort(rng.normal(0, 1.5, n))[::-1]
+    s = np.exp(l - l[0])
+    return s / s.sum()
+
+
+@pytest.mark.parametrize("n", [9, 40, 65, 256])
+def test_short_sums_with_stop_past_the_serial_prefix(n, wide):
+    # Sums of at most 256 terms with a top-p stop take their first 8 terms one by one and
+    # the rest by the scan from term 8: stops exactly at the 8th and 9th partial sums, just
+    # above them, and late.
+    w = _stop_terms(n, n)
+    c = np.cumsum(w)
+    stops = [c[7], c[8], np.nextafter(c[7], 2.0), np.nextafter(c[8], 2.0), c[n - 2], c[n - 1]]
+    if n > 20:
+        stops.append(c[n // 2])
+    for st in stops:
+        _check(w, st, wide)
+
+
+@pytest.mark.parametrize("n", [9, 40, 65, 256])
+def test_short_sums_binade_and_tie_after_the_serial_prefix(n, wide):
+    # The 8th partial sum is 1 + 2^-52 (odd); term 9 is half its ulp, an exact tie that
+    # rounds to the even sum; then terms that cross into [2, 4).
+    head = [1.0, 2.0 ** -52] + [0.0] * 6
+    t = np.array(head + [2.0 ** -53] + [0.75] * (n - 9), dtype=np.float64)[:n]
+    c = np.cumsum(t)
+    for st in (np.inf, c[8], c[min(n - 1, 9)], c[-1]):
+        _check(t, st, wide)
+    # A crossing of 1.0 at term 9 itself, then small terms.
+    t2 = np.array([0.5] + [1.0 / 16] * 7 + [0.25] + [2.0 ** -20] * (n - 9), dtype=np.float64)[:n]
+    c2 = np.cumsum(t2)
+    for st in (np.inf, c2[8], np.nextafter(c2[8], 0.0), c2[-1]):
+        _check(t2, st, wide)
+
+
+@pytest.mark.parametrize("n", [1, 2, 63, 64, 65, 100, 4095, 4096, 4097, 5000, 60000, 151936])
+def test_draw_search_first_above(n):
+    # The whole-vocabulary draw: the first i with target < c[i] over non-decreasing running
+    # sums (long tie runs included), or n - 1 when none, against a brute-force search.
+    import torch
+    rng = np.random.default_rng(n + 7)
+    for trial in range(4):
+        inc = rng.random(n)
+        inc[rng.random(n) < (0.2 if trial % 2 else 0.9)] = 0.0  # runs of equal sums
+        c = np.cumsum(inc)
+        c = c / max(c[-1], 1.0)
+        probes = np.concatenate([rng.random(300) * (c[-1] + 0.01), c[rng.integers(0, n, 200)],
+                                 np.nextafter(c[rng.integers(0, n, 100)], -1.0), [0.0, -1.0, c[-1], c[-1] + 1]])
+        want = np.minimum(np.searchsorted(c, probes, side="right"), n - 1)
+        got = S.device_first_above(torch.from_numpy(c).cuda(), torch.from_numpy(probes).cuda()).cpu().numpy()
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, (f"n={n} trial {trial}: {bad.size} wrong, first target {probes[bad[0]]!r}: "
+                               f"got {got[bad[0]]}, want {want[bad[0]]}")
