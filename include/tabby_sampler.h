@@ -109,6 +109,25 @@ TABBY_API int tabby_sampler_sample(tabby_sampler *sampler, const void *logits_de
                          tabby_row_result *results_host, int32_t *topk_ids_host,
                          float *topk_logits_host, int32_t topk_cap, void *stream);
 
+/*
+ * Allocation-free form of tabby_sampler_sample_device. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It takes no handle and
+ * calls no hipMalloc, hipFree or allocating routine; its scratch is a fixed 16 MiB array in
+ * the library's device image, one per GPU, kept until the process ends (the first call on a
+ * device looks up its address). The caller passes inputs and outputs as for
+ * tabby_sampler_sample_device, with flags = 0, on the current device. Limits: k_max <= 256,
+ * and rows whose pool is the whole vocabulary (top_k = 0 or >= vocab, vocab > 256) get
+ * status TABBY_EINVAL; a batch whose scratch would exceed 16 MiB returns TABBY_ECAPACITY
+ * (batches of the sizes of the reference's configurations need at most ~10 MiB). Calls that
+ * overlap on one GPU share that scratch and race: serialise them (one stream).
+ */
+TABBY_API int tabby_sampler_sample_device_noalloc(const void *logits_dev, int32_t dtype, int32_t rows,
+                                                  int32_t vocab, int32_t k_max,
+                                                  const tabby_row_params *params_dev,
+                                                  tabby_row_result *results_dev, int32_t *topk_ids_dev,
+                                                  float *topk_logits_dev, int32_t topk_cap, void *stream);
+
 /* Message of the calling thread's last failure ("" if none). */
 TABBY_API const char *tabby_last_error(void);
 

@@ -112,6 +112,9 @@ struct Launch {
   int32_t parts;      // row_kernel: 1 = one workgroup per row; > 1 = workgroups per row (each
                       // a part of slice_len elements, finished by wave_merge_kernel); 0 = unused
   int32_t row_waves;  // row_kernel: waves per workgroup
+  int32_t list_stride;  // pools <= 256: entries between the sorted lists of consecutive slices
+                        // (or parts) of a row in cands -- slice_len, or kWaveKcap when the
+                        // lists are packed (a list never holds more than the pool)
 };
 
 // The (row, slice) of workgroup b of a grid of rows x splits. Workgroup b runs on XCD b % 8
@@ -1120,7 +1123,7 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
   row_slice_of((int)blockIdx.x, L.rows, L.splits, row, slice);
   const tabby_row_params P = L.params[row];
   wave_slice<In, VEC, false>(sm, L, P, row, slice, 0,
-                             W.cands + (size_t)row * W.row_cand_stride + (size_t)slice * L.slice_len,
+                             W.cands + (size_t)row * W.row_cand_stride + (size_t)slice * L.list_stride,
                              W.stats + (size_t)row * kMaxSplits + slice, nullptr, nullptr, 0);
 }
 
@@ -1798,7 +1801,7 @@ template <typename In>
 __global__ __launch_bounds__(kBlock) void wave_merge_kernel(Launch L, Workspace W) {
   __shared__ WaveMergeSmem sm;
   const int row = (int)blockIdx.x;
-  const RowLists lists{W.cands + (size_t)row * W.row_cand_stride, L.splits, L.slice_len, W.row_cand_stride};
+  const RowLists lists{W.cands + (size_t)row * W.row_cand_stride, L.splits, L.list_stride, W.row_cand_stride};
   const tabby_row_params P = L.params[row];
   merge_row<In>(sm, L, W, row, P, W.stats + (size_t)row * kMaxSplits, lists);
 }
@@ -1864,7 +1867,7 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
       int total = 0;
       for (int s = 0; s < nw; ++s) total += (int)sm.stats[s].count;
       const int count = min(rp.K, total);
-      uint64_t *out = W.cands + (size_t)row * W.row_cand_stride + (size_t)part * L.slice_len;
+      uint64_t *out = W.cands + (size_t)row * W.row_cand_stride + (size_t)part * L.list_stride;
       for (int i = wave_lane(); i < count; i += kWaveSize) out[i] = sm.merge.sorted[i];
       if (wave_lane() == 0) {
         SliceStat st;
@@ -2361,6 +2364,10 @@ __global__ void exp_kernel(const double *x, double *y, int64_t n) {
 
 }  // namespace tabby
 
+// Scratch of the allocation-free entry (tabby_sampler_sample_device_noalloc), per GPU.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 // =========================================================================================
 // Host side.
 // =========================================================================================
@@ -2503,6 +2510,79 @@ hipError_t dispatch(int dtype, const Plan &p, const Launch &L, const Workspace &
   return e;
 }
 
+// The launch shape of one call: which kernels run and how each row is cut (everything in L
+// except the parameter, result and top-k pointers). Sorted lists of consecutive slices sit
+// slice_len entries apart (the handle's candidate region has room for a whole row).
+Plan plan_launch(int rows, int vocab, int dtype, const void *logits, int k_max, int topk_cap, int cus,
+                 bool head_pass, Launch &L) {
+  const int kcap = k_max <= kKcapSmall ? kKcapSmall : kKcapLarge;
+  const Plan p = make_plan(rows, vocab, dtype, logits, kcap <= kWaveKcap);
+  L = Launch{};
+  L.logits = logits;
+  L.rows = rows;
+  L.vocab = vocab;
+  L.splits = p.splits;
+  L.slice_len = p.slice_len;
+  L.topk_cap = topk_cap;
+  L.k_max = k_max;
+  L.kcap = kcap;
+  L.head_pass = head_pass ? 1 : 0;
+  const Plan hp = make_plan(rows, vocab, dtype, logits, true);
+  L.h_splits = hp.splits;
+  L.h_slice_len = hp.slice_len;
+  L.parts = 0;
+  L.row_waves = 0;
+  if (per_row_launch(L, cus)) {
+    L.parts = 1;
+    L.row_waves = std::max(L.splits, kRowMinWaves);  // at least the five the merge uses
+  } else if (kcap <= kWaveKcap) {
+    int part_len = 0;
+    const int parts = row_parts(rows, vocab, cus, part_len);
+    if (parts >= 2 && parts <= 3) {
+      // Two or three parts' worth of row: one workgroup streams it all and finishes it, with
+      // no second launch (config 1, one row of 49,152: 14.2 us, against 14.9 us in three
+      // parts).
+      L.parts = 1;
+      L.row_waves = kRowWaves;
+    } else if (parts >= 2) {
+      L.parts = parts;
+      L.splits = parts;  // wave_merge_kernel merges one list per part
+      L.slice_len = part_len;
+      L.row_waves = kRowWaves;
+    }
+  }
+  L.list_stride = L.slice_len;
+  return p;
+}
+
+// The allocation-free entry's scratch: its row statuses, slice statistics and packed
+// sorted lists live in `scratch`, one copy per GPU, held until the process ends. In host
+// code the array's name stands for a host-side placeholder, not a device address: each
+// device's address is taken once with hipGetSymbolAddress (with that device current) and
+// only that pointer reaches kernels.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices];
+int g_scratch_cus[kMaxDevices];
+
+int scratch_of_current_device(int &device, void *&base, int &cus) {
+  HIP_TRY(hipGetDevice(&device));
+  if (device < 0 || device >= kMaxDevices)
+    return fail(TABBY_EINVAL, "device ordinal " + std::to_string(device) + " is beyond " + std::to_string(kMaxDevices));
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    int n = 0;
+    HIP_TRY(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device));
+    g_scratch_cus[device] = n;
+    g_scratch_ptr[device] = p;
+  }
+  base = g_scratch_ptr[device];
+  cus = g_scratch_cus[device];
+  return TABBY_OK;
+}
+
 int check_common(tabby_sampler *h, const void *logits, int32_t dtype, int32_t rows, int32_t vocab,
                  int32_t topk_cap) {
   if (!h) return fail(TABBY_EINVAL, "sampler handle is null");
@@ -2637,46 +2717,13 @@ int tabby_sampler_sample_device(tabby_sampler *h, const void *logits_dev, int32_
     }
   }
 
-  const int kcap = h->k_max <= kKcapSmall ? kKcapSmall : kKcapLarge;
-  const Plan p = make_plan(rows, vocab, dtype, logits_dev, kcap <= kWaveKcap);
   Launch L;
-  L.logits = logits_dev;
+  const Plan p = plan_launch(rows, vocab, dtype, logits_dev, h->k_max, topk_cap, h->cus,
+                             (flags & TABBY_FLAG_FULL_VOCAB) != 0, L);
   L.params = params_dev;
   L.results = results_dev;
   L.topk_ids = topk_ids_dev;
   L.topk_logits = topk_logits_dev;
-  L.rows = rows;
-  L.vocab = vocab;
-  L.splits = p.splits;
-  L.slice_len = p.slice_len;
-  L.topk_cap = topk_cap;
-  L.k_max = h->k_max;
-  L.kcap = kcap;
-  L.head_pass = (flags & TABBY_FLAG_FULL_VOCAB) ? 1 : 0;
-  const Plan hp = make_plan(rows, vocab, dtype, logits_dev, true);
-  L.h_splits = hp.splits;
-  L.h_slice_len = hp.slice_len;
-  L.parts = 0;
-  L.row_waves = 0;
-  if (per_row_launch(L, h->cus)) {
-    L.parts = 1;
-    L.row_waves = std::max(L.splits, kRowMinWaves);  // at least the five the merge uses
-  } else if (kcap <= kWaveKcap) {
-    int part_len = 0;
-    const int parts = row_parts(rows, vocab, h->cus, part_len);
-    if (parts >= 2 && parts <= 3) {
-      // Two or three parts' worth of row: one workgroup streams it all and finishes it, with
-      // no second launch (config 1, one row of 49,152: 14.2 us, against 14.9 us in three
-      // parts).
-      L.parts = 1;
-      L.row_waves = kRowWaves;
-    } else if (parts >= 2) {
-      L.parts = parts;
-      L.splits = parts;  // wave_merge_kernel merges one list per part
-      L.slice_len = part_len;
-      L.row_waves = kRowWaves;
-    }
-  }
   HIP_TRY(hipSetDevice(h->device));
   HIP_TRY(dispatch(dtype, p, L, h->ws, h->cus, (hipStream_t)stream));
   return TABBY_OK;
@@ -2738,6 +2785,58 @@ int tabby_sampler_sample(tabby_sampler *h, const void *logits_dev, int32_t dtype
     if (st == TABBY_EEMPTY) return fail(st, "sampleFromTopK: empty candidate set");
     return fail(st, "row " + std::to_string(r) + " failed with status " + std::to_string(st));
   }
+  return TABBY_OK;
+}
+
+int tabby_sampler_sample_device_noalloc(const void *logits_dev, int32_t dtype, int32_t rows, int32_t vocab,
+                                        int32_t k_max, const tabby_row_params *params_dev,
+                                        tabby_row_result *results_dev, int32_t *topk_ids_dev,
+                                        float *topk_logits_dev, int32_t topk_cap, void *stream) {
+  if (!logits_dev) return fail(TABBY_EINVAL, "logits pointer is null");
+  if (dtype != TABBY_F32 && dtype != TABBY_F16) return fail(TABBY_EINVAL, "dtype must be TABBY_F32 or TABBY_F16");
+  if (rows < 1 || rows > (1 << 20)) return fail(TABBY_EINVAL, "rows must be between 1 and 1048576, got " + std::to_string(rows));
+  if (vocab < 1 || vocab > kMaxSplits * kChunk)
+    return fail(TABBY_EINVAL, "vocab must be between 1 and " + std::to_string(kMaxSplits * kChunk) + ", got " + std::to_string(vocab));
+  if (k_max < 1 || k_max > kWaveKcap)
+    return fail(TABBY_ECAPACITY, "k_max must be between 1 and " + std::to_string(kWaveKcap) +
+                                     " for the allocation-free entry, got " + std::to_string(k_max));
+  if (topk_cap < 0) return fail(TABBY_EINVAL, "topk_cap must be >= 0");
+  if (!params_dev || !results_dev) return fail(TABBY_EINVAL, "params and results pointers must be non-null");
+  if (topk_cap > 0 && (!topk_ids_dev || !topk_logits_dev))
+    return fail(TABBY_EINVAL, "topk_cap > 0 needs both top-k output pointers");
+  int device = 0, cus = 0;
+  void *base = nullptr;
+  const int rc = scratch_of_current_device(device, base, cus);
+  if (rc) return rc;
+
+  Launch L;
+  const Plan p = plan_launch(rows, vocab, dtype, logits_dev, k_max, topk_cap, cus, false, L);
+  L.params = params_dev;
+  L.results = results_dev;
+  L.topk_ids = topk_ids_dev;
+  L.topk_logits = topk_logits_dev;
+  // Row statuses always; when rows are cut into slices or parts, their statistics and their
+  // sorted lists, packed kWaveKcap entries apart (a list never holds more than the pool).
+  // Everything is written before it is read within the call, so nothing needs clearing.
+  Workspace W{};
+  size_t off = 0;
+  auto carve = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) & ~(size_t)255;
+    return (char *)base + at;
+  };
+  W.row_state = (RowState *)carve((size_t)rows * sizeof(RowState));
+  L.list_stride = kWaveKcap;
+  if (L.parts != 1) {
+    W.stats = (SliceStat *)carve((size_t)rows * kMaxSplits * sizeof(SliceStat));
+    W.row_cand_stride = (int64_t)L.splits * kWaveKcap;
+    W.cands = (uint64_t *)carve((size_t)rows * (size_t)W.row_cand_stride * sizeof(uint64_t));
+  }
+  if (off > kNoAllocScratchBytes)
+    return fail(TABBY_ECAPACITY, std::to_string(rows) + " rows of " + std::to_string(vocab) + " need " +
+                                     std::to_string(off) + " bytes of scratch; the allocation-free entry has " +
+                                     std::to_string(kNoAllocScratchBytes));
+  HIP_TRY(dispatch(dtype, p, L, W, cus, (hipStream_t)stream));
   return TABBY_OK;
 }
 

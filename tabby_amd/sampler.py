@@ -45,7 +45,7 @@ assert PARAMS_DTYPE.itemsize == 32 and RESULT_DTYPE.itemsize == 48
 EXPORTED_SYMBOLS = (
     "tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
     "tabby_sampler_sample", "tabby_last_error", "tabby_version", "tabby_debug_exp",
-    "tabby_debug_seq_sum", "tabby_debug_first_above",
+    "tabby_debug_seq_sum", "tabby_debug_first_above", "tabby_sampler_sample_device_noalloc",
 )
 
 
@@ -78,9 +78,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     L.tabby_debug_exp.argtypes = [vp, vp, i64, vp]
     L.tabby_debug_seq_sum.argtypes = [vp, i32, ctypes.c_double, vp, vp, i32, vp]
     L.tabby_debug_first_above.argtypes = [vp, i32, vp, i32, vp, vp]
+    L.tabby_sampler_sample_device_noalloc.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]
     for name in ("tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
                  "tabby_sampler_sample", "tabby_debug_exp", "tabby_debug_seq_sum",
-                 "tabby_debug_first_above"):
+                 "tabby_debug_first_above", "tabby_sampler_sample_device_noalloc"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -307,6 +308,21 @@ class GpuSampler:
         n = int(res[0]["topk_count"])
         return TopKResult(maxLogit=float(res[0]["max_logit"]), sumExp=float(res[0]["sum_exp"]),
                           ids=[int(v) for v in ids[0, :n]], logits=[float(v) for v in vals[0, :n]])
+
+
+def sample_device_noalloc(logits, params_dev, results_dev, k_max: int, topk_ids=None, topk_logits=None,
+                          stream=None) -> None:
+    """The allocation-free device-resident entry (tabby_sampler_sample_device_noalloc): no
+    handle, scratch in the library's fixed per-GPU array; k_max <= 256, no whole-vocabulary
+    pools. Asynchronous; same buffers as GpuSampler.sample_device."""
+    x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+    rows, vocab = int(x.shape[0]), int(x.shape[1])
+    cap = int(topk_ids.shape[-1]) if topk_ids is not None else 0
+    _check(load_library().tabby_sampler_sample_device_noalloc(
+        ctypes.c_void_p(x.data_ptr()), _dtype_code(x), rows, vocab, int(k_max),
+        ctypes.c_void_p(params_dev.data_ptr()), ctypes.c_void_p(results_dev.data_ptr()),
+        ctypes.c_void_p(topk_ids.data_ptr()) if cap else None,
+        ctypes.c_void_p(topk_logits.data_ptr()) if cap else None, cap, GpuSampler._stream(stream)))
 
 
 _default: Optional[GpuSampler] = None
