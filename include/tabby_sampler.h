@@ -147,7 +147,8 @@ TABBY_API int tabby_debug_exp(const double *x_dev, double *y_dev, int64_t n, voi
  * j-th partial sum up to the first that is >= stop_at (INFINITY: none), and *count_dev the
  * number of partial sums written. wide = 1 selects the form used for long sums (16 terms per
  * lane per step), wide = 2 the same taken by a four-wave workgroup, wide = 3 by an eight-wave
- * workgroup (the form that finishes whole-vocabulary heads). prefix_dev may be terms_dev
+ * workgroup (the form that finishes whole-vocabulary heads), wide = 4 the register form for
+ * n <= 64 (term i in lane i: the form that finishes pools of at most 64). prefix_dev may be terms_dev
  * itself (the sums are then written over their terms, as whole-vocabulary heads run them).
  * For parity tests.
  */

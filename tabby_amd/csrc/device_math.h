@@ -105,6 +105,32 @@ __device__ __forceinline__ double fdlibm_exp_inline(double x) {
          9.33263618503218878990e-302;
 }
 
+// exp(x) for x <= 0 to within a few ulp, without branches: x = k*ln2 + r with the Cody-Waite
+// split of ln2 above (k*ln2_hi exact), e^r by its Taylor series to degree 12 evaluated in
+// Estrin's form (|r| <= ln2/2, truncation below 2^-52 relative), then an exact scaling by 2^k
+// (ldexp, gradual underflow). Not V8's bits: for sums and probabilities whose bits the
+// callers do not need, or that they check against a margin.
+__device__ __forceinline__ double exp_nonpos(double x) {
+  x = fmax(x, -746.0);  // exp(-746) rounds to 0; -inf too
+  const double k = __builtin_rint(x * 1.44269504088896338700e+00);
+  double r = __builtin_fma(-k, 6.93147180369123816490e-01, x);
+  r = __builtin_fma(-k, 1.90821492927058770002e-10, r);
+  const double r2 = r * r, r4 = r2 * r2, r8 = r4 * r4;
+  const double p01 = 1.0 + r;
+  const double p23 = __builtin_fma(r, 1.66666666666666666667e-01, 5.0e-01);
+  const double p45 = __builtin_fma(r, 8.33333333333333333333e-03, 4.16666666666666666667e-02);
+  const double p67 = __builtin_fma(r, 1.98412698412698412698e-04, 1.38888888888888888889e-03);
+  const double p89 = __builtin_fma(r, 2.75573192239858906526e-06, 2.48015873015873015873e-05);
+  const double pab = __builtin_fma(r, 2.50521083854417187751e-08, 2.75573192239858906526e-07);
+  const double q0 = __builtin_fma(r2, p23, p01);
+  const double q1 = __builtin_fma(r2, p67, p45);
+  const double q2 = __builtin_fma(r2, pab, p89);
+  const double q3 = 2.08767569878680989792e-09;  // 1/12!
+  const double s0 = __builtin_fma(r4, q1, q0);
+  const double s1 = __builtin_fma(r4, q3, q2);
+  return __builtin_ldexp(__builtin_fma(r8, s1, s0), (int)k);
+}
+
 // Out-of-line form for call sites where code size matters more than the call.
 __device__ __noinline__ double fdlibm_exp(double x) { return fdlibm_exp_inline(x); }
 

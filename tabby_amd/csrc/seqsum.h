@@ -235,6 +235,63 @@ __device__ __forceinline__ SeqSum wave_seq_sum(const double *t, int n, double *o
   return {P, n};
 }
 
+// The same sum for at most 64 terms held in registers, lane i holding t_i (lanes >= n hold
+// 0), with no memory traffic: a step masks the lanes before its first term instead of moving
+// the terms between lanes. Same contract as wave_seq_sum (n >= 1, t >= 0, t_0 > 0); *partial
+// receives in lane i < count the i-th partial sum (other lanes: 0).
+__device__ __forceinline__ SeqSum reg_seq_sum(double t, int n, double stop_at, double *partial) {
+  const int lane = wave_lane();
+  double P = lane_f64(t, 0);
+  double mine = lane == 0 ? P : 0.0;
+  if (P >= stop_at) {
+    *partial = mine;
+    return {P, 1};
+  }
+  int a = 1;
+  while (a < n) {
+    const int E = ((int)((uint64_t)__double_as_longlong(P) >> 52) & 0x7ff) - 1023;
+    const double u = __longlong_as_double((long long)((uint64_t)(E - 52 + 1023) << 52));
+    const double scale = __longlong_as_double((long long)((uint64_t)(52 - E + 1023) << 52));
+    const double m = P * scale;
+    const bool live = lane >= a && lane < n;
+    const double q = live ? t * scale : 0.0;
+    const double fl = __builtin_floor(q);
+    const bool tie = live && q < kTwo52 && q - fl == 0.5;
+    double r = __builtin_rint(q);
+    if (__ballot(tie)) {  // lanes outside the step add 0 and pass the parity through
+      const uint32_t parity_before = parity_apply(parity_exclusive_scan(tie ? 0u : 1u | (low_bit(r) << 1)), low_bit(m));
+      if (tie) r = fl + (double)(parity_before ^ low_bit(fl));
+    }
+    const double cum = m + wave_inclusive_scan(r);
+    const bool crosses = cum >= kTwo53;
+    const bool stops = cum * u >= stop_at;
+    const uint64_t flagged = __ballot(live && (crosses || stops));
+    const int Lf = flagged ? __ffsll((unsigned long long)flagged) - 1 : kWaveSize;
+    if (live && lane < Lf) mine = cum * u;  // exact partial sums before the first event
+    if (Lf == kWaveSize) {
+      P = lane_f64(cum, n - 1) * u;
+      break;
+    }
+    if (__builtin_amdgcn_readlane((int)(stops && !crosses), Lf) != 0) {  // a plain stop
+      const double at = lane_f64(cum, Lf) * u;
+      if (lane == Lf) mine = at;
+      *partial = mine;
+      return {at, Lf + 1};
+    }
+    // A binade change: one ordinary f64 add from the exact partial sum before it.
+    const double before = (Lf == a ? m : lane_f64(cum, Lf - 1)) * u;
+    P = before + lane_f64(t, Lf);
+    if (lane == Lf) mine = P;
+    if (P >= stop_at) {
+      *partial = mine;
+      return {P, Lf + 1};
+    }
+    a = Lf + 1;
+  }
+  *partial = mine;
+  return {P, n};
+}
+
 // The same sum for long sequences in global memory or padded LDS: each lane takes 16
 // consecutive terms (one 128-byte line) per step, so a step covers 1024 terms; an event
 // restarts the step after the event term. Same contract as wave_seq_sum; out is written

@@ -894,7 +894,7 @@ __device__ __forceinline__ int bound_regs(int kk, int waves) {
 
 // The kk-th largest (1 <= kk <= total <= 64 * R) of keys[0..total), on every lane.
 template <int R>
-__device__ __forceinline__ uint32_t union_kth(const uint32_t *keys, int total, int kk) {
+__device__ __forceinline__ uint32_t union_kth(const uint32_t *keys, int total, int kk, uint32_t &largest) {
   uint32_t v[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -902,12 +902,37 @@ __device__ __forceinline__ uint32_t union_kth(const uint32_t *keys, int total, i
     v[r] = i < total ? keys[i] : 0u;
   }
   wave_sort_desc<R>(v);
+  largest = (uint32_t)__builtin_amdgcn_readlane((int)v[0], 0);
   const int p = kk - 1;
   uint32_t t = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r)
     if (r == p / kWaveSize) t = (uint32_t)__builtin_amdgcn_readlane((int)v[r], p % kWaveSize);
   return t;
+}
+
+// The row's selection histogram for pools of at most 64 (finish_small_pool): 256 bins of keys
+// counted down from `top` (the largest key of the row's first bound's union; larger keys go
+// to bin 0) to the row's first bound, below which no list entry lies.
+constexpr int kSelBins = 256;
+
+struct SelBins {
+  uint32_t top;
+  int shift;
+  __device__ __forceinline__ uint32_t bin(uint32_t key) const {
+    return key >= top ? 0u : min((top - key) >> shift, (uint32_t)(kSelBins - 1));
+  }
+  // The smallest key of bin b (b < kSelBins - 1): keys at or above it lie in bins <= b.
+  __device__ __forceinline__ uint32_t lowest(int b) const {
+    const uint64_t edge = (uint64_t)(b + 1) << shift;
+    return edge > top ? 0u : top - (uint32_t)edge + 1u;
+  }
+};
+
+__device__ __forceinline__ SelBins sel_bins(uint32_t top, uint32_t bound) {
+  const uint32_t range = top - min(bound, top);
+  const int bits = range == 0 ? 0 : 32 - __clz((int)range);
+  return SelBins{top, bits > 8 ? bits - 8 : 0};
 }
 
 // One wave's share of row `row`: slice `slice` of L.slice_len elements or, when `claim` is
@@ -923,7 +948,8 @@ __device__ __forceinline__ uint32_t union_kth(const uint32_t *keys, int total, i
 template <typename In, int VEC, bool CLAIM>
 __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const tabby_row_params &P, int row,
                                            int slice, int part, uint64_t *out, SliceStat *stat, int *claim,
-                                           uint32_t *bound_keys, int waves) {
+                                           uint32_t *bound_keys, int waves, bool sort_end = true,
+                                           uint32_t *bound_out = nullptr, uint32_t *sel_hist = nullptr) {
   const int V = L.vocab;
   // CLAIM: the row, or part `part` of it (L.slice_len elements) when the row has several
   // workgroups.
@@ -943,6 +969,7 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
   int count = 0;          // entries in the list; wave-uniform (readfirstlane keeps it scalar)
   uint32_t theta_key = kNegInfKey;
   float theta = -INFINITY;  // == value_of(theta_key)
+  uint32_t union_top = kNegInfKey;  // CLAIM: the largest key of the first bound's union
 
   // Processes chunk c held in `cur` while chunk nc, if any, loads into `nxt`. (A load past
   // the last chunk would be waited for by the end-of-slice prune.) `first`: the wave's first
@@ -1062,13 +1089,18 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
       __syncthreads();
       uint32_t t;
       switch (regs) {
-        case 1: t = union_kth<1>(bound_keys, waves * m, kk); break;
-        case 2: t = union_kth<2>(bound_keys, waves * m, kk); break;
-        case 4: t = union_kth<4>(bound_keys, waves * m, kk); break;
-        default: t = union_kth<8>(bound_keys, waves * m, kk); break;
+        case 1: t = union_kth<1>(bound_keys, waves * m, kk, union_top); break;
+        case 2: t = union_kth<2>(bound_keys, waves * m, kk, union_top); break;
+        case 4: t = union_kth<4>(bound_keys, waves * m, kk, union_top); break;
+        default: t = union_kth<8>(bound_keys, waves * m, kk, union_top); break;
       }
       theta_key = max(theta_key, t);
       theta = value_of(theta_key);
+      union_top = max(union_top, theta_key);
+      if (bound_out && slice == 0 && wave_lane() == 0) {
+        bound_out[0] = theta_key;
+        bound_out[1] = union_top;
+      }
     } else {
       __syncthreads();
     }
@@ -1093,7 +1125,16 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
   // The slice's top min(count, kk), sorted descending: the merge only has to merge sorted
   // lists.
   int keep = 0;
-  if (kk > 0) {
+  if (kk > 0 && !sort_end) {
+    keep = count;  // the raw, unsorted list stays in sm.list for the caller
+    if (sel_hist) {
+      // Its keys into the row's selection histogram (finish_small_pool), bins counted down
+      // from the largest key of the first bound's union.
+      const SelBins sb = sel_bins(union_top, bound_out[0]);
+      wave_lds_sync();
+      for (int i = wave_lane(); i < count; i += kWaveSize) atomicAdd(&sel_hist[sb.bin(raw_key(sm.list[i]))], 1u);
+    }
+  } else if (kk > 0) {
     // Prune when the list is longer than kk's register class: the sort then stays in the
     // fewest registers (one for kk <= 64).
     if (count > kWaveSize * ((kk + kWaveSize - 1) / kWaveSize)) {
@@ -1829,7 +1870,133 @@ struct RowSmem {
   WaveMergeSmem merge;
   int next_chunk;
   uint32_t bound_keys[8 * kWaveSize];
+  // Pools of at most 64 (finish_small_pool): the key histogram over every wave's list, the
+  // selected entries and their count, and the row's shared first bound.
+  uint32_t sel_hist[kSelBins];
+  uint64_t sel[kWaveSize];
+  int sel_count;
+  uint32_t bound_key[2];  // the row's first bound and the largest key of its union
 };
+
+// The decisions of sampleFromTopK's draw (src/engine/sampler.ts:170-203) from the running sums
+// of the weights held one per lane (lane i: the i-th running sum, lanes >= K unused): the cut
+// (the first running sum reaching top-p, +1; K without one) and the draw (the first i < cut
+// whose running sum exceeds uniform * the running sum at cut - 1; cut - 1 without one).
+struct Draw {
+  int cut, chosen;
+  double total, target;
+};
+
+__device__ __forceinline__ Draw draw_of(double running, int K, double top_p, double uniform) {
+  const int lane = wave_lane();
+  Draw d;
+  const uint64_t reach = top_p < 1.0 ? __ballot(lane < K && running >= top_p) : 0ull;
+  d.cut = reach ? __ffsll((unsigned long long)reach) : K;
+  d.total = lane_f64(running, d.cut - 1);
+  d.target = uniform * d.total;
+  const uint64_t hit = __ballot(lane < d.cut && d.target < running);
+  d.chosen = hit ? __ffsll((unsigned long long)hit) - 1 : d.cut - 1;
+  return d;
+}
+
+// sampleFromTopK (src/engine/sampler.ts:147-212) over a pool of K <= 64 candidates sorted
+// descending one per lane (lane i holds the i-th largest composite), by one wave in registers.
+// The reference's sums are sequential left-to-right f64 sums and the cut and the draw depend
+// on their last bits. Here the terms come from exp_nonpos (within 8 ulp of exp) and every sum
+// is a parallel prefix (wave_inclusive_scan: each partial sum a tree of at most seven
+// roundings). Against the reference's sequential sums of its exact terms, the weights then
+// differ by less than 82 * 2^-53 relative and their running sums by less than 2^-45.6 of
+// their value: when every comparison that decides the cut and the draw clears its threshold
+// by more than 2^-36 relative, the reference decides the same way. Otherwise the weights are
+// recomputed with V8's exp (fdlibm) and summed bit for bit (reg_seq_sum), and decided again.
+// poolMass and the probability (compared within 1e-5) keep the fast terms. T <= 0 is greedy
+// (sampler.ts:159-167). S1 is the row's sum-exp, obtained after the terms (its loads overlap
+// them).
+template <typename In, class SumExp>
+__device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int row, const In *row_src,
+                                         float M, SumExp sum_exp_of, const tabby_row_params &P) {
+  const int lane = wave_lane();
+  const bool in = lane < K;
+  const double T = P.temperature;
+  const double d = (double)value_of(composite_key(v)) - (double)M;
+  const double e1 = in ? exp_nonpos(d) : 0.0;
+  const double s = !(in && T > 0.0) ? 0.0 : T == 1.0 ? e1 : exp_nonpos(d / T);
+  const double S1 = sum_exp_of();
+  const double exact = e1 / S1;
+  const double pool = lane_f64(wave_inclusive_scan(exact), K - 1);
+  tabby_row_result res;
+  res.max_logit = M;
+  res.sum_exp = S1;
+  res.pool_mass = pool;
+  res.status = TABBY_OK;
+  res.topk_count = min(K, L.topk_cap);
+  int chosen = 0;
+  if (!(T > 0.0)) {
+    res.considered = 1;
+    res.pool_exhausted = 0;
+  } else {
+    const double top_p = P.top_p;
+    const double scaled = lane_f64(wave_inclusive_scan(s), K - 1);
+    const double running = wave_inclusive_scan(in ? s / scaled : 0.0);
+    Draw dr = draw_of(running, K, top_p, P.uniform);
+    // Margins of every comparison that fixed the cut and the draw (running sums are
+    // non-decreasing, so the neighbours of each boundary are the only ones to check).
+    constexpr double kMargin = 1.0 / 68719476736.0;  // 2^-36
+    const double r_cut = lane_f64(running, dr.cut - 1);
+    const double r_before = dr.cut >= 2 ? lane_f64(running, dr.cut - 2) : 0.0;
+    bool clear = true;
+    if (top_p < 1.0) {
+      const double m = kMargin * top_p;
+      clear = (dr.cut < K || r_cut < top_p - m) &&
+              (dr.cut == K || (r_cut >= top_p + m && (dr.cut == 1 || r_before < top_p - m)));
+    }
+    const double r_hi = lane_f64(running, dr.chosen);
+    const double r_lo = dr.chosen >= 1 ? lane_f64(running, dr.chosen - 1) : 0.0;
+    const double m2 = kMargin * dr.total;
+    clear = clear && r_hi > dr.target + m2 && (dr.chosen == 0 || r_lo < dr.target - m2);
+    if (!__builtin_amdgcn_readfirstlane((int)clear)) {
+      // Bit for bit: V8's exp for the weights, sequential sums (sampler.ts:170-203).
+      const double se = in ? fdlibm_exp_inline(d / T) : 0.0;
+      double partial;
+      const double S = reg_seq_sum(se, K, INFINITY, &partial).total;
+      const double w = in ? se / S : 0.0;
+      double exact_running;
+      const SeqSum run = reg_seq_sum(w, K, top_p < 1.0 ? top_p : INFINITY, &exact_running);
+      dr.cut = run.count;
+      dr.total = run.total;
+      dr.target = P.uniform * dr.total;
+      const uint64_t hit = __ballot(lane < dr.cut && dr.target < exact_running);
+      dr.chosen = hit ? __ffsll((unsigned long long)hit) - 1 : dr.cut - 1;
+    }
+    chosen = dr.chosen;
+    res.considered = (uint32_t)dr.cut;
+    res.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
+  }
+  const uint64_t cv = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, chosen) |
+                      ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), chosen) << 32);
+  res.id = (int32_t)composite_index(cv);
+  res.probability = lane_f64(exact, chosen);
+  if (lane == 0) L.results[row] = res;
+  if (in && lane < L.topk_cap) {
+    const uint32_t idx = composite_index(v);
+    L.topk_ids[(size_t)row * L.topk_cap + lane] = (int32_t)idx;
+    L.topk_logits[(size_t)row * L.topk_cap + lane] = load_one(row_src + min(idx, (uint32_t)(L.vocab - 1)));
+  }
+}
+
+// A row (or part of a row) whose pool is at most 64, after its waves' streaming: the waves'
+// lists are unsorted (every entry at or above the row's shared first bound), and the row's top
+// K is selected from their union without sorting them. If the union holds at most 64 entries
+// all are taken; otherwise a 256-bin histogram of the keys below the row max (every wave adds
+// its own entries) gives the bin where the count from the top reaches K, and the entries in
+// and above it are taken. The taken entries (at most 64) go to one LDS array by one atomic per
+// wave; wave 0 sorts them in one register and runs the tail (reg_tail), or, for a part, hands
+// its top K and statistics on to wave_merge_kernel. Returns false, with every wave's list
+// sorted in place and its count cut to K, when more than 64 entries would be taken (the
+// general merge then takes over). Every wave calls it.
+template <typename In>
+__device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, const Workspace &W, int row, int part,
+                                  const tabby_row_params &P, const RowPool &rp, int nw);
 
 template <typename In, int VEC>
 __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Workspace W) {
@@ -1839,18 +2006,25 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
   const int nw = (int)(blockDim.x / kWaveSize);  // the row's waves, >= kRowMinWaves
   const tabby_row_params P = L.params[row];  // kept in registers for the merge
+  const RowPool rp = row_pool(L, P);
+  // Pools of at most 64 skip the waves' end-of-stream sorts and the list merge: the row's top
+  // K is selected from the unsorted lists (finish_small_pool). A part of a row (parts > 1)
+  // only hands its top K on, whatever its pool; a whole row must be finished here.
+  const bool small = rp.valid && rp.K > 0 && rp.K <= kWaveSize && (L.parts > 1 || rp.finite);
   if (threadIdx.x == 0) {
     sm.next_chunk = nw;  // chunk w is wave w's first
+    sm.sel_count = 0;
   }
+  for (int i = (int)threadIdx.x; i < kSelBins; i += (int)blockDim.x) sm.sel_hist[i] = 0u;
   __syncthreads();
   wave_slice<In, VEC, true>(sm.wave[w], L, P, row, w, part, sm.wave[w].list, &sm.stats[w], &sm.next_chunk,
-                            sm.bound_keys, nw);
+                            sm.bound_keys, nw, !small, sm.bound_key, small ? sm.sel_hist : nullptr);
   __syncthreads();
+  if (small && finish_small_pool<In>(sm, L, W, row, part, P, rp, nw)) return;
   constexpr int stride = (int)(sizeof(WaveSmem) / sizeof(uint64_t));
   const RowLists lists{sm.wave[0].list, nw, stride, (int64_t)nw * stride};
   ListMerger<1> m1 = lists_of_wave<1>(lists);
   m1.start();
-  const RowPool rp = row_pool(L, P);
   if (w == kWaves) {
     const RowStats rs = row_stats(sm.stats, nw);
     if (wave_lane() == 0) {
@@ -1880,6 +2054,118 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
     return;
   }
   finish_pool<In>(sm.merge, L, W, row, P, rp, sm.merge.row_max, sm.merge.row_sum);
+}
+
+template <typename In>
+__device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, const Workspace &W, int row, int part,
+                                                  const tabby_row_params &P, const RowPool &rp, int nw) {
+  const int w = wave_id(), lane = wave_lane();
+  const int K = rp.K;
+  const uint64_t *list = sm.wave[w].list;  // raw entries: value bits << 32 | ~index
+  const int count = (int)sm.stats[w].count;
+  // The bin holding the K-th largest key, from the top of the histogram the waves filled as
+  // they finished (four bins per lane; every wave computes the same).
+  const SelBins sb = sel_bins(sm.bound_key[1], sm.bound_key[0]);
+  uint32_t h[4], sum = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    h[q] = sm.sel_hist[lane * 4 + q];
+    sum += h[q];
+  }
+  const uint32_t inc = wave_inclusive_scan_u32(sum);
+  const int total = __builtin_amdgcn_readlane((int)inc, kWaveSize - 1);  // every list entry
+  uint32_t take_key = 0u;  // entries with key >= take_key are taken
+  int taken = total;
+  if (total > kWaveSize) {
+    const int owner = __ffsll((unsigned long long)__ballot(inc >= (uint32_t)K)) - 1;  // total >= K
+    int bin = 0;
+    uint32_t upto = 0;
+    if (lane == owner) {
+      uint32_t c = inc - sum;
+      bool found = false;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        c += h[q];
+        if (!found && c >= (uint32_t)K) {
+          bin = lane * 4 + q;
+          upto = c;
+          found = true;
+        }
+      }
+    }
+    bin = __builtin_amdgcn_readlane(bin, owner);
+    taken = __builtin_amdgcn_readlane((int)upto, owner);
+    if (bin < kSelBins - 1) take_key = sb.lowest(bin);
+    else taken = total;
+  }
+  if (taken > kWaveSize) {
+    // More than 64 would be taken (ties at the boundary, or a row whose top lies far above
+    // the first bound's union): sort each list in place for the general merge.
+    const int keep = min(count, K);
+    if (count <= kWaveSize) store_sorted_top<1>(list, count, keep, sm.wave[w].list);
+    else if (count <= 2 * kWaveSize) store_sorted_top<2>(list, count, keep, sm.wave[w].list);
+    else if (count <= 4 * kWaveSize) store_sorted_top<4>(list, count, keep, sm.wave[w].list);
+    else store_sorted_top<8>(list, count, keep, sm.wave[w].list);
+    if (lane == 0) sm.stats[w].count = (uint32_t)keep;
+    __syncthreads();
+    return false;
+  }
+  for (int base = 0; base < count; base += kWaveSize) {
+    const int i = base + lane;
+    const uint64_t e = i < count ? list[i] : 0ull;
+    const bool take = i < count && raw_key(e) >= take_key;
+    const uint64_t mask = __ballot(take);
+    if (mask) {
+      int at = 0;
+      if (lane == 0) at = atomicAdd(&sm.sel_count, (int)__popcll(mask));
+      at = __builtin_amdgcn_readfirstlane(at);
+      if (take) sm.sel[at + (int)lanes_below(mask)] = e;
+    }
+  }
+  __syncthreads();
+  if (w != 0) return true;
+  uint64_t v[1] = {lane < taken ? composite_of_raw(sm.sel[lane]) : 0ull};
+  wave_sort_desc<1>(v);
+  const int k = min(K, taken);
+  float mx = lane < nw ? sm.stats[lane].max : -INFINITY;
+  const float M = wave_max(mx);
+  auto sum_exp = [&]() { return row_stats(sm.stats, nw).sum_exp; };
+  if (L.parts > 1) {
+    // One part of the row: its top k, sorted, and its statistics go where wave_merge_kernel
+    // reads a slice's (slice = part).
+    const double S1 = sum_exp();
+    uint64_t *out = W.cands + (size_t)row * W.row_cand_stride + (size_t)part * L.list_stride;
+    if (lane < k) out[lane] = v[0];
+    if (lane == 0) {
+      SliceStat st;
+      st.max = M;
+      st.count = (uint32_t)k;
+      st.sum = S1;
+      W.stats[(size_t)row * kMaxSplits + part] = st;
+    }
+    return true;
+  }
+  if (!((M > -INFINITY) && (M < INFINITY))) {
+    if (lane == 0) {
+      write_status(L, row, TABBY_EDOMAIN, M, sum_exp());
+      W.row_state[row].status = TABBY_EDOMAIN;
+    }
+    return true;
+  }
+  const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * L.vocab;
+  bool in_domain = true;
+  reg_tail<In>(v[0], k, L, row, row_src, M,
+               [&]() {
+                 const double S1 = sum_exp();
+                 in_domain = (S1 > 0.0) && (S1 < INFINITY);
+                 return S1;
+               },
+               P);
+  if (!in_domain && lane == 0) {
+    write_status(L, row, TABBY_EDOMAIN, M, row_stats(sm.stats, nw).sum_exp);
+    W.row_state[row].status = TABBY_EDOMAIN;
+  }
+  return true;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2336,6 +2622,15 @@ __global__ __launch_bounds__(kFinishThreads) void head_finish_kernel(Launch L, W
 // Diagnostic kernel: sequential partial sums of t[0..n) by one wave (wave_seq_sum).
 __global__ __launch_bounds__(kWaveSize) void seq_sum_kernel(const double *t, int32_t n, double stop_at,
                                                            double *out, int32_t *count, int32_t wide) {
+  if (wide == 4) {  // the register form (n <= 64): term i in lane i
+    const int lane = wave_lane();
+    const double ti = lane < n ? t[lane] : 0.0;
+    double partial;
+    const SeqSum r = reg_seq_sum(ti, n, stop_at, &partial);
+    if (lane < r.count) out[lane] = partial;
+    if (lane == 0) *count = r.count;
+    return;
+  }
   const SeqSum r = wide ? wave_seq_sum_wide(t, n, out, stop_at) : wave_seq_sum(t, n, out, stop_at);
   if (wave_lane() == 0) *count = r.count;
 }
@@ -2844,6 +3139,7 @@ int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double stop_at, doub
                         int32_t *count_dev, int32_t wide, void *stream) {
   if (!terms_dev || !prefix_dev || !count_dev) return fail(TABBY_EINVAL, "null pointer");
   if (n < 1) return fail(TABBY_EINVAL, "n must be >= 1");
+  if (wide == 4 && n > kWaveSize) return fail(TABBY_EINVAL, "the register form takes at most 64 terms");
   if (wide == 2)
     hipLaunchKernelGGL(seq_sum_block_kernel<kWaves>, dim3(1), dim3(kWaves * kWaveSize), 0, (hipStream_t)stream,
                        terms_dev, n, stop_at, prefix_dev, count_dev);

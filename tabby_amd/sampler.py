@@ -353,8 +353,9 @@ def device_seq_sum(terms, stop_at: float = float("inf"), wide: int = 0, in_place
     """The device's sequential f64 partial sums of a CUDA float64 tensor (diagnostic):
     returns (prefix sums actually written, as a CUDA tensor, count). ``wide``: 0 the
     one-term-per-lane form, 1 the 16-terms-per-lane form used for long sums, 2 that form
-    taken by a four-wave workgroup, 3 by an eight-wave workgroup. ``in_place``: the sums
-    are written over (a copy of) the terms."""
+    taken by a four-wave workgroup, 3 by an eight-wave workgroup, 4 the register form (at
+    most 64 terms, term i in lane i). ``in_place``: the sums are written over (a copy of)
+    the terms."""
     import torch
     t = terms.contiguous().clone() if in_place else terms.contiguous()
     out = t if in_place else torch.zeros_like(t)

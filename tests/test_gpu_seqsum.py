@@ -162,3 +162,28 @@ def test_draw_search_first_above(n):
         bad = np.nonzero(got != want)[0]
         assert bad.size == 0, (f"n={n} trial {trial}: {bad.size} wrong, first target {probes[bad[0]]!r}: "
                                f"got {got[bad[0]]}, want {want[bad[0]]}")
+
+
+@pytest.mark.parametrize("n", [1, 2, 9, 15, 16, 17, 33, 50, 63, 64])
+def test_register_form_short_sums(n):
+    # Pools of at most 64 finish with term i in lane i (wide = 4): sorted weights at several
+    # temperatures, with and without a top-p stop at every position, integer terms (a binade
+    # crossing at each power of two), exact half-ulp ties, and quantised-logit weights.
+    rng = np.random.default_rng(100 + n)
+    l = np.sort(rng.normal(0, 3, n))[::-1]
+    for T in (0.05, 0.7, 2.0, 50.0):
+        s = np.exp((l - l[0]) / T)
+        _check(s, wide=4)
+        w = s / s.sum()
+        c = np.cumsum(w)
+        for st in np.unique(np.concatenate([c, np.nextafter(c, 2.0), [0.5, 0.9, 0.95]])):
+            _check(w, st, wide=4)
+    _check(np.ones(n), wide=4)
+    _check(np.ones(n), float(max(1, n // 2)), wide=4)
+    t = ([1.0] + [2.0 ** -53] * 20 + [2.0 ** -52] + [2.0 ** -53] * 20 + [3 * 2.0 ** -53] * 22)[:n]
+    _check(np.array(t), wide=4)
+    q = np.sort(np.round(rng.normal(0, 2, n) * 4) / 4)[::-1]
+    e = np.exp(q - q[0])
+    _check(e / e.sum(), wide=4)
+    _check(e / e.sum(), 0.98, wide=4)
+    _check(np.concatenate([[1.0], np.full(n - 1, 1e-300)]), wide=4)
