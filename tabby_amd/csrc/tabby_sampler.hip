@@ -1025,19 +1025,27 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
       for (int e = 0; e < kWChunkPerLane; ++e)
         if (wave_local<VEC>(c, e) >= n) cur[e] = __builtin_nanf("");
     }
+    // Elements in groups of four: a group no lane's maximum reaches is skipped with one
+    // branch (most chunks hold a candidate, but only in one or two of their groups).
 #pragma unroll
-    for (int e = 0; e < kWChunkPerLane; ++e) {
-      if (count > prune_at) {
-        const Pruned pr = wave_prune_any(sm, count, kk, theta_key);
-        count = __builtin_amdgcn_readfirstlane(pr.count);
-        theta_key = (uint32_t)__builtin_amdgcn_readfirstlane((int)pr.theta_key);
-        theta = value_of(theta_key);
-      }
-      const bool take = cur[e] >= theta;
-      const uint64_t mask = __ballot(take);
-      if (mask) {
-        if (take) sm.list[count + (int)lanes_below(mask)] = raw_entry(cur[e], (uint32_t)(begin + wave_local<VEC>(c, e)));
-        count = __builtin_amdgcn_readfirstlane(count + (int)__popcll(mask));
+    for (int g = 0; g < kWChunkPerLane / 4; ++g) {
+      const float gm = fmaxf(fmaxf(cur[4 * g], cur[4 * g + 1]), fmaxf(cur[4 * g + 2], cur[4 * g + 3]));
+      if (!__ballot(gm >= theta)) continue;  // NaN padding never reaches theta
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = 4 * g + q;
+        if (count > prune_at) {
+          const Pruned pr = wave_prune_any(sm, count, kk, theta_key);
+          count = __builtin_amdgcn_readfirstlane(pr.count);
+          theta_key = (uint32_t)__builtin_amdgcn_readfirstlane((int)pr.theta_key);
+          theta = value_of(theta_key);
+        }
+        const bool take = cur[e] >= theta;
+        const uint64_t mask = __ballot(take);
+        if (mask) {
+          if (take) sm.list[count + (int)lanes_below(mask)] = raw_entry(cur[e], (uint32_t)(begin + wave_local<VEC>(c, e)));
+          count = __builtin_amdgcn_readfirstlane(count + (int)__popcll(mask));
+        }
       }
     }
   };

@@ -465,3 +465,27 @@ def test_headline_workload_device_form(oracle):
         g.sample_device(x, pd, rd)
         res = rd.cpu().numpy().view(S.RESULT_DTYPE)
     _log("headline device form", compare(w, res, None, None, run_oracle(oracle, w, 0), 0))
+
+
+@pytest.mark.parametrize("rows", [256, 4])
+def test_exact_boundary_draws(oracle, rows):
+    # Pools whose running sums land exactly on top-p and on the draw's target: the top K
+    # values are equal, so every weight is 1/K and the running sums are j/K exactly. The
+    # cut and the draw then sit on a boundary, where only the sequential sums decide (the
+    # fast parallel sums must hand over to the exact ones). 256 rows take the per-row kernel,
+    # 4 rows the parts and the merge kernel.
+    V = 20000
+    w = synth.random_workload(rows=rows, vocab=V, seed=211 + rows, k_choices=(4,), temperatures=(1.0,),
+                              top_ps=(0.5,), sigma=1.0)
+    for r in range(rows):
+        K = (4, 8, 16, 64)[r % 4]
+        w.logits[r, :] = np.minimum(w.logits[r, :], 3.0)
+        pos = (np.arange(K) * 997 + r * 13) % V
+        w.logits[r, pos] = 7.5
+        w.top_k[r] = K
+        j = 1 + (r // 4) % (K - 1)
+        w.top_p[r] = j / K
+        w.temperature[r] = (1.0, 0.5, 2.0)[(r // 8) % 3]
+        w.uniform[r] = ((r // 24) % K) / K if r % 3 else 0.5
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=64)
+    _log(f"exact boundaries, {rows} rows", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
