@@ -8,6 +8,8 @@ of the sampling kernel against MI355X's 8 TB/s, and the Node CPU baseline timed 
 host in the same run.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
+       python bench.py --config N | --host-params | --read-ceiling | --greedy | --softmax
+                       (secondary measurements, one JSON line each)
 """
 from __future__ import annotations
 
@@ -48,6 +50,18 @@ def parse_args():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (reference for the "
                          "FETCH_SIZE / WRITE_SIZE counters) and print its JSON line")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="time a plain read of the headline's rotated logit batches with the "
+                         "sampling kernels' own 16-byte nontemporal loads and launch shape "
+                         "(tabby_debug_stream_read): the practical read ceiling; also the "
+                         "kernel whose FETCH_SIZE calibrates the counter for those loads")
+    ap.add_argument("--greedy", action="store_true",
+                    help="time the greedy fast path (tabby_argmax_device) on the headline's "
+                         "logits; a secondary measurement")
+    ap.add_argument("--softmax", action="store_true",
+                    help="time the attention row softmax (tabby_softmax_rows_device) on a "
+                         "prefill shape: 14 heads x 512 queries over 512 positions, causal; a "
+                         "secondary measurement")
     return ap.parse_args()
 
 
@@ -64,6 +78,94 @@ def copy_calibration() -> int:
     print(json.dumps({"copy_kib_read_per_launch": n * 4 // 1024,
                       "copy_kib_written_per_launch": n * 4 // 1024, "launches": 10}), flush=True)
     return 0
+
+
+def _timed(fn, steps: int, warmup: int, stream) -> float:
+    """Average duration (us) of `steps` back-to-back calls of fn(i), between two HIP events on
+    the launch stream, after `warmup` untimed calls."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
+def secondary(args) -> int:
+    """--read-ceiling, --greedy, --softmax: one JSON line each, not the headline metric."""
+    import numpy as np
+    import torch
+
+    from tabby_amd import sampler as S
+    from tabby_amd import synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    if args.softmax:
+        heads, queries = 14, 512
+        n_rows, row_len = heads * queries, 512
+        g = torch.Generator(device="cpu").manual_seed(7)
+        xs = [(torch.randn(n_rows * row_len, generator=g) * 3).to(dev) for _ in range(ROTATE)]
+        outs = [torch.empty_like(x) for x in xs]
+        us = _timed(lambda i: S.softmax_rows(xs[i % ROTATE], n_rows, row_len, queries, 0,
+                                             out=outs[i % ROTATE], stream=stream),
+                    args.steps, args.warmup, stream)
+        moved = 2 * n_rows * row_len * 4  # read once, written once
+        print(json.dumps({
+            "metric": "attention row softmax (softmaxRows), 14x512 rows x 512 f32, causal",
+            "value": round(moved / (us * 1e-6) / 1e9, 1), "unit": "GB/s", "us_per_call": round(us, 2),
+            "rows_per_s": round(n_rows / (us * 1e-6), 1), "bytes_per_call": moved,
+            "roofline": {"bound": "hbm", "achieved": round(moved / (us * 1e-6) / 1e9, 1),
+                         "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                         "frac": round(moved / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)},
+            "dtype": "f32", "data": "synthetic N(0, 3^2) scores, 4 rotated buffers"}), flush=True)
+        return 0
+    w = synth.config(3, rows=args.rows, vocab=args.vocab)
+    base = torch.from_numpy(w.logits).to(dev)
+    buffers = [torch.roll(base, shifts=(b * 61) % w.rows, dims=0).contiguous() for b in range(ROTATE)]
+    del base
+    nbytes = w.rows * w.vocab * 4
+    if args.read_ceiling:
+        sink = torch.zeros(w.rows, dtype=torch.int32, device=dev)
+        us = _timed(lambda i: S.stream_read(buffers[i % ROTATE], sink, stream=stream),
+                    args.steps, args.warmup, stream)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        print(json.dumps({
+            "metric": "plain read of the headline's logits (read ceiling), 256x151936 f32",
+            "value": round(gbps, 1), "unit": "GB/s", "us_per_call": round(us, 2),
+            "bytes_per_call": nbytes, "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4),
+            "kernel": "stream_read_kernel: one 1,024-lane workgroup per row, 16-byte nontemporal "
+                      "loads, 4 in flight per lane, nothing else",
+            "data": "config-3 logits, 4 rotated device batches"}), flush=True)
+        return 0
+    # --greedy
+    ids = torch.zeros(w.rows, dtype=torch.int32, device=dev)
+    with S.GpuSampler(vocab_max=w.vocab, rows_max=w.rows, k_max=64) as g:
+        us = _timed(lambda i: g.argmax_device(buffers[i % ROTATE], ids, stream=stream),
+                    args.steps, args.warmup, stream)
+        g.argmax_device(buffers[0], ids, stream=stream)
+        torch.cuda.synchronize()
+    got = ids.cpu().numpy()
+    oracle = _oracle()
+    logits = w.logits_f32()
+    pick = np.linspace(0, w.rows - 1, 16).astype(int)
+    bad = [int(r) for r in pick if oracle.argmax(logits[r]) != int(got[r])]
+    gbps = nbytes / (us * 1e-6) / 1e9
+    print(json.dumps({
+        "metric": "greedy rows/sec (argmax fast path), 256x151936 f32 logits",
+        "value": round(w.rows / (us * 1e-6), 1), "unit": "rows/s", "us_per_call": round(us, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4)},
+        "bytes_per_call": nbytes, "dtype": "f32",
+        "data": "config-3 logits, 4 rotated device batches",
+        "parity": {"rows_checked": len(pick), "mismatched_rows": bad}}), flush=True)
+    return 1 if bad else 0
 
 
 def _oracle():
@@ -127,6 +229,11 @@ def main() -> int:
     args = parse_args()
     if args.copy_calibration:
         return copy_calibration()
+    if args.read_ceiling or args.greedy or args.softmax:
+        if args.gpus != 1:
+            print("bench.py measures one GPU only", file=sys.stderr)
+            return 2
+        return secondary(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the sampler is "
               f"single-device in this build; rows shard across GPUs with no communication.",

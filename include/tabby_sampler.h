@@ -128,6 +128,33 @@ TABBY_API int tabby_sampler_sample_device_noalloc(const void *logits_dev, int32_
                                                   tabby_row_result *results_dev, int32_t *topk_ids_dev,
                                                   float *topk_logits_dev, int32_t topk_cap, void *stream);
 
+/*
+ * Greedy fast path: ids_dev[r] = argmax of row r (src/engine/sampler.ts:13-23: the lowest
+ * index among equal maxima, +0 equal to -0, NaN never chosen; 0 when the row's first entry
+ * is NaN or nothing lies above -inf), for logits_dev [rows, vocab] of `dtype` in device
+ * memory. max_logits_dev (may be NULL) receives the chosen entry's value. It replaces the
+ * one-candidate sampling pass the reference's greedy and profile paths make
+ * (forward.runSegment with {topK: 1}, src/worker/inference.worker.ts:216-229, read back by
+ * argmaxOf) and generateGreedy's host argmax (sampler.ts:54-76): one read of the logits, no
+ * pool, no uniform. Uses the handle's scratch; asynchronous on `stream`.
+ */
+TABBY_API int tabby_argmax_device(tabby_sampler *sampler, const void *logits_dev, int32_t dtype,
+                                  int32_t rows, int32_t vocab, int32_t *ids_dev,
+                                  float *max_logits_dev, void *stream);
+/*
+ * Row softmax of attention scores, replacing the softmax_rows kernel
+ * (src/shaders/softmax_rows.wgsl:1-55, dispatched at src/engine/forward.ts:912-926) with the
+ * results of its CPU reference softmaxRows (src/reference/cpu.ts:238-264) bit for bit.
+ * x_dev and out_dev are [n_rows, row_len] f32 in device memory; out_dev may be x_dev (in
+ * place, as the reference runs it) or a buffer that does not overlap it. With
+ * causal_period > 0, row r covers its first causal_offset + (r % causal_period) + 1 entries
+ * and the rest of the row is written 0; causal_period = 0 softmaxes whole rows.
+ * causal_offset + causal_period must not exceed row_len. Asynchronous on `stream`; no
+ * scratch.
+ */
+TABBY_API int tabby_softmax_rows_device(const float *x_dev, float *out_dev, int32_t n_rows,
+                                        int32_t row_len, int32_t causal_period,
+                                        int32_t causal_offset, void *stream);
 /* Message of the calling thread's last failure ("" if none). */
 TABBY_API const char *tabby_last_error(void);
 
@@ -164,6 +191,16 @@ TABBY_API int tabby_debug_seq_sum(const double *terms_dev, int32_t n, double sto
  */
 TABBY_API int tabby_debug_first_above(const double *c_dev, int32_t n, const double *targets_dev,
                                       int32_t m, int32_t *out_dev, void *stream);
+/*
+ * Diagnostic with no counterpart in the reference, for measurements (bench.py
+ * --read-ceiling and the FETCH_SIZE calibration): reads src_dev ([rows, row_floats] f32,
+ * 16-byte aligned, row_floats a multiple of 4) once with the sampling kernels' 16-byte
+ * nontemporal loads in their launch shape (one 1,024-lane workgroup per row) and does nothing
+ * else with it -- the read ceiling of those bytes on this GPU, and a kernel whose FETCH_SIZE
+ * per dispatch must equal a known byte count. sink_dev ([rows] u32) is almost never written.
+ */
+TABBY_API int tabby_debug_stream_read(const float *src_dev, int32_t rows, int64_t row_floats,
+                                      uint32_t *sink_dev, void *stream);
 
 #ifdef __cplusplus
 }

@@ -7,6 +7,10 @@
  *   node node_driver.js sample SPEC.json            rows of an f32 file through sampleRow
  *   node node_driver.js bench SPEC.json             time sampleRow (single thread, or
  *                                                   worker_threads when spec.threads > 1)
+ *   node node_driver.js softmax SPEC.json           softmaxRows over an f32 file
+ *                                                   ({x, nRows, rowLen, period, offset, out})
+ *   node node_driver.js argmax SPEC.json            argmax of each row of an f32 file
+ *                                                   ({logits, rows, vocab, out: JSON ids})
  *
  * SPEC.json: {logits: path (f32, row-major), rows, vocab, topK[], temperature[], topP[],
  *             uniform[], out: path (JSON outcomes), topkCap, threads, seconds}
@@ -111,6 +115,15 @@ function main() {
       });
       w.on('error', (e) => { process.stderr.write(String(e) + '\n'); process.exit(1); });
     }
+  } else if (cmd === 'softmax') {
+    const spec = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
+    const buf = fs.readFileSync(spec.x);
+    const x = new Float32Array(buf.buffer, buf.byteOffset, buf.byteLength / 4);
+    const y = oracle.softmaxRows(x, spec.nRows, spec.rowLen, spec.period, spec.offset);
+    fs.writeFileSync(spec.out, Buffer.from(y.buffer, y.byteOffset, y.byteLength));
+  } else if (cmd === 'argmax') {
+    const spec = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
+    fs.writeFileSync(spec.out, JSON.stringify(readRows(spec).map((row) => oracle.argmax(row))));
   } else if (cmd === 'worker') {
     const { parentPort, workerData } = require('worker_threads');
     const rows = readRows(workerData);

@@ -75,6 +75,9 @@ def load(path: str) -> ctypes.CDLL:
         P(ctypes.c_float), ctypes.c_int32, ctypes.c_int32, ctypes.c_double, ctypes.c_double,
         ctypes.c_double, P(Outcome), P(ctypes.c_int32), P(ctypes.c_float), ctypes.c_int32,
         P(ctypes.c_float), P(ctypes.c_double)]
+    L.tabby_oracle_softmax_rows.argtypes = [P(ctypes.c_float), P(ctypes.c_float), ctypes.c_int32,
+                                            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+    L.tabby_oracle_softmax_rows.restype = None
     return L
 
 
@@ -126,6 +129,17 @@ def f16_to_f32(bits: int) -> float:
 def argmax(row: np.ndarray) -> int:
     row = np.ascontiguousarray(row, dtype=np.float32)
     return lib().tabby_oracle_argmax(_ptr(row, ctypes.c_float), row.size)
+
+
+def softmax_rows(x: np.ndarray, n_rows: int, row_len: int, causal_period: int = 0,
+                 causal_offset: int = 0) -> np.ndarray:
+    """softmaxRows (src/reference/cpu.ts:238-264): a new f32 array [n_rows * row_len]."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    assert x.size == n_rows * row_len
+    out = np.empty_like(x)
+    lib().tabby_oracle_softmax_rows(_ptr(x, ctypes.c_float), _ptr(out, ctypes.c_float), n_rows,
+                                    row_len, causal_period, causal_offset)
+    return out
 
 
 def topk(row: np.ndarray, k: int):
@@ -254,3 +268,31 @@ def node_bench(logits, top_k, temperature, top_p, uniform, seconds: float, threa
         r = subprocess.run(["node", NODE_DRIVER, "bench", sp], check=True, capture_output=True,
                            text=True)
         return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def node_softmax_rows(x: np.ndarray, n_rows: int, row_len: int, causal_period: int = 0,
+                      causal_offset: int = 0) -> np.ndarray:
+    """softmaxRows restated in JS, run by Node with V8's Math.exp and Math.fround."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    with tempfile.TemporaryDirectory() as d:
+        src, dst, sp = os.path.join(d, "x.f32"), os.path.join(d, "y.f32"), os.path.join(d, "s.json")
+        x.tofile(src)
+        with open(sp, "w") as f:
+            json.dump({"x": src, "nRows": int(n_rows), "rowLen": int(row_len),
+                       "period": int(causal_period), "offset": int(causal_offset), "out": dst}, f)
+        subprocess.run(["node", NODE_DRIVER, "softmax", sp], check=True)
+        return np.fromfile(dst, dtype=np.float32)
+
+
+def node_argmax(logits: np.ndarray) -> list:
+    """argmax of each row, restated in JS and run by Node."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    with tempfile.TemporaryDirectory() as d:
+        lp, sp, out = os.path.join(d, "l.f32"), os.path.join(d, "s.json"), os.path.join(d, "o.json")
+        logits.tofile(lp)
+        with open(sp, "w") as f:
+            json.dump({"logits": lp, "rows": int(logits.shape[0]), "vocab": int(logits.shape[1]),
+                       "out": out}, f)
+        subprocess.run(["node", NODE_DRIVER, "argmax", sp], check=True)
+        with open(out) as f:
+            return json.load(f)

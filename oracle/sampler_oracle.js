@@ -12,6 +12,7 @@
  *   sumExp           tests/sampling.test.ts:73-77
  *   sampleRow        encodeSampling (src/engine/forward.ts:522-601) + sampleFromTopK, with
  *                    topK = 0 meaning the whole vocabulary
+ *   softmaxRows      src/reference/cpu.ts:238-264 (f32 = Math.fround)
  */
 
 class SeededRandom {
@@ -131,4 +132,29 @@ function sampleRow(row, params, uniform, topkCap) {
   return outcome;
 }
 
-module.exports = { SeededRandom, argmax, topK, sumExp, sampleFromTopK, sampleRow };
+// Row softmax with a causal prefix: each row's first `valid` entries are normalised in f32
+// steps, the rest set to 0. Returns a new Float32Array.
+function softmaxRows(x, nRows, rowLen, causalPeriod, causalOffset) {
+  const f32 = Math.fround;
+  const period = causalPeriod || 0;
+  const offset = causalOffset || 0;
+  const out = Float32Array.from(x);
+  for (let row = 0; row < nRows; row++) {
+    const valid = period !== 0 ? offset + (row % period) + 1 : rowLen;
+    const base = row * rowLen;
+    let maxV = out[base];
+    for (let i = 1; i < valid; i++) maxV = Math.max(maxV, out[base + i]);
+    let sum = 0;
+    for (let i = 0; i < valid; i++) {
+      const e = f32(Math.exp(f32(out[base + i] - maxV)));
+      out[base + i] = e;
+      sum = f32(sum + e);
+    }
+    const inv = f32(1 / sum);
+    for (let i = 0; i < valid; i++) out[base + i] = f32(out[base + i] * inv);
+    for (let i = valid; i < rowLen; i++) out[base + i] = 0;
+  }
+  return out;
+}
+
+module.exports = { SeededRandom, argmax, topK, sumExp, sampleFromTopK, sampleRow, softmaxRows };

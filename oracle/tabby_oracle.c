@@ -352,3 +352,37 @@ int tabby_oracle_sample_batch(const float *logits, int32_t rows, int32_t n,
   }
   return worst;
 }
+
+/* Math.max(a, b) (ECMAScript): NaN if either is NaN; +0 over -0; else the larger. */
+static float js_max_f32(float a, float b) {
+  if (a != a || b != b) return NAN;
+  if (a == 0.0f && b == 0.0f) return (signbit(a) && signbit(b)) ? -0.0f : 0.0f;
+  return a > b ? a : b;
+}
+
+/*
+ * softmaxRows, src/reference/cpu.ts:238-264. The reference's f32(v) is Math.fround: each f32
+ * step below is the f64 operation of two f32 values rounded to f32, written out as such.
+ * out may equal x (the reference works on a copy, `out = Float32Array.from(x)`).
+ */
+void tabby_oracle_softmax_rows(const float *x, float *out, int32_t n_rows, int32_t row_len,
+                               int32_t causal_period, int32_t causal_offset) {
+  if (out != x) memcpy(out, x, (size_t)n_rows * (size_t)row_len * sizeof(float));
+  for (int32_t row = 0; row < n_rows; ++row) {
+    const int32_t valid =
+        causal_period != 0 ? causal_offset + (row % causal_period) + 1 : row_len;
+    float *o = out + (int64_t)row * row_len;
+    float max_v = o[0];
+    for (int32_t i = 1; i < valid; ++i) max_v = js_max_f32(max_v, o[i]);
+    float sum = 0.0f;
+    for (int32_t i = 0; i < valid; ++i) {
+      const float d = (float)((double)o[i] - (double)max_v);
+      const float e = (float)tabby_oracle_exp((double)d);
+      o[i] = e;
+      sum = (float)((double)sum + (double)e);
+    }
+    const float inv = (float)(1.0 / (double)sum);
+    for (int32_t i = 0; i < valid; ++i) o[i] = (float)((double)o[i] * (double)inv);
+    for (int32_t i = valid; i < row_len; ++i) o[i] = 0.0f;
+  }
+}

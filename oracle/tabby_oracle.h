@@ -17,6 +17,8 @@
  *                                  sampleFromTopK (src/worker/inference.worker.ts:162-168),
  *                                  with top_k = 0 meaning the whole vocabulary
  *   tabby_oracle_f16_to_f32     <- tests/support.ts:67-74 (exact widening)
+ *   tabby_oracle_softmax_rows   <- src/reference/cpu.ts:238-264 (softmaxRows: f32 steps,
+ *                                  Math.exp, causal prefix)
  */
 #ifndef TABBY_ORACLE_H
 #define TABBY_ORACLE_H
@@ -73,6 +75,10 @@ int tabby_oracle_sample_batch(const float *logits, int32_t rows, int32_t n,
                               const int32_t *top_k, const double *temperature,
                               const double *top_p, const double *uniform,
                               tabby_oracle_outcome *out);
+
+/* softmaxRows over [n_rows, row_len] f32; out may equal x. */
+void tabby_oracle_softmax_rows(const float *x, float *out, int32_t n_rows, int32_t row_len,
+                               int32_t causal_period, int32_t causal_offset);
 
 #ifdef __cplusplus
 }

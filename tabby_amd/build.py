@@ -1,7 +1,8 @@
 """Builds the native parts of tabby_amd in-tree.
 
 * ``tabby_amd/lib/libtabby_sampler.so`` -- the HIP kernels and the C ABI of
-  ``include/tabby_sampler.h``, compiled for gfx950 with hipcc.
+  ``include/tabby_sampler.h``, compiled for gfx950 with hipcc (every ``csrc/*.hip``, one
+  object each under ``tabby_amd/_build/``, then linked).
 * ``tabby_amd/node/build/tabby_sampler.node`` -- the N-API addon that exposes the C ABI to
   Node (g++ against ``/usr/include/node``), when the Node headers are present.
 
@@ -20,6 +21,7 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libtabby_sampler.so")
+OBJ_DIR = os.path.join(PKG, "_build")
 NODE_DIR = os.path.join(PKG, "node")
 NODE_ADDON = os.path.join(NODE_DIR, "build", "tabby_sampler.node")
 NODE_INCLUDE = "/usr/include/node"
@@ -48,15 +50,38 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; the sampler library cannot be built")
 
 
+def sources() -> list:
+    """Every HIP translation unit of the library (csrc/*.hip), in name order."""
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
 def build_library(verbose: bool = False) -> str:
+    """Compiles each csrc/*.hip to an object in parallel, then links the shared library."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    hipcc = _hipcc()
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = []
+    for src in sources():
+        obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + ".o")
+        cmd = [hipcc, *compile_flags, "-c", "-o", obj, src]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        jobs.append((cmd, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                                text=True)))
+    objs = []
+    for cmd, obj, proc in jobs:
+        _, err = proc.communicate()
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({proc.returncode}) on {cmd[-1]}:\n{err[-6000:]}")
+        objs.append(obj)
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB_PATH + ".tmp"
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-o", tmp, os.path.join(CSRC, "tabby_sampler.hip")]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr[-6000:]}")
+        raise RuntimeError(f"hipcc (link) failed ({r.returncode}):\n{r.stderr[-6000:]}")
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -41,9 +41,11 @@
 
 #include "block_ops.h"
 #include "device_math.h"
+#include "loads.h"
 #include "seqsum.h"
 #include "wave_ops.h"
 #include "tabby_sampler.h"
+#include "abi_internal.h"
 
 namespace tabby {
 
@@ -133,60 +135,6 @@ __device__ __forceinline__ void row_slice_of(int b, int rows, int splits, int &r
   }
 }
 
-// ---------------------------------------------------------------------------------------
-// Loads: VEC consecutive elements (16 bytes for the vector forms) widened to f32. f16
-// widening is exact (tests/support.ts:61-74 states the same property for its reference).
-// ---------------------------------------------------------------------------------------
-template <typename In, int VEC>
-struct Loader;
-
-// Streaming loads are nontemporal: every logit is read once, so they should not displace
-// other lines in the caches (measured ~12% more HBM bandwidth on MI355X for this pattern).
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-template <>
-struct Loader<float, 4> {
-  __device__ static void load(const float *p, float (&v)[4]) {
-    const f32x4 f = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
-    v[0] = f.x;
-    v[1] = f.y;
-    v[2] = f.z;
-    v[3] = f.w;
-  }
-};
-
-template <>
-struct Loader<float, 1> {
-  __device__ static void load(const float *p, float (&v)[1]) { v[0] = __builtin_nontemporal_load(p); }
-};
-
-__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
-}
-
-template <>
-struct Loader<uint16_t, 8> {
-  __device__ static void load(const uint16_t *p, float (&v)[8]) {
-    const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = half_bits_to_float(w[i] & 0xffffu);
-      v[2 * i + 1] = half_bits_to_float(w[i] >> 16);
-    }
-  }
-};
-
-template <>
-struct Loader<uint16_t, 1> {
-  __device__ static void load(const uint16_t *p, float (&v)[1]) {
-    v[0] = half_bits_to_float(__builtin_nontemporal_load(p));
-  }
-};
-
-__device__ __forceinline__ float load_one(const float *p) { return *p; }
-__device__ __forceinline__ float load_one(const uint16_t *p) { return half_bits_to_float(*p); }
 
 __device__ __forceinline__ int32_t effective_k(const tabby_row_params &p, int vocab) {
   return (p.top_k <= 0 || p.top_k >= vocab) ? vocab : p.top_k;
@@ -2693,14 +2641,47 @@ struct tabby_sampler {
   size_t topk_elems_cap = 0;
 };
 
-namespace {
+namespace tabby {
 
 thread_local std::string g_last_error;
 
-int fail(int status, const std::string &msg) {
+int record_failure(int status, const std::string &msg) {
   g_last_error = msg;
   return status;
 }
+
+int device_cus(int device, int *cus) {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  if (device < 0 || device >= 64) return record_failure(TABBY_EINVAL, "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[device] == 0) {
+    int n = 0;
+    const hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return record_hip_failure(e, "hipDeviceGetAttribute(multiprocessor count)");
+    cached[device] = n;
+  }
+  *cus = cached[device];
+  return TABBY_OK;
+}
+
+int handle_view(const tabby_sampler *h, HandleView *out) {
+  if (!h) return record_failure(TABBY_EINVAL, "sampler handle is null");
+  out->device = h->device;
+  out->cus = h->cus;
+  out->vocab_max = h->vocab_max;
+  out->rows_max = h->rows_max;
+  out->k_max = h->k_max;
+  out->scratch = h->ws.cands;
+  out->scratch_bytes = (size_t)h->rows_max * (size_t)h->ws.row_cand_stride * sizeof(uint64_t);
+  return TABBY_OK;
+}
+
+}  // namespace tabby
+
+namespace {
+
+int fail(int status, const std::string &msg) { return record_failure(status, msg); }
 
 int hip_fail(hipError_t e, const char *what) {
   return fail(TABBY_EHIP, std::string(what) + ": " + hipGetErrorString(e));

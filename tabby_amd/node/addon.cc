@@ -11,6 +11,10 @@
 //   sample                       tabby_sampler_sample: params packed by index.js as
 //                                tabby_row_params, results returned as tabby_row_result bytes
 //                                (encodeSampling + readback, forward.ts:442-451, 522-601)
+//   argmax                       tabby_argmax_device + a 4-byte-per-row readback (the greedy
+//                                path: sampler.ts:13-23, inference.worker.ts:216-229)
+//   softmaxRows / download       tabby_softmax_rows_device between device buffers, and a
+//                                device -> host copy (softmax_rows.wgsl, forward.ts:912-926)
 //   version
 #define NAPI_VERSION 6
 #include <node_api.h>
@@ -27,6 +31,9 @@ namespace {
 
 struct Handle {
   tabby_sampler *sampler = nullptr;
+  int device = 0;
+  int32_t *ids_dev = nullptr;  // argmax results, grown to the largest batch seen
+  size_t ids_cap = 0;
 };
 
 struct DeviceBuffer {
@@ -56,9 +63,20 @@ bool get_i64(napi_env env, napi_value v, int64_t *out) {
   return napi_get_value_int64(env, v, out) == napi_ok;
 }
 
+void release_handle(Handle *h) {
+  if (h->sampler) tabby_sampler_destroy(h->sampler);
+  h->sampler = nullptr;
+  if (h->ids_dev) {
+    (void)hipSetDevice(h->device);
+    (void)hipFree(h->ids_dev);
+  }
+  h->ids_dev = nullptr;
+  h->ids_cap = 0;
+}
+
 void finalize_handle(napi_env, void *data, void *) {
   Handle *h = static_cast<Handle *>(data);
-  if (h->sampler) tabby_sampler_destroy(h->sampler);
+  release_handle(h);
   delete h;
 }
 
@@ -88,7 +106,9 @@ napi_value Create(napi_env env, napi_callback_info info) {
   tabby_sampler *s = nullptr;
   const int rc = tabby_sampler_create((int)a[0], (int32_t)a[1], (int32_t)a[2], (int32_t)a[3], &s);
   if (rc) return fail(env, tabby_last_error());
-  Handle *h = new Handle{s};
+  Handle *h = new Handle{};
+  h->sampler = s;
+  h->device = (int)a[0];
   napi_value out;
   CHECK_NAPI(env, napi_create_external(env, h, finalize_handle, nullptr, &out));
   return out;
@@ -100,8 +120,7 @@ napi_value Destroy(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 1, argv)) return fail(env, "destroy(handle)");
   Handle *h = unwrap_external<Handle>(env, argv[0]);
   if (!h) return fail(env, "destroy: not a sampler handle");
-  if (h->sampler) tabby_sampler_destroy(h->sampler);
-  h->sampler = nullptr;
+  release_handle(h);
   return nullptr;
 }
 
@@ -183,6 +202,16 @@ napi_value Upload(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+napi_value throw_status(napi_env env, int rc) {
+  napi_value err, msg, code;
+  CHECK_NAPI(env, napi_create_string_utf8(env, tabby_last_error(), NAPI_AUTO_LENGTH, &msg));
+  CHECK_NAPI(env, napi_create_error(env, nullptr, msg, &err));
+  CHECK_NAPI(env, napi_create_int32(env, rc, &code));
+  CHECK_NAPI(env, napi_set_named_property(env, err, "status", code));
+  napi_throw(env, err);
+  return nullptr;
+}
+
 // sample(handle, buffer, dtype, rows, vocab, paramsBytes, topkCap)
 //   -> { results: ArrayBuffer(rows*48), topkIds: Int32Array|null, topkLogits: Float32Array|null }
 napi_value Sample(napi_env env, napi_callback_info info) {
@@ -219,15 +248,7 @@ napi_value Sample(napi_env env, napi_callback_info info) {
                                       static_cast<tabby_row_result *>(res_ptr),
                                       static_cast<int32_t *>(ids_ptr), static_cast<float *>(logits_ptr),
                                       (int32_t)cap, nullptr);
-  if (rc) {
-    napi_value err, msg, code;
-    CHECK_NAPI(env, napi_create_string_utf8(env, tabby_last_error(), NAPI_AUTO_LENGTH, &msg));
-    CHECK_NAPI(env, napi_create_error(env, nullptr, msg, &err));
-    CHECK_NAPI(env, napi_create_int32(env, rc, &code));
-    CHECK_NAPI(env, napi_set_named_property(env, err, "status", code));
-    napi_throw(env, err);
-    return nullptr;
-  }
+  if (rc) return throw_status(env, rc);
   napi_value out, ids = nullptr, logits = nullptr, null_value;
   CHECK_NAPI(env, napi_create_object(env, &out));
   CHECK_NAPI(env, napi_get_null(env, &null_value));
@@ -239,6 +260,92 @@ napi_value Sample(napi_env env, napi_callback_info info) {
   CHECK_NAPI(env, napi_set_named_property(env, out, "topkIds", ids ? ids : null_value));
   CHECK_NAPI(env, napi_set_named_property(env, out, "topkLogits", logits ? logits : null_value));
   return out;
+}
+
+// argmax(handle, buffer, dtype, rows, vocab) -> Int32Array(rows): one launch, then the ids
+// read back (rows x 4 bytes).
+napi_value Argmax(napi_env env, napi_callback_info info) {
+  napi_value argv[5];
+  if (!get_args(env, info, 5, argv)) return fail(env, "argmax(handle, buffer, dtype, rows, vocab)");
+  Handle *h = unwrap_external<Handle>(env, argv[0]);
+  if (!h || !h->sampler) return fail(env, "argmax: the sampler was destroyed");
+  DeviceBuffer *b = unwrap_external<DeviceBuffer>(env, argv[1]);
+  if (!b || !b->ptr) return fail(env, "argmax: not a live device buffer");
+  int64_t dtype, rows, vocab;
+  if (!get_i64(env, argv[2], &dtype) || !get_i64(env, argv[3], &rows) || !get_i64(env, argv[4], &vocab))
+    return fail(env, "argmax: integer dtype, rows and vocab expected");
+  if (rows <= 0 || vocab <= 0) return fail(env, "argmax: rows and vocab must be positive");
+  const size_t elem = dtype == TABBY_F16 ? 2 : 4;
+  if ((size_t)rows * (size_t)vocab * elem > b->bytes) return fail(env, "argmax: rows x vocab exceeds the device buffer");
+  if ((size_t)rows > h->ids_cap) {
+    (void)hipSetDevice(h->device);
+    if (h->ids_dev) (void)hipFree(h->ids_dev);
+    h->ids_dev = nullptr;
+    h->ids_cap = 0;
+    if (hipMalloc((void **)&h->ids_dev, (size_t)rows * sizeof(int32_t)) != hipSuccess)
+      return fail(env, "argmax: hipMalloc failed");
+    h->ids_cap = (size_t)rows;
+  }
+  const int rc = tabby_argmax_device(h->sampler, b->ptr, (int32_t)dtype, (int32_t)rows, (int32_t)vocab,
+                                     h->ids_dev, nullptr, nullptr);
+  if (rc) return throw_status(env, rc);
+  napi_value ab, out;
+  void *host;
+  CHECK_NAPI(env, napi_create_arraybuffer(env, (size_t)rows * 4, &host, &ab));
+  if (hipMemcpy(host, h->ids_dev, (size_t)rows * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(env, "argmax: reading the ids back failed");
+  CHECK_NAPI(env, napi_create_typedarray(env, napi_int32_array, (size_t)rows, ab, 0, &out));
+  return out;
+}
+
+// softmaxRows(inBuffer, outBuffer, nRows, rowLen, causalPeriod, causalOffset): on the device,
+// in place when both are the same buffer; returns when it is done.
+napi_value SoftmaxRows(napi_env env, napi_callback_info info) {
+  napi_value argv[6];
+  if (!get_args(env, info, 6, argv))
+    return fail(env, "softmaxRows(inBuffer, outBuffer, nRows, rowLen, causalPeriod, causalOffset)");
+  DeviceBuffer *in = unwrap_external<DeviceBuffer>(env, argv[0]);
+  DeviceBuffer *out = unwrap_external<DeviceBuffer>(env, argv[1]);
+  if (!in || !in->ptr || !out || !out->ptr) return fail(env, "softmaxRows: not a live device buffer");
+  int64_t a[4];
+  for (int i = 0; i < 4; ++i)
+    if (!get_i64(env, argv[2 + i], &a[i])) return fail(env, "softmaxRows: integer arguments expected");
+  if (a[0] <= 0 || a[1] <= 0) return fail(env, "softmaxRows: nRows and rowLen must be positive");
+  const size_t bytes = (size_t)a[0] * (size_t)a[1] * 4;
+  if (bytes > in->bytes || bytes > out->bytes) return fail(env, "softmaxRows: nRows x rowLen exceeds a buffer");
+  (void)hipSetDevice(in->device);
+  const int rc = tabby_softmax_rows_device(static_cast<const float *>(in->ptr), static_cast<float *>(out->ptr),
+                                           (int32_t)a[0], (int32_t)a[1], (int32_t)a[2], (int32_t)a[3], nullptr);
+  if (rc) return throw_status(env, rc);
+  if (hipStreamSynchronize(nullptr) != hipSuccess) return fail(env, "softmaxRows: the kernel failed");
+  return nullptr;
+}
+
+// download(buffer, typedArray): synchronous device -> host copy into the array's bytes.
+napi_value Download(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return fail(env, "download(buffer, typedArray)");
+  DeviceBuffer *b = unwrap_external<DeviceBuffer>(env, argv[0]);
+  if (!b || !b->ptr) return fail(env, "download: not a live device buffer");
+  napi_typedarray_type type;
+  size_t length;
+  void *data;
+  napi_value ab;
+  size_t offset;
+  if (napi_get_typedarray_info(env, argv[1], &type, &length, &data, &ab, &offset) != napi_ok)
+    return fail(env, "download: a typed array is expected");
+  size_t elem = 0;
+  switch (type) {
+    case napi_float32_array: case napi_int32_array: case napi_uint32_array: elem = 4; break;
+    case napi_uint16_array: elem = 2; break;
+    default: return fail(env, "download: a 16- or 32-bit typed array is expected");
+  }
+  const size_t bytes = length * elem;
+  if (bytes > b->bytes) return fail(env, "download: the array is larger than the device buffer");
+  (void)hipSetDevice(b->device);
+  if (hipMemcpy(data, b->ptr, bytes, hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(env, "download: hipMemcpy failed");
+  return nullptr;
 }
 
 napi_value Version(napi_env env, napi_callback_info) {
@@ -256,6 +363,9 @@ napi_value Init(napi_env env, napi_value exports) {
       {"wrapDevicePointer", nullptr, WrapDevicePointer, nullptr, nullptr, nullptr, napi_default, nullptr},
       {"upload", nullptr, Upload, nullptr, nullptr, nullptr, napi_default, nullptr},
       {"sample", nullptr, Sample, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"argmax", nullptr, Argmax, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"softmaxRows", nullptr, SoftmaxRows, nullptr, nullptr, nullptr, napi_default, nullptr},
+      {"download", nullptr, Download, nullptr, nullptr, nullptr, napi_default, nullptr},
       {"version", nullptr, Version, nullptr, nullptr, nullptr, napi_default, nullptr},
   };
   if (napi_define_properties(env, exports, sizeof props / sizeof props[0], props) != napi_ok)

@@ -40,6 +40,47 @@ export declare class SeededRandom {
 export declare const F32: 0;
 export declare const F16: 1;
 
+/** inference.worker.ts:118-123: the worker's candidate pool (1 at temperature 0). */
+export declare function poolSize(sampling: Pick<SamplingParams, 'temperature' | 'topK'>, maxTopK?: number): number;
+export declare const MAX_TOP_K: 64;
+
+/** sampler.ts:32-52 */
+export interface GenerateOptions {
+  maxNewTokens: number;
+  stopTokens?: readonly number[];
+  /** An AbortSignal, or any object with `aborted` (and optionally `reason`). */
+  signal?: { aborted: boolean; reason?: unknown; throwIfAborted?(): void };
+  onToken?: (id: number, index: number) => void;
+}
+export interface GenerateResult {
+  tokens: number[];
+  stopped: boolean;
+  ms: number;
+}
+
+/** The decode loop of inference.worker.ts:108-206 over Sampler.generate. */
+export interface DecodeLoopOptions {
+  promptIds: readonly number[];
+  prefill(ids: readonly number[]): Promise<DeviceLogits | Float32Array>;
+  decode(id: number): Promise<DeviceLogits | Float32Array>;
+  sampling: SamplingParams;
+  maxNewTokens: number;
+  stopTokens?: Iterable<number>;
+  isCancelled?(): boolean;
+  onToken?(id: number, index: number): void;
+  maxTopK?: number;
+}
+export interface DecodeLoopResult {
+  tokens: number[];
+  stopped: boolean;
+  cancelled: boolean;
+  poolExhausted: boolean;
+  readbackPerToken: number;
+  totalReadback: number;
+  ttftMs: number;
+  decodeMs: number;
+}
+
 export declare class DeviceLogits {
   readonly device: number;
   readonly rows: number;
@@ -48,6 +89,7 @@ export declare class DeviceLogits {
   static fromDevicePointer(address: bigint, rows: number, vocab: number, dtype?: 0 | 1,
                            device?: number): DeviceLogits;
   upload(data: Float32Array | Uint16Array): this;
+  download(): Float32Array | Uint16Array;
   free(): void;
 }
 
@@ -61,8 +103,25 @@ export declare class Sampler {
   sample(logits: DeviceLogits | Float32Array | Uint16Array,
          params: Pick<SamplingParams, 'temperature' | 'topK' | 'topP'>,
          rng: UniformSource): SampleOutcome;
+  /** Greedy ids on the GPU, one per row (sampler.ts:13-23). */
+  argmax(logits: DeviceLogits | Float32Array | Uint16Array): Int32Array;
+  generate(opts: DecodeLoopOptions): Promise<DecodeLoopResult>;
+  softmaxRowsDevice(x: DeviceLogits, out: DeviceLogits, nRows: number, rowLen: number,
+                    causalPeriod?: number, causalOffset?: number): DeviceLogits;
   destroy(): void;
 }
+
+/** sampler.ts:13-23, on the GPU. */
+export declare function argmax(logits: Float32Array | Uint16Array | DeviceLogits): number;
+
+/** sampler.ts:54-76, the argmax on the GPU. */
+export declare function generateGreedy(promptIds: readonly number[],
+                                       forward: (ids: readonly number[]) => Promise<Float32Array | DeviceLogits>,
+                                       options: GenerateOptions, sampler?: Sampler): Promise<GenerateResult>;
+
+/** cpu.ts:238-264 (softmax_rows.wgsl's contract), computed on the GPU, bit for bit. */
+export declare function softmaxRows(x: Float32Array, nRows: number, rowLen: number,
+                                    causalPeriod?: number, causalOffset?: number): Float32Array;
 
 export declare function version(): string;
 

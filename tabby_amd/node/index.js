@@ -16,11 +16,20 @@
  *   encodeSampleBlock / decodeSampleBlock   the sample block a decode step reads back
  *                      (forward.ts:127-157): [maxLogit, sumExp, (value, index) * k] as
  *                      f32 words, each index a u32 in its word's bytes
+ *   poolSize           the worker's candidate-pool rule (inference.worker.ts:118-123)
+ *   Sampler.generate   the worker's decode loop (inference.worker.ts:108-206): one launch and
+ *                      one 48-byte readback per token, stop tokens, cancellation re-checked
+ *                      after every await
+ *   argmax / Sampler.argmax / generateGreedy   greedy decoding (sampler.ts:13-23, 54-76) on
+ *                      the GPU's argmax, no pool and no uniform
+ *   softmaxRows / Sampler.softmaxRows   the attention row softmax (cpu.ts:238-264,
+ *                      softmax_rows.wgsl), bit for bit the CPU reference's
  *
  * Every sampling computation runs on the GPU. There is no JavaScript fallback: if the
  * addon or the library is missing, require() throws.
  */
 const native = require('./build/tabby_sampler.node');
+const { performance } = require('perf_hooks');
 
 const F32 = 0;
 const F16 = 1;
@@ -43,6 +52,34 @@ class SeededRandom {
 
 const DEFAULT_SAMPLING = Object.freeze({ temperature: 0.7, topK: 40, topP: 0.9, seed: 0 });
 
+/** The reference's largest pool (MAX_TOP_K, the topK bound of forward.ts:348-351). */
+const MAX_TOP_K = 64;
+
+/**
+ * The candidate pool the worker asks the GPU for (inference.worker.ts:118-123): temperature 0
+ * needs only the argmax; otherwise top-p may look past top-k, so the pool is the larger of the
+ * two intents, topK = 0 meaning the largest pool.
+ */
+function poolSize(sampling, maxTopK) {
+  const cap = maxTopK === undefined ? MAX_TOP_K : maxTopK;
+  return sampling.temperature <= 0 ? 1 : Math.min(cap, Math.max(1, sampling.topK || cap));
+}
+
+/** AbortSignal.throwIfAborted for signals with or without that method (Node 12 has none). */
+function throwIfAborted(signal) {
+  if (!signal) return;
+  if (typeof signal.throwIfAborted === 'function') {
+    signal.throwIfAborted();
+    return;
+  }
+  if (signal.aborted) {
+    if (signal.reason !== undefined) throw signal.reason;
+    const e = new Error('This operation was aborted');
+    e.name = 'AbortError';
+    throw e;
+  }
+}
+
 /** Logits resident on the GPU: [rows, vocab] of f32, or of f16 given as Uint16Array bits. */
 class DeviceLogits {
   constructor(device, rows, vocab, dtype, address) {
@@ -62,6 +99,14 @@ class DeviceLogits {
    */
   static fromDevicePointer(address, rows, vocab, dtype, device) {
     return new DeviceLogits(device || 0, rows, vocab, dtype === undefined ? F32 : dtype, address);
+  }
+
+  /** Copies the buffer back into a new Float32Array (f32) or Uint16Array (f16 bits). */
+  download() {
+    const n = this.rows * this.vocab;
+    const out = this.dtype === F16 ? new Uint16Array(n) : new Float32Array(n);
+    native.download(this.buffer, out);
+    return out;
   }
 
   upload(data) {
@@ -188,24 +233,167 @@ class Sampler {
    * which is uploaded to a staging buffer kept by this Sampler.
    */
   sample(logits, params, rng) {
-    let dev = logits;
-    if (!(logits instanceof DeviceLogits)) {
-      const dtype = dtypeOf(logits);
-      const s = this.staging;
-      if (!s || s.vocab !== logits.length || s.dtype !== dtype) {
-        if (s) s.free();
-        this.staging = new DeviceLogits(this.device, 1, logits.length, dtype);
-      }
-      dev = this.staging.upload(logits);
-    }
+    const dev = logits instanceof DeviceLogits ? logits : this.stage(logits);
     if (dev.rows !== 1) throw new Error('sample() takes one row; use sampleBatch() for more');
     return this.sampleBatch(dev, [params], rng)[0];
+  }
+
+  /**
+   * Greedy ids on the GPU (sampler.ts:13-23 per row): one launch over `logits` (a
+   * DeviceLogits, or a Float32Array / Uint16Array row uploaded to the staging buffer), one
+   * 4-byte-per-row readback. Returns an Int32Array, one id per row.
+   */
+  argmax(logits) {
+    const dev = logits instanceof DeviceLogits ? logits : this.stage(logits);
+    return native.argmax(this.handle, dev.buffer, dev.dtype, dev.rows, dev.vocab);
+  }
+
+  /** Uploads one host row into this Sampler's staging buffer (reused while it fits). */
+  stage(row) {
+    const dtype = dtypeOf(row);
+    const s = this.staging;
+    if (!s || s.vocab !== row.length || s.dtype !== dtype) {
+      if (s) s.free();
+      this.staging = new DeviceLogits(this.device, 1, row.length, dtype);
+    }
+    return this.staging.upload(row);
+  }
+
+  /**
+   * The worker's decode loop (handleGenerate, inference.worker.ts:108-206) with this sampler
+   * in place of encodeSampling + readback + sampleFromTopK: per token one launch on the
+   * step's logits and one 48-byte result read back.
+   *   opts.promptIds           the prompt's ids
+   *   opts.prefill(ids)        -> Promise<DeviceLogits | Float32Array>: the last position's logits
+   *   opts.decode(id)          -> Promise<DeviceLogits | Float32Array>: logits after `id`
+   *   opts.sampling            {temperature, topK, topP, seed}: a SeededRandom(seed) per request
+   *   opts.maxNewTokens, opts.stopTokens (ids), opts.isCancelled() (checked before every
+   *   decode and again after its await), opts.onToken(id, index), opts.maxTopK (default 64:
+   *   the worker's pool bound; the pool is poolSize(sampling, maxTopK))
+   * Resolves to {tokens, stopped, cancelled, poolExhausted, readbackPerToken, totalReadback,
+   * ttftMs, decodeMs}.
+   */
+  async generate(opts) {
+    const sampling = opts.sampling;
+    const stopTokens = new Set(opts.stopTokens || []);
+    const isCancelled = opts.isCancelled || (() => false);
+    const pool = poolSize(sampling, opts.maxTopK);
+    const params = { temperature: sampling.temperature, topK: pool, topP: sampling.topP, seed: sampling.seed };
+    const random = new SeededRandom(sampling.seed);
+    const started = performance.now();
+    const tokens = [];
+    let stopped = false;
+    let poolExhausted = false;
+    let totalReadback = 0;
+    let readbackPerToken = 0;
+
+    const choose = (logits) => {
+      const dev = logits instanceof DeviceLogits ? logits : this.stage(logits);
+      const outcome = this.sampleBatch(dev, [params], random)[0];
+      readbackPerToken = RESULT_BYTES;
+      totalReadback += RESULT_BYTES;
+      if (outcome.poolExhausted) poolExhausted = true;
+      return outcome.id;
+    };
+    const emit = (id) => {
+      tokens.push(id);
+      if (opts.onToken) opts.onToken(id, tokens.length - 1);
+    };
+    const finish = (cancelled, ttftMs, decodeMs) => ({
+      tokens, stopped, cancelled, poolExhausted, readbackPerToken, totalReadback, ttftMs, decodeMs,
+    });
+
+    let next = choose(await opts.prefill(opts.promptIds));
+    const ttftMs = performance.now() - started;
+    if (isCancelled()) return finish(true, ttftMs, 0);
+    emit(next);
+    if (stopTokens.has(next)) stopped = true;
+
+    const decodeStart = performance.now();
+    while (!stopped && tokens.length < opts.maxNewTokens) {
+      if (isCancelled()) break;
+      const logits = await opts.decode(next);
+      // A cancel may land while the forward pass is busy: nothing is emitted after it.
+      if (isCancelled()) break;
+      next = choose(logits);
+      emit(next);
+      if (stopTokens.has(next)) stopped = true;
+    }
+    return finish(isCancelled(), ttftMs, performance.now() - decodeStart);
+  }
+
+  /**
+   * Row softmax on the device (softmax_rows.wgsl's contract; bit for bit cpu.ts:238-264):
+   * `x` and `out` are DeviceLogits-shaped f32 buffers of nRows x rowLen (`out` may be `x`).
+   */
+  softmaxRowsDevice(x, out, nRows, rowLen, causalPeriod, causalOffset) {
+    native.softmaxRows(x.buffer, out.buffer, nRows, rowLen, causalPeriod || 0, causalOffset || 0);
+    return out;
   }
 
   destroy() {
     if (this.staging) this.staging.free();
     this.staging = null;
     native.destroy(this.handle);
+  }
+}
+
+// A Sampler grown to fit, for the module-level functions that mirror the reference's free
+// functions (argmax, generateGreedy, softmaxRows).
+let defaultSampler = null;
+function samplerFor(vocab, rows) {
+  const s = defaultSampler;
+  if (!s || s.vocabMax < vocab || s.rowsMax < rows) {
+    if (s) s.destroy();
+    defaultSampler = new Sampler({ vocabMax: vocab, rowsMax: rows, kMax: MAX_TOP_K });
+  }
+  return defaultSampler;
+}
+
+/** sampler.ts:13-23 on the GPU: the id of the first maximum of one row (Float32Array,
+ *  Uint16Array of f16 bits, or a one-row DeviceLogits). */
+function argmax(logits) {
+  const vocab = logits instanceof DeviceLogits ? logits.vocab : logits.length;
+  return samplerFor(vocab, 1).argmax(logits)[0];
+}
+
+/**
+ * generateGreedy (sampler.ts:54-76): greedy decoding against any function mapping the full
+ * token sequence to next-token logits (a Float32Array or a one-row DeviceLogits), the argmax
+ * taken on the GPU. options: {maxNewTokens, stopTokens, signal, onToken(id, index)}; an
+ * optional Sampler to use. Resolves to {tokens, stopped, ms}.
+ */
+async function generateGreedy(promptIds, forward, options, sampler) {
+  const stopTokens = new Set(options.stopTokens || []);
+  const sequence = promptIds.slice();
+  const tokens = [];
+  const started = performance.now();
+  for (let step = 0; step < options.maxNewTokens; step++) {
+    throwIfAborted(options.signal);
+    const logits = await forward(sequence);
+    const vocab = logits instanceof DeviceLogits ? logits.vocab : logits.length;
+    const next = (sampler || samplerFor(vocab, 1)).argmax(logits)[0];
+    tokens.push(next);
+    sequence.push(next);
+    if (options.onToken) options.onToken(next, step);
+    if (stopTokens.has(next)) return { tokens, stopped: true, ms: performance.now() - started };
+  }
+  return { tokens, stopped: false, ms: performance.now() - started };
+}
+
+/** softmaxRows (cpu.ts:238-264) computed on the GPU: a new Float32Array, bit for bit the
+ *  CPU reference's. */
+function softmaxRows(x, nRows, rowLen, causalPeriod, causalOffset) {
+  if (!(x instanceof Float32Array) || x.length !== nRows * rowLen) {
+    throw new Error(`softmaxRows: expected a Float32Array of ${nRows} x ${rowLen}`);
+  }
+  const s = samplerFor(1, 1);
+  const dev = new DeviceLogits(s.device, nRows, rowLen, F32).upload(x);
+  try {
+    s.softmaxRowsDevice(dev, dev, nRows, rowLen, causalPeriod, causalOffset);
+    return dev.download();
+  } finally {
+    dev.free();
   }
 }
 
@@ -252,6 +440,11 @@ function decodeSampleBlock(raw, k) {
 
 module.exports = {
   Sampler,
+  poolSize,
+  MAX_TOP_K,
+  argmax,
+  generateGreedy,
+  softmaxRows,
   encodeSampleBlock,
   decodeSampleBlock,
   DeviceLogits,

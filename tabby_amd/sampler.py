@@ -46,6 +46,7 @@ EXPORTED_SYMBOLS = (
     "tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
     "tabby_sampler_sample", "tabby_last_error", "tabby_version", "tabby_debug_exp",
     "tabby_debug_seq_sum", "tabby_debug_first_above", "tabby_sampler_sample_device_noalloc",
+    "tabby_argmax_device", "tabby_softmax_rows_device", "tabby_debug_stream_read",
 )
 
 
@@ -79,9 +80,13 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     L.tabby_debug_seq_sum.argtypes = [vp, i32, ctypes.c_double, vp, vp, i32, vp]
     L.tabby_debug_first_above.argtypes = [vp, i32, vp, i32, vp, vp]
     L.tabby_sampler_sample_device_noalloc.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]
+    L.tabby_argmax_device.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp]
+    L.tabby_softmax_rows_device.argtypes = [vp, vp, i32, i32, i32, i32, vp]
+    L.tabby_debug_stream_read.argtypes = [vp, i32, i64, vp, vp]
     for name in ("tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
                  "tabby_sampler_sample", "tabby_debug_exp", "tabby_debug_seq_sum",
-                 "tabby_debug_first_above", "tabby_sampler_sample_device_noalloc"):
+                 "tabby_debug_first_above", "tabby_sampler_sample_device_noalloc",
+                 "tabby_argmax_device", "tabby_softmax_rows_device", "tabby_debug_stream_read"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -289,6 +294,32 @@ class GpuSampler:
             ctypes.c_void_p(topk_logits.data_ptr()) if cap else None, cap, flags,
             self._stream(stream)))
 
+    def argmax_device(self, logits, ids_dev, max_dev=None, stream=None) -> None:
+        """Greedy fast path (tabby_argmax_device): ``ids_dev`` (int32 CUDA tensor [rows])
+        receives each row's argmax, ``max_dev`` (float32, optional) its value.
+        Asynchronous."""
+        x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+        if not x.is_contiguous():
+            raise ValueError("logits must be contiguous")
+        rows, vocab = int(x.shape[0]), int(x.shape[1])
+        if ids_dev.numel() < rows or (max_dev is not None and max_dev.numel() < rows):
+            raise ValueError("ids_dev / max_dev must hold one entry per row")
+        _check(self._lib.tabby_argmax_device(
+            self._h, ctypes.c_void_p(x.data_ptr()), _dtype_code(x), rows, vocab,
+            ctypes.c_void_p(ids_dev.data_ptr()),
+            ctypes.c_void_p(max_dev.data_ptr()) if max_dev is not None else None,
+            self._stream(stream)))
+
+    def argmax(self, logits, stream=None):
+        """argmax of each row (sampler.ts:13-23) on the GPU: an int for a 1-D ``logits``,
+        a list of ints for [rows, vocab]."""
+        import torch
+        x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+        ids = torch.empty(int(x.shape[0]), dtype=torch.int32, device=x.device)
+        self.argmax_device(x, ids, stream=stream)
+        out = [int(v) for v in ids.cpu().tolist()]
+        return out[0] if logits.dim() == 1 else out
+
     def sample(self, logits, params: SamplingParams, rng) -> SampleOutcome:
         """One row: sample(logits, {temperature, topK, topP}, rng) -> SampleOutcome."""
         res, _, _ = self.sample_params(logits, make_params(params, 1, rng))
@@ -338,6 +369,51 @@ def sample(logits, params: SamplingParams, rng) -> SampleOutcome:
             _default.close()
         _default = GpuSampler(vocab_max=vocab, rows_max=1, k_max=max(64, min(k, 1024)))
     return _default.sample(logits, params, rng)
+
+
+def argmax(logits) -> Union[int, List[int]]:
+    """Module-level drop-in for sampler.ts's argmax (lines 13-23), on the GPU: one row (1-D)
+    gives an int, [rows, vocab] a list."""
+    global _default
+    x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+    rows, vocab = int(x.shape[0]), int(x.shape[1])
+    if _default is None or _default.vocab_max < vocab or _default.rows_max < rows:
+        k = _default.k_max if _default is not None else 64
+        if _default is not None:
+            _default.close()
+        _default = GpuSampler(vocab_max=vocab, rows_max=rows, k_max=k)
+    return _default.argmax(logits)
+
+
+def softmax_rows(x, n_rows: int, row_len: int, causal_period: int = 0, causal_offset: int = 0,
+                 out=None, stream=None):
+    """softmaxRows (src/reference/cpu.ts:238-264), the softmax_rows kernel's contract, on the
+    GPU and bit for bit the CPU reference's: ``x`` is a float32 CUDA tensor of n_rows *
+    row_len entries; returns ``out`` (a new tensor, as the CPU reference returns a copy, or
+    ``x`` itself for the in-place form the kernel runs). Asynchronous."""
+    import torch
+    if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float32 CUDA tensor")
+    if x.numel() != n_rows * row_len:
+        raise ValueError(f"x holds {x.numel()} entries, expected {n_rows} x {row_len}")
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.dtype != torch.float32 or out.numel() != x.numel() or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float32 tensor shaped like x")
+    _check(load_library().tabby_softmax_rows_device(
+        ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()), int(n_rows), int(row_len),
+        int(causal_period), int(causal_offset), GpuSampler._stream(stream)))
+    return out
+
+
+def stream_read(src, sink, stream=None) -> None:
+    """The measurement diagnostic tabby_debug_stream_read over a [rows, row_floats] float32
+    CUDA tensor: one plain read with the sampling kernels' loads. ``sink`` is an int32 CUDA
+    tensor of at least ``rows`` entries. Asynchronous."""
+    rows, row_floats = int(src.shape[0]), int(src.shape[1])
+    _check(load_library().tabby_debug_stream_read(
+        ctypes.c_void_p(src.data_ptr()), rows, row_floats, ctypes.c_void_p(sink.data_ptr()),
+        GpuSampler._stream(stream)))
 
 
 def device_exp(x) -> "object":

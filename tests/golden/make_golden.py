@@ -8,6 +8,9 @@ sampling vectors. So the expected values come from two sources:
 * ``sampling_fixture.json`` -- the reference's own CPU fixture (tests/sampling.test.ts:206-250:
   a four-candidate TopKResult and its assertions), with each outcome's values worked out in
   closed form below (exp of integers, the cumulative weights, the cut), not by any oracle.
+* ``softmax_vectors.json`` (``--softmax``) -- softmaxRows outputs of the Node restatement
+  (V8's Math.exp and Math.fround) on integer-derived scores (``softmax_input``): every output
+  bit for small cases, a SHA-256 of the output bytes for long ones.
 * ``node_vectors.json`` -- outputs of the Node restatement (oracle/sampler_oracle.js), which
   runs V8's own Math.exp and Array.prototype.sort comparator the reference runs on: mulberry32
   streams, Math.exp over assorted arguments, and sampled outcomes (+ sorted pool ids) of
@@ -148,8 +151,75 @@ def closed_form_fixture() -> dict:
     }
 
 
+# name -> (n_rows, row_len, causal_period, causal_offset, kind): inputs of softmax_vectors.json
+SOFTMAX_CASES = {
+    # The reference's own kernel test: nHeads 3 x nTokens 5, randomF32(75, 0x50f7, 4),
+    # softmaxRows(scores, 15, 5, 5) (tests/kernels.test.ts:457-473).
+    "reference_causal_3x5": (15, 5, 5, 0, "reference"),
+    # Decode-like: 4 heads x 6 new queries over 10 positions, 4 of them cached (posStart 4).
+    "attention_offset": (24, 10, 6, 4, "scores"),
+    "whole_rows_300": (8, 300, 0, 0, "scores"),
+    "long_rows_5000": (3, 5000, 0, 0, "scores"),
+    "quantised_ties": (6, 777, 0, 0, "ties"),
+    "special_rows": (7, 64, 0, 0, "special"),
+}
+
+
+def softmax_input(name: str) -> np.ndarray:
+    """f32 scores for SOFTMAX_CASES[name], reproducible from mulberry32 without libm.
+
+    reference: randomF32 of tests/support.ts:19-24 -- fround((u * 2 - 1) * scale), scale 4
+    scores:    top 24 bits of a draw scaled to [-24, 24) in steps of 2^-18 (exps from 1 down
+               to subnormal f32 and zero)
+    ties:      multiples of 0.5 in [-8, 8) (long runs of equal terms: exact half-ulp ties)
+    special:   NaN, +inf, all -inf, a single finite entry among -inf, +0/-0 mixes, all equal,
+               and entries 100 apart (exps that underflow)
+    """
+    n_rows, row_len, _, _, kind = SOFTMAX_CASES[name]
+    n = n_rows * row_len
+    if kind == "reference":
+        u = mulberry32_stream(0x50F7, n)
+        return ((u * 2.0 - 1.0) * 4.0).astype(np.float32)
+    u = mulberry32_stream(sum(map(ord, name)) * 7919 & 0xFFFFFFFF, n)
+    bits = (u * 4294967296.0).astype(np.uint64)
+    if kind == "scores":
+        return (((bits >> np.uint64(8)).astype(np.float64) - 8388608.0) / 349525.33333333331).astype(np.float32)
+    if kind == "ties":
+        return (((bits >> np.uint64(27)).astype(np.float64) - 16.0) * 0.5).astype(np.float32)
+    x = (((bits >> np.uint64(8)).astype(np.float64) - 8388608.0) / 1048576.0).reshape(n_rows, row_len)
+    x[0, 9] = np.nan
+    x[1, 3] = np.inf
+    x[2, :] = -np.inf
+    x[3, :] = -np.inf
+    x[3, 40] = -7.0
+    x[4, :] = np.where(bits[4 * row_len:5 * row_len] % np.uint64(2) == 0, 0.0, -0.0)
+    x[5, :] = 2.5
+    x[6, :] = -100.0 * (np.arange(row_len) % 3)
+    return x.astype(np.float32).reshape(-1)
+
+
+def softmax_vectors(o) -> dict:
+    out = {}
+    for name, (n_rows, row_len, period, offset, _) in SOFTMAX_CASES.items():
+        x = softmax_input(name)
+        y = o.node_softmax_rows(x, n_rows, row_len, period, offset)
+        rec = {"n_rows": n_rows, "row_len": row_len, "causal_period": period, "causal_offset": offset,
+               "x_sha256": hashlib.sha256(x.tobytes()).hexdigest(),
+               "y_sha256": hashlib.sha256(y.tobytes()).hexdigest()}
+        if y.size <= 2048:
+            rec["y_bits"] = [int(v) for v in y.view(np.uint32)]
+        out[name] = rec
+    return {"source": "oracle/sampler_oracle.js softmaxRows (V8 Math.exp, Math.fround)", "cases": out}
+
+
 def main() -> None:
     import oracle as o
+
+    if "--softmax" in sys.argv:
+        with open(os.path.join(HERE, "softmax_vectors.json"), "w") as f:
+            json.dump(softmax_vectors(o), f, separators=(",", ":"))
+        print("wrote softmax_vectors.json")
+        return
 
     if not o.node_available():
         raise SystemExit("node is required to write the golden vectors")

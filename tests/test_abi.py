@@ -32,9 +32,10 @@ def test_header_cites_the_reference_for_each_entry_point():
             continue
         block = text[:text.index(name)].rsplit("*/", 2)[-2]
         if "no counterpart in the" in " ".join(block.split()):
-            # An addition of this library (the allocation-free entry): its comment says so
-            # and names the callers it is for.
-            assert "cannot allocate" in block, f"{name} does not name its callers"
+            # An addition of this library (the allocation-free entry, the measurement
+            # diagnostic): its comment says so and names the callers it is for.
+            assert "cannot allocate" in block or "for measurements" in block, \
+                f"{name} does not name its callers"
             continue
         assert re.search(r"\.ts:\d+", block), f"{name} has no reference citation"
 

@@ -331,3 +331,110 @@ def test_rows_outside_the_contract_are_flagged(oracle):
     row[3] = np.nan
     assert oracle.sample_row(row, 5, 0.7, 0.9, 0.5)["status"] != 0
     assert oracle.sample_row(np.full(10, -np.inf, np.float32), 5, 0.7, 0.9, 0.5)["status"] != 0
+
+
+# ---- softmaxRows (src/reference/cpu.ts:238-264) --------------------------------------------
+
+def _same_f32(a_bits, b_bits):
+    """Bitwise equality of f32 arrays (as uint32), any NaN equal to any NaN: a NaN's sign and
+    payload are not part of the result (V8 stores one canonical NaN, x86 arithmetic makes
+    another)."""
+    a = np.asarray(a_bits, np.uint32)
+    b = np.asarray(b_bits, np.uint32)
+    nan_a = (a & 0x7FFFFFFF) > 0x7F800000
+    nan_b = (b & 0x7FFFFFFF) > 0x7F800000
+    return (a == b) | (nan_a & nan_b)
+
+
+def _canonical_nan(y):
+    """A copy with every NaN as the one quiet NaN V8 stores (0x7FC00000)."""
+    y = np.array(y, dtype=np.float32)
+    y[np.isnan(y)] = np.float32("nan")
+    return y
+
+
+@pytest.fixture(scope="module")
+def softmax_vectors():
+    return _load("softmax_vectors.json")
+
+
+def test_softmax_matches_node_vectors(oracle, softmax_vectors):
+    # Bit for bit against the Node restatement (V8's Math.exp and Math.fround), committed.
+    gm = _golden_module()
+    for name, rec in softmax_vectors["cases"].items():
+        x = gm.softmax_input(name)
+        assert hashlib.sha256(x.tobytes()).hexdigest() == rec["x_sha256"], name
+        y = oracle.softmax_rows(x, rec["n_rows"], rec["row_len"], rec["causal_period"],
+                                rec["causal_offset"])
+        if "y_bits" in rec:
+            want = np.asarray(rec["y_bits"], np.uint32)
+            bad = np.nonzero(~_same_f32(y.view(np.uint32), want))[0]
+            assert bad.size == 0, f"{name}: {bad.size} entries differ, first at {bad[:5]}"
+        else:
+            assert hashlib.sha256(_canonical_nan(y).tobytes()).hexdigest() == rec["y_sha256"], name
+
+
+@pytest.mark.skipif(not __import__("oracle").node_available(), reason="node not on PATH")
+def test_softmax_matches_node_live(oracle):
+    rng = np.random.default_rng(5)
+    for n_rows, row_len, period, offset in ((40, 37, 8, 29), (5, 4100, 0, 0), (33, 1, 0, 0)):
+        x = (rng.normal(0, 6, n_rows * row_len)).astype(np.float32)
+        a = oracle.softmax_rows(x, n_rows, row_len, period, offset)
+        b = oracle.node_softmax_rows(x, n_rows, row_len, period, offset)
+        assert np.all(_same_f32(a.view(np.uint32), b.view(np.uint32))), (n_rows, row_len)
+
+
+def test_softmax_closed_forms(oracle):
+    # n equal entries: every exp is exp(0) = 1, the f32 sum is n (exact), out = fround(1 / n).
+    for n in (1, 2, 3, 7, 64, 1000):
+        y = oracle.softmax_rows(np.full(n, -3.25, np.float32), 1, n)
+        assert np.all(y == np.float32(1.0 / n)), n
+    # One finite entry among -inf: exp(-inf - m) = 0 elsewhere.
+    x = np.full(9, -np.inf, np.float32)
+    x[4] = 0.5
+    assert oracle.softmax_rows(x, 1, 9).tolist() == [0, 0, 0, 0, 1, 0, 0, 0, 0]
+    # Two entries ln 3 apart: weights 3/4 and 1/4 up to f32 rounding.
+    y = oracle.softmax_rows(np.array([math.log(3.0), 0.0], np.float32), 1, 2)
+    assert abs(y[0] - 0.75) < 2e-7 and abs(y[1] - 0.25) < 2e-7
+    # A NaN or +inf entry makes the row's valid prefix NaN (Math.max propagates NaN;
+    # inf - inf is NaN); all -inf is NaN too (-inf - -inf). The masked rest is still 0.
+    for bad in (np.nan, np.inf):
+        x = np.array([1.0, bad, 2.0, 0.5, 0.25, -1.0], np.float32)
+        y = oracle.softmax_rows(x, 2, 3, 2, 1)  # row 0 covers 2 entries, row 1 all 3
+        assert np.isnan(y[0]) and np.isnan(y[1]) and y[2] == 0 and np.all(np.isfinite(y[3:]))
+    assert np.all(np.isnan(oracle.softmax_rows(np.full(3, -np.inf, np.float32), 1, 3)))
+
+
+def test_softmax_reference_kernel_test_assertions(oracle):
+    # tests/kernels.test.ts:457-487 on its own input: masked entries exactly 0, each row's
+    # valid prefix sums to 1 to 5 decimals, and every entry within 1e-6 of the f64 softmax.
+    gm = _golden_module()
+    x = gm.softmax_input("reference_causal_3x5")
+    y = oracle.softmax_rows(x, 15, 5, 5, 0).reshape(15, 5)
+    xs = x.reshape(15, 5).astype(np.float64)
+    for row in range(15):
+        valid = row % 5 + 1
+        assert np.all(y[row, valid:] == 0)
+        assert abs(float(np.sum(y[row].astype(np.float64))) - 1.0) < 5e-6
+        e = np.exp(xs[row, :valid] - xs[row, :valid].max())
+        assert np.max(np.abs(y[row, :valid] - e / e.sum())) < 1e-6
+
+
+def test_softmax_rows_match_float64_math(oracle):
+    # Against numpy's f64 softmax: the f32 steps stay within the error of an f32 sequential
+    # sum of `valid` terms (valid * 2^-24 relative) plus a few ulps. Scores near +120 make
+    # exp overflow f32 unless the max is subtracted first; a wrong mask or a sum over the
+    # wrong range fails too.
+    rng = np.random.default_rng(11)
+    for n_rows, row_len, period, offset, shift in ((12, 50, 4, 46, 0.0), (6, 2000, 0, 0, 120.0),
+                                                   (16, 16, 16, 0, -60.0)):
+        x = (rng.normal(0, 5, (n_rows, row_len)) + shift).astype(np.float32)
+        y = oracle.softmax_rows(x.reshape(-1), n_rows, row_len, period, offset).reshape(n_rows, row_len)
+        for r in range(n_rows):
+            valid = offset + r % period + 1 if period else row_len
+            v = x[r, :valid].astype(np.float64)
+            e = np.exp(v - v.max())
+            ref = e / e.sum()
+            tol = (valid * 2.0 ** -24 + 1e-6) * np.maximum(ref, 1e-3)
+            assert np.all(np.abs(y[r, :valid] - ref) <= tol), (r, valid)
+            assert np.all(y[r, valid:] == 0)

@@ -45,6 +45,12 @@ MUTANTS = {
     "exp tiny-argument branch": ("return 1.0 + x;", "return 1.0;"),
     "f16 subnormal scale": ("ldexp((double)mantissa / 1024.0, -14)", "ldexp((double)mantissa / 1024.0, -15)"),
     "f16 exponent bias": ("exponent - 15)", "exponent - 14)"),
+    "softmax causal prefix one short": ("causal_offset + (row % causal_period) + 1",
+                                        "causal_offset + (row % causal_period)"),
+    "softmax without the max": ("(float)((double)o[i] - (double)max_v)", "(float)((double)o[i])"),
+    "softmax tail not zeroed": ("for (int32_t i = valid; i < row_len; ++i) o[i] = 0.0f;", ""),
+    "softmax sum skips the first exp": ("    o[i] = e;\n      sum = (float)((double)sum + (double)e);",
+                                        "    o[i] = e;\n      if (i > 0) sum = (float)((double)sum + (double)e);"),
 }
 
 
@@ -67,6 +73,10 @@ def _battery(oracle, vectors, fixture):
         lambda: pins.test_sum_exp_is_sequential_f64_sum(oracle),
         lambda: pins.test_draw_is_inverse_cdf_over_a_grid(oracle),
         lambda: pins.test_c_oracle_matches_node_vectors(oracle, vectors),
+        lambda: pins.test_softmax_closed_forms(oracle),
+        lambda: pins.test_softmax_reference_kernel_test_assertions(oracle),
+        lambda: pins.test_softmax_rows_match_float64_math(oracle),
+        lambda: pins.test_softmax_matches_node_vectors(oracle, pins._load("softmax_vectors.json")),
     ]
     for i, check in enumerate(checks):
         try:
