@@ -168,6 +168,12 @@ TABBY_API const char *tabby_version(void);
 TABBY_API int tabby_debug_exp(const double *x_dev, double *y_dev, int64_t n, void *stream);
 
 /*
+ * Diagnostic: y[i] = fround(Math.exp(x[i])) for x[i] <= 0 (or NaN), the f32 exps of the row
+ * softmax (src/reference/cpu.ts:253), as tabby_softmax_rows_device computes them. For
+ * parity tests.
+ */
+TABBY_API int tabby_debug_exp_f32(const float *x_dev, float *y_dev, int64_t n, void *stream);
+/*
  * Diagnostic: the device's bit-exact sequential f64 sum (the left-to-right sums of
  * sampler.ts:156-203: poolMass, the scaled total, the running sums), computed in parallel by
  * one wave. terms_dev[0..n) must be >= 0 with terms_dev[0] > 0; prefix_dev[j] receives the

@@ -131,6 +131,25 @@ __device__ __forceinline__ double exp_nonpos(double x) {
   return __builtin_ldexp(__builtin_fma(r8, s1, s0), (int)k);
 }
 
+// fround(Math.exp(x)) for x <= 0 (or NaN): V8's exp rounded to f32, the exps of the reference's
+// f32 softmax (src/reference/cpu.ts:253). exp_nonpos gives e^x within a few f64 ulps, and
+// V8's fdlibm exp is within one; both round to the same f32 unless e^x lies within their
+// combined error of a rounding boundary of f32 (the midpoint between two neighbours). So the
+// fast value is kept when its distance to that boundary exceeds 2^-44 of it -- thousands of
+// times either error bound -- and otherwise (about one argument in 2^20) fdlibm_exp decides.
+__device__ __forceinline__ float exp_to_f32(float x) {
+  if (x != x) return x;
+  const double r = exp_nonpos((double)x);
+  const float y = (float)r;
+  const double res = r - (double)y;  // exact: r and y are within half an f32 ulp
+  const uint32_t yb = __float_as_uint(y);
+  const int e = (int)(yb >> 23);
+  double half = __builtin_ldexp(1.0, (e > 1 ? e : 1) - 151);  // half the f32 ulp above y
+  if (res < 0.0 && (yb & 0x7fffffu) == 0u && e > 1) half *= 0.5;  // below a power of two
+  if (__builtin_fabs(res) < half - r * 0x1p-44) return y;
+  return (float)fdlibm_exp_inline((double)x);
+}
+
 // Out-of-line form for call sites where code size matters more than the call.
 __device__ __noinline__ double fdlibm_exp(double x) { return fdlibm_exp_inline(x); }
 

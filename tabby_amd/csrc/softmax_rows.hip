@@ -8,8 +8,9 @@
 //   e_i   = f32(Math.exp(f32(x_i - M)));  S = f32(S + e_i) left to right from 0
 //   out_i = f32(e_i * f32(1 / S)) for i < valid, 0 for the masked rest.
 // Here each row is one wave. x_i - M is one f32 subtraction (the reference rounds the f64
-// difference of two f32 values to f32, which is the same number); Math.exp is V8's fdlibm
-// method (fdlibm_exp_inline, bit for bit), rounded to f32; 1 / S is an f64 division rounded
+// difference of two f32 values to f32, which is the same number); Math.exp rounded to f32 is
+// exp_to_f32 (a fast f64 exp, V8's fdlibm method where the f32 rounding is close); 1 / S is an
+// f64 division rounded
 // to f32, as JS evaluates it; e_i * inv is one f32 multiplication (the f64 product of two f32
 // values is exact, so JS's rounding of it to f32 is the f32 product).
 //
@@ -39,6 +40,11 @@ namespace tabby {
 namespace {
 
 constexpr int kSmWaves = 4;  // rows per workgroup, one wave each
+// Rows per workgroup of softmax_rows_block_kernel: one per wave. Measured on 14 x 512 causal
+// rows of 512 (the prefill shape): 16 rows 17.8 us, 8 rows 15.5 us, 4 rows 13.1 us -- the
+// batch is small for the chip, and smaller blocks overlap more of their loads, exps and sums.
+constexpr int kBlockRows = 4;
+constexpr int kBlockMinRows = 256;  // batches with fewer rows keep one wave per row
 constexpr double kTwo24 = 16777216.0;
 constexpr double kTwo25 = 33554432.0;
 
@@ -129,7 +135,8 @@ __device__ float seq_sum_f32_step(float P, const float (&t)[V]) {
   }
 }
 
-__device__ __forceinline__ float exp_f32_of(float d) { return (float)fdlibm_exp_inline((double)d); }
+// fround(Math.exp(d)), d = x_i - M <= 0 or NaN (exp_to_f32).
+__device__ __forceinline__ float exp_f32_of(float d) { return exp_to_f32(d); }
 
 struct RowDims {
   int n_rows;
@@ -200,6 +207,100 @@ __global__ __launch_bounds__(kSmWaves *kWaveSize) void softmax_rows_reg_kernel(c
   }
 }
 
+// Many short rows (row_len <= kBlockCols): BR rows per workgroup of four waves, one lane per
+// row for the sum (BR a multiple of 4). The waves take the block's rows one at a time (coalesced loads into
+// registers, the row max by DPP, the exps of their own entries) and leave the exps in LDS;
+// then lane r of wave 0 adds row r's exps left to right -- the reference's own sequential f32
+// sum, one row per lane -- and the waves scale the exps in LDS and write the rows out.
+// HBM traffic 2 * row_len * 4 bytes per row. The sum is a chain of row_len dependent adds
+// per lane, shared by BR rows: for many rows this beats the wave-wide exact scan, whose
+// restart per binade crossing costs a whole step.
+constexpr int kBlockCols = 512;
+
+template <int BR>
+__global__ __launch_bounds__(kSmWaves *kWaveSize) void softmax_rows_block_kernel(const float *x, float *out,
+                                                                                 RowDims d) {
+  // Row pitch: eight pad words keep each row's start 16-byte aligned (the sum reads 16 bytes
+  // at a time), put rows r and r + 1 on different banks, and hold the sum's read-ahead of
+  // eight entries past a full row.
+  constexpr int kPitch = kBlockCols + 8;
+  constexpr int kPer = kBlockCols / kWaveSize;
+  constexpr int kRowsPerWave = BR / kSmWaves;
+  __shared__ float tile[BR * kPitch];
+  __shared__ float inv[BR];
+  const int lane = wave_lane();
+  const int wave = (int)threadIdx.x / kWaveSize;
+  const int row0 = (int)blockIdx.x * BR;
+  const int rows = min(BR, d.n_rows - row0);
+  // Wave w takes rows w, w + 4, ...: every load of all of them is issued before any is used.
+  float v[kRowsPerWave][kPer];
+  int valid[kRowsPerWave];
+#pragma unroll
+  for (int j = 0; j < kRowsPerWave; ++j) {
+    const int r = wave + j * kSmWaves;
+    valid[j] = r < rows ? valid_of(d, row0 + r) : 0;
+    const float *src = x + (size_t)(row0 + r) * d.row_len;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = k * kWaveSize + lane;
+      v[j][k] = i < valid[j] ? __builtin_nontemporal_load(src + i) : -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kRowsPerWave; ++j) {
+    const int r = wave + j * kSmWaves;
+    float mx = -INFINITY;
+    bool nan = false;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      mx = fmaxf(mx, v[j][k]);
+      nan |= v[j][k] != v[j][k];
+    }
+    mx = wave_max(mx);
+    if (__ballot(nan)) mx = __builtin_nanf("");
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = k * kWaveSize + lane;
+      if (i < valid[j]) tile[r * kPitch + i] = exp_f32_of(v[j][k] - mx);
+    }
+  }
+  __syncthreads();
+  if (wave == 0 && lane < rows) {
+    // The row's exps left to right; the next eight are read while these eight are added.
+    const int n = valid_of(d, row0 + lane);
+    const sm_f32x4 *t4 = reinterpret_cast<const sm_f32x4 *>(tile + lane * kPitch);
+    float sum = 0.0f;
+    const int n8 = n / 8;
+    sm_f32x4 a = t4[0], b = t4[1];
+    for (int g = 0; g < n8; ++g) {
+      const sm_f32x4 na = t4[2 * g + 2], nb = t4[2 * g + 3];  // at most the row's padding
+      sum = sum + a.x;
+      sum = sum + a.y;
+      sum = sum + a.z;
+      sum = sum + a.w;
+      sum = sum + b.x;
+      sum = sum + b.y;
+      sum = sum + b.z;
+      sum = sum + b.w;
+      a = na;
+      b = nb;
+    }
+    const float *t = tile + lane * kPitch;
+    for (int i = n8 * 8; i < n; ++i) sum = sum + t[i];
+    inv[lane] = (float)(1.0 / (double)sum);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kRowsPerWave; ++j) {
+    const int r = wave + j * kSmWaves;
+    if (r >= rows) break;
+    const float q = inv[r];
+    float *dst = out + (size_t)(row0 + r) * d.row_len;
+    for (int i = lane; i < d.row_len; i += kWaveSize)
+      __builtin_nontemporal_store(i < valid[j] ? tile[r * kPitch + i] * q : 0.0f, dst + i);
+  }
+}
+
 // Any row: three passes of one element per lane per step (64 entries), as the reference's
 // kernel makes them -- max; exp, sum and e_i written to out; out_i = e_i * inv and the
 // masked tail zeroed. In place (out == x) each lane rewrites only entries it has read.
@@ -232,10 +333,24 @@ __global__ __launch_bounds__(kSmWaves *kWaveSize) void softmax_rows_stream_kerne
   for (int i = lane; i < d.row_len; i += kWaveSize) dst[i] = i < valid ? dst[i] * inv : 0.0f;
 }
 
+__global__ void exp_f32_kernel(const float *x, float *y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = exp_f32_of(x[i]);
+}
+
 }  // namespace
 }  // namespace tabby
 
 using namespace tabby;
+
+extern "C" int tabby_debug_exp_f32(const float *x_dev, float *y_dev, int64_t n, void *stream) {
+  if (!x_dev || !y_dev) return record_failure(TABBY_EINVAL, "null pointer");
+  if (n < 1 || n > ((int64_t)1 << 31)) return record_failure(TABBY_EINVAL, "n must be in [1, 2^31]");
+  hipLaunchKernelGGL(exp_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x_dev,
+                     y_dev, n);
+  TABBY_HIP_CHECK(hipGetLastError());
+  return TABBY_OK;
+}
 
 extern "C" int tabby_softmax_rows_device(const float *x_dev, float *out_dev, int32_t n_rows, int32_t row_len,
                                          int32_t causal_period, int32_t causal_offset, void *stream) {
@@ -257,7 +372,10 @@ extern "C" int tabby_softmax_rows_device(const float *x_dev, float *out_dev, int
   const hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)((n_rows + kSmWaves - 1) / kSmWaves)), block(kSmWaves * kWaveSize);
   const bool aligned = (uintptr_t)x_dev % 16 == 0 && (uintptr_t)out_dev % 16 == 0 && row_len % 4 == 0;
-  if (aligned && row_len <= 256) {
+  if (row_len <= kBlockCols && n_rows >= kBlockMinRows) {
+    hipLaunchKernelGGL(softmax_rows_block_kernel<kBlockRows>, dim3((unsigned)((n_rows + kBlockRows - 1) / kBlockRows)),
+                       block, 0, s, x_dev, out_dev, d);
+  } else if (aligned && row_len <= 256) {
     hipLaunchKernelGGL(softmax_rows_reg_kernel<1>, grid, block, 0, s, x_dev, out_dev, d);
   } else if (aligned && row_len <= 512) {
     hipLaunchKernelGGL(softmax_rows_reg_kernel<2>, grid, block, 0, s, x_dev, out_dev, d);

@@ -47,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "tabby_sampler_sample", "tabby_last_error", "tabby_version", "tabby_debug_exp",
     "tabby_debug_seq_sum", "tabby_debug_first_above", "tabby_sampler_sample_device_noalloc",
     "tabby_argmax_device", "tabby_softmax_rows_device", "tabby_debug_stream_read",
+    "tabby_debug_exp_f32",
 )
 
 
@@ -83,10 +84,12 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     L.tabby_argmax_device.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp]
     L.tabby_softmax_rows_device.argtypes = [vp, vp, i32, i32, i32, i32, vp]
     L.tabby_debug_stream_read.argtypes = [vp, i32, i64, vp, vp]
+    L.tabby_debug_exp_f32.argtypes = [vp, vp, i64, vp]
     for name in ("tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
                  "tabby_sampler_sample", "tabby_debug_exp", "tabby_debug_seq_sum",
                  "tabby_debug_first_above", "tabby_sampler_sample_device_noalloc",
-                 "tabby_argmax_device", "tabby_softmax_rows_device", "tabby_debug_stream_read"):
+                 "tabby_argmax_device", "tabby_softmax_rows_device", "tabby_debug_stream_read",
+                 "tabby_debug_exp_f32"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -422,6 +425,16 @@ def device_exp(x) -> "object":
     y = torch.empty_like(x)
     _check(load_library().tabby_debug_exp(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()),
                                           x.numel(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    return y
+
+
+def device_exp_f32(x):
+    """fround(Math.exp(x)) over a CUDA float32 tensor of arguments <= 0, as the row softmax
+    computes it (diagnostic)."""
+    import torch
+    y = torch.empty_like(x)
+    _check(load_library().tabby_debug_exp_f32(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr()),
+                                              x.numel(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
     return y
 
 

@@ -11,6 +11,8 @@ sampling vectors. So the expected values come from two sources:
 * ``softmax_vectors.json`` (``--softmax``) -- softmaxRows outputs of the Node restatement
   (V8's Math.exp and Math.fround) on integer-derived scores (``softmax_input``): every output
   bit for small cases, a SHA-256 of the output bytes for long ones.
+* ``exp_f32_hard.json`` (``--exp-f32``) -- f32 arguments whose exp sits within 2^-46 of an f32
+  rounding boundary (``hard_exp_f32_arguments``), with V8's fround(Math.exp(x)) for each.
 * ``node_vectors.json`` -- outputs of the Node restatement (oracle/sampler_oracle.js), which
   runs V8's own Math.exp and Array.prototype.sort comparator the reference runs on: mulberry32
   streams, Math.exp over assorted arguments, and sampled outcomes (+ sorted pool ids) of
@@ -212,8 +214,42 @@ def softmax_vectors(o) -> dict:
     return {"source": "oracle/sampler_oracle.js softmaxRows (V8 Math.exp, Math.fround)", "cases": out}
 
 
+def hard_exp_f32_arguments(limit_bits: int = 46) -> np.ndarray:
+    """Every f32 d in [-20, -2^-10) whose e^d (numpy's f64 exp) lies within 2^-limit_bits of
+    its own size from a rounding boundary of f32 (the midpoint between two neighbours, or
+    below a power of two the narrower one): the arguments where rounding a fast f64 exp to
+    f32 could differ from rounding V8's. A scan of 120 M values (about 20 s)."""
+    start = int(np.float32(-2.0 ** -10).view(np.uint32))
+    stop = int(np.float32(-20.0).view(np.uint32))
+    hits = []
+    for lo in range(start, stop, 1 << 22):
+        d = np.arange(lo, min(lo + (1 << 22), stop), dtype=np.uint64).astype(np.uint32).view(np.float32)
+        e = np.exp(d.astype(np.float64))
+        y = e.astype(np.float32)
+        res = e - y.astype(np.float64)
+        yb = y.view(np.uint32)
+        ex = ((yb >> 23) & 0xFF).astype(np.int64)
+        half = np.ldexp(1.0, np.maximum(ex, 1) - 151)
+        half = np.where((res < 0) & ((yb & 0x7FFFFF) == 0) & (ex > 1), half * 0.5, half)
+        hits.append(d[(half - np.abs(res)) / e < 2.0 ** -limit_bits])
+    return np.concatenate(hits)
+
+
+def exp_f32_vectors(o) -> dict:
+    x = hard_exp_f32_arguments()
+    y = o.node_exp(x.astype(np.float64)).astype(np.float32)  # fround(Math.exp(x)) in V8
+    return {"source": "node Math.exp, rounded to f32 (Math.fround)",
+            "x_bits": [int(v) for v in x.view(np.uint32)], "y_bits": [int(v) for v in y.view(np.uint32)]}
+
+
 def main() -> None:
     import oracle as o
+
+    if "--exp-f32" in sys.argv:
+        with open(os.path.join(HERE, "exp_f32_hard.json"), "w") as f:
+            json.dump(exp_f32_vectors(o), f, separators=(",", ":"))
+        print("wrote exp_f32_hard.json")
+        return
 
     if "--softmax" in sys.argv:
         with open(os.path.join(HERE, "softmax_vectors.json"), "w") as f:

@@ -164,6 +164,20 @@ def test_softmax_every_row_length(oracle, row_len):
     _check_softmax(oracle, x, n_rows, row_len, period, row_len - period)
 
 
+@pytest.mark.parametrize("row_len", [1, 3, 100, 257, 511, 512])
+def test_softmax_many_short_rows(oracle, row_len):
+    # Batches of at least 256 rows of at most 512 entries take the lane-per-row kernel:
+    # a ragged last block, causal prefixes, in place and not, ties and NaN rows.
+    rng = np.random.default_rng(row_len + 40)
+    n_rows = 256 + 37
+    x = rng.normal(0, 4, (n_rows, row_len)).astype(np.float32)
+    x[5] = np.round(x[5])
+    x[6, row_len // 2] = np.nan
+    x = x.reshape(-1)
+    _check_softmax(oracle, x, n_rows, row_len)
+    _check_softmax(oracle, x, n_rows, row_len, min(row_len, 64), row_len - min(row_len, 64), in_place=True)
+
+
 @pytest.mark.parametrize("row_len", [512, 4096, 6000])
 def test_softmax_in_place(oracle, row_len):
     rng = np.random.default_rng(row_len + 1)
@@ -221,3 +235,34 @@ def test_softmax_rejects_bad_arguments():
     rc = lib.tabby_softmax_rows_device(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(x.data_ptr() + 8),
                                        4, 10, 0, 0, None)
     assert rc == S.TABBY_EINVAL  # out overlaps x without being x
+
+
+def test_device_exp_f32_matches_v8(oracle):
+    # The softmax's f32 exps: the fast f64 exp with its rounding check, against fround of the
+    # oracle's (V8's) exp -- on the committed arguments closest to an f32 rounding boundary
+    # (the check's fallback path), a million random ones, and special values.
+    import json
+    torch = _torch()
+    with open(os.path.join(HERE, "golden", "exp_f32_hard.json")) as f:
+        hard = np.asarray(json.load(f)["x_bits"], np.uint32).view(np.float32)
+    rng = np.random.default_rng(17)
+    rand = np.concatenate([-rng.random(600_000) * 20, -rng.random(300_000) * 110,
+                           -rng.random(100_000) * 1e-6]).astype(np.float32)
+    special = np.array([0.0, -0.0, -np.inf, np.nan, -87.3, -88.7, -103.2, -103.97, -104.0, -149 * 0.6931,
+                        -745.2, -1e30, -np.finfo(np.float32).tiny], np.float32)
+    x = np.concatenate([hard, rand, special])
+    got = S.device_exp_f32(torch.from_numpy(x).cuda()).cpu().numpy()
+    want = oracle.exp_array(x.astype(np.float64)).astype(np.float32)
+    bad = np.nonzero(~_same_f32(got, want))[0]
+    assert bad.size == 0, (f"{bad.size} differ; first x={x[bad[0]]!r}: device {got[bad[0]]!r} "
+                           f"oracle {want[bad[0]]!r}")
+
+
+def test_softmax_row_of_hard_exp_arguments(oracle):
+    import json
+    with open(os.path.join(HERE, "golden", "exp_f32_hard.json")) as f:
+        hard = np.asarray(json.load(f)["x_bits"], np.uint32).view(np.float32)
+    row = np.concatenate([[0.0], hard]).astype(np.float32)  # x - max = x exactly
+    _check_softmax(oracle, row, 1, row.size)
+    many = np.tile(row, 1100)
+    _check_softmax(oracle, many, 1100, row.size)

@@ -438,3 +438,13 @@ def test_softmax_rows_match_float64_math(oracle):
             tol = (valid * 2.0 ** -24 + 1e-6) * np.maximum(ref, 1e-3)
             assert np.all(np.abs(y[r, :valid] - ref) <= tol), (r, valid)
             assert np.all(y[r, valid:] == 0)
+
+
+def test_exp_rounded_to_f32_on_hard_arguments(oracle):
+    # fround(Math.exp(x)) where e^x sits within 2^-46 of an f32 rounding boundary: the oracle's
+    # exp (bit for bit V8's) rounded to f32 gives V8's answers (committed from Node).
+    d = _load("exp_f32_hard.json")
+    x = np.asarray(d["x_bits"], np.uint32).view(np.float32)
+    want = np.asarray(d["y_bits"], np.uint32)
+    got = oracle.exp_array(x.astype(np.float64)).astype(np.float32).view(np.uint32)
+    assert x.size >= 40 and np.array_equal(got, want)
