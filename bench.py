@@ -116,7 +116,9 @@ def secondary(args) -> int:
         us = _timed(lambda i: S.softmax_rows(xs[i % ROTATE], n_rows, row_len, queries, 0,
                                              out=outs[i % ROTATE], stream=stream),
                     args.steps, args.warmup, stream)
-        moved = 2 * n_rows * row_len * 4  # read once, written once
+        # Each row's causal prefix read once (row r covers r % 512 + 1 entries), every row
+        # written once (the masked rest as zeros).
+        moved = heads * sum(q + 1 for q in range(queries)) * 4 + n_rows * row_len * 4
         print(json.dumps({
             "metric": "attention row softmax (softmaxRows), 14x512 rows x 512 f32, causal",
             "value": round(moved / (us * 1e-6) / 1e9, 1), "unit": "GB/s", "us_per_call": round(us, 2),

@@ -10,9 +10,9 @@
 // by 64-bit composites (value key, ~index), the larger value or, for equal values, the lower
 // index winning -- exactly the reference's order. HBM-bound: vocab * sizeof(In) per row.
 //
-// Grid: rows x splits workgroups of 256 lanes. With splits = 1 a workgroup writes its row's
-// answer; otherwise each writes a composite to the handle's scratch and argmax_finish_kernel
-// combines a row's splits in split order.
+// Grid: one 1,024-lane workgroup per row when there are at least as many rows as CUs, which
+// writes its row's answer; otherwise rows x splits workgroups of 256 lanes, each writing a
+// composite to the handle's scratch, and argmax_finish_kernel combines a row's splits.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -27,8 +27,9 @@
 namespace tabby {
 namespace {
 
-constexpr int kArgBlock = 256;   // lanes per workgroup
-constexpr int kArgUnroll = 4;    // 16-byte loads in flight per lane
+constexpr int kArgBlock = 256;       // lanes per workgroup when rows are split
+constexpr int kArgRowBlock = 1024;   // lanes per workgroup when a workgroup takes a whole row
+constexpr int kArgUnroll = 4;        // 16-byte loads in flight per lane
 constexpr int kArgMaxSplits = 64;
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
@@ -45,12 +46,12 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // the reference's strict `>`: a NaN never compares greater, so it is skipped. A lane whose
 // elements are all -inf or NaN offers -inf at an arbitrary index; the row's answer is then
 // decided without it (see row_answer).
-template <typename In, int VEC>
+template <typename In, int VEC, int BLOCK>
 __device__ __forceinline__ uint64_t lane_first_max(const In *row, int begin, int end) {
   const int lane = (int)threadIdx.x;
   float best = -INFINITY;
   int at = 0;
-  constexpr int kStep = kArgBlock * VEC;
+  constexpr int kStep = BLOCK * VEC;
   // Whole 16-byte groups: kArgUnroll loads in flight per lane.
   const int vend = begin + ((end - begin) / VEC) * VEC;
   int i = begin + lane * VEC;
@@ -99,16 +100,16 @@ __device__ __forceinline__ int row_answer(const In *src, uint64_t best) {
   return (int)composite_index(best);
 }
 
-template <typename In, int VEC>
-__global__ __launch_bounds__(kArgBlock) void argmax_kernel(const In *logits, int vocab, int splits, int split_len,
-                                                           uint64_t *partial, int32_t *ids, float *max_logits) {
-  __shared__ uint64_t wave_best[kArgBlock / kWaveSize];
+template <typename In, int VEC, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void argmax_kernel(const In *logits, int vocab, int splits, int split_len,
+                                                       uint64_t *partial, int32_t *ids, float *max_logits) {
+  __shared__ uint64_t wave_best[BLOCK / kWaveSize];
   const int row = (int)blockIdx.x / splits;
   const int split = (int)blockIdx.x - row * splits;
   const In *src = logits + (size_t)row * (size_t)vocab;
   const int begin = split * split_len;
   const int end = min(vocab, begin + split_len);
-  uint64_t c = lane_first_max<In, VEC>(src, begin, end);
+  uint64_t c = lane_first_max<In, VEC, BLOCK>(src, begin, end);
   c = wave_max_u64(c);
   const int w = (int)threadIdx.x / kWaveSize;
   if (wave_lane() == 0) wave_best[w] = c;
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(kArgBlock) void argmax_kernel(const In *logits, int
   if (threadIdx.x == 0) {
     uint64_t b = wave_best[0];
 #pragma unroll
-    for (int i = 1; i < kArgBlock / kWaveSize; ++i) b = tmax(b, wave_best[i]);
+    for (int i = 1; i < BLOCK / kWaveSize; ++i) b = tmax(b, wave_best[i]);
     if (splits == 1) {
       const int id = row_answer(src, b);
       ids[row] = id;
@@ -146,8 +147,16 @@ __global__ __launch_bounds__(kArgBlock) void argmax_finish_kernel(const In *logi
 template <typename In, int VEC>
 int launch_argmax(const HandleView &hv, const In *logits, int rows, int vocab, int32_t *ids, float *max_logits,
                   hipStream_t stream) {
-  // Workgroups enough for about four 4-wave workgroups per CU (16 waves, as the sampling
-  // kernels keep resident), each split at least 16 KB of logits, at most kArgMaxSplits.
+  if (rows >= hv.cus) {
+    // A 16-wave workgroup per row writes the row's answer itself: no second launch (a split
+    // batch's finishing kernel cost ~4 us on 256 rows, the read itself ~24.7 us).
+    hipLaunchKernelGGL((argmax_kernel<In, VEC, kArgRowBlock>), dim3((unsigned)rows), dim3(kArgRowBlock), 0, stream,
+                       logits, vocab, 1, vocab, (uint64_t *)nullptr, ids, max_logits);
+    TABBY_HIP_CHECK(hipGetLastError());
+    return TABBY_OK;
+  }
+  // Fewer rows: workgroups enough for about four 4-wave workgroups per CU, each split at
+  // least 16 KB of logits, at most kArgMaxSplits.
   const int min_split = (16384 / (int)sizeof(In) + kArgBlock * VEC - 1) / (kArgBlock * VEC) * (kArgBlock * VEC);
   const int want = (4 * hv.cus + rows - 1) / rows;
   const int by_len = (vocab + min_split - 1) / min_split;
@@ -160,8 +169,8 @@ int launch_argmax(const HandleView &hv, const In *logits, int rows, int vocab, i
   uint64_t *partial = (uint64_t *)hv.scratch;
   if (splits > 1 && (size_t)rows * splits * sizeof(uint64_t) > hv.scratch_bytes)
     return record_failure(TABBY_ECAPACITY, "argmax: the handle's scratch is too small for this batch");
-  hipLaunchKernelGGL((argmax_kernel<In, VEC>), dim3((unsigned)(rows * splits)), dim3(kArgBlock), 0, stream, logits,
-                     vocab, splits, split_len, partial, ids, max_logits);
+  hipLaunchKernelGGL((argmax_kernel<In, VEC, kArgBlock>), dim3((unsigned)(rows * splits)), dim3(kArgBlock), 0,
+                     stream, logits, vocab, splits, split_len, partial, ids, max_logits);
   TABBY_HIP_CHECK(hipGetLastError());
   if (splits > 1) {
     hipLaunchKernelGGL((argmax_finish_kernel<In>), dim3((unsigned)((rows + kArgBlock - 1) / kArgBlock)),

@@ -75,17 +75,17 @@ def test_argmax_special_rows(oracle):
     assert np.all(_same_f32(mx, logits[np.arange(len(rows)), want]))
 
 
-@pytest.mark.parametrize("vocab", [151936, 4099])
-def test_argmax_f16(oracle, vocab):
-    rng = np.random.default_rng(vocab)
-    h = rng.normal(0, 3, (64, vocab)).astype(np.float16)
+@pytest.mark.parametrize("rows,vocab", [(64, 151936), (64, 4099), (256, 151936), (260, 4099)])
+def test_argmax_f16(oracle, rows, vocab):
+    rng = np.random.default_rng(vocab + rows)
+    h = rng.normal(0, 3, (rows, vocab)).astype(np.float16)
     h[5, :] = np.float16(1.0)
     h[6, 123] = np.float16(np.nan)
     ids, mx = _gpu_argmax(h, "f16")
     wide = h.astype(np.float32)
-    want = np.array([oracle.argmax(wide[r]) for r in range(64)])
+    want = np.array([oracle.argmax(wide[r]) for r in range(rows)])
     assert np.array_equal(ids, want)
-    assert np.array_equal(mx, wide[np.arange(64), want])
+    assert np.array_equal(mx, wide[np.arange(rows), want])
 
 
 def test_argmax_agrees_with_greedy_sampling(oracle):
