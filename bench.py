@@ -58,6 +58,11 @@ def parse_args():
     ap.add_argument("--greedy", action="store_true",
                     help="time the greedy fast path (tabby_argmax_device) on the headline's "
                          "logits; a secondary measurement")
+    ap.add_argument("--lmhead", action="store_true",
+                    help="time the lm_head fused with sampling (tabby_sampler_sample_lmhead_q4_device) "
+                         "against the unfused pair (tabby_lmhead_q4_device, then the sampler) on "
+                         "Qwen2.5-0.5B's lm_head shape (151,936 x 896 int4, block 32), one decode "
+                         "row (--rows up to 8); a secondary measurement")
     ap.add_argument("--softmax", action="store_true",
                     help="time the attention row softmax (tabby_softmax_rows_device) on a "
                          "prefill shape: 14 heads x 512 queries over 512 positions, causal; a "
@@ -128,6 +133,8 @@ def secondary(args) -> int:
                          "frac": round(moved / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)},
             "dtype": "f32", "data": "synthetic N(0, 3^2) scores, 4 rotated buffers"}), flush=True)
         return 0
+    if args.lmhead:
+        return lmhead_bench(args, dev, stream)
     w = synth.config(3, rows=args.rows, vocab=args.vocab)
     base = torch.from_numpy(w.logits).to(dev)
     buffers = [torch.roll(base, shifts=(b * 61) % w.rows, dims=0).contiguous() for b in range(ROTATE)]
@@ -167,6 +174,58 @@ def secondary(args) -> int:
         "bytes_per_call": nbytes, "dtype": "f32",
         "data": "config-3 logits, 4 rotated device batches",
         "parity": {"rows_checked": len(pick), "mismatched_rows": bad}}), flush=True)
+    return 1 if bad else 0
+
+
+def lmhead_bench(args, dev, stream) -> int:
+    """--lmhead: the fused lm_head + sampling call against the unfused pair, Qwen2.5-0.5B's
+    lm_head (151,936 x 896 int4, block 32) and k 40 / p 0.9 / T 0.7 (DEFAULT_SAMPLING)."""
+    import numpy as np
+    import torch
+
+    from tabby_amd import sampler as S
+    from tabby_amd import synth
+
+    vocab, hidden, block = 151936, 896, 32
+    rows = min(args.rows, 8) if args.rows != 256 else 1
+    words, f16, f32 = synth.lm_head_q4(vocab, hidden, block)
+    head = S.LmHeadQ4(words, f16, vocab, hidden, block)
+    xs = [torch.from_numpy(synth.hidden_states(rows, hidden, seed=11 + b)).to(dev) for b in range(ROTATE)]
+    params = np.zeros(rows, dtype=S.PARAMS_DTYPE)
+    params["temperature"], params["top_k"], params["top_p"] = 0.7, 40, 0.9
+    params["uniform"] = synth.mulberry32_stream(5, rows)
+    pdev = torch.from_numpy(params.view(np.uint8).copy()).to(dev)
+    res = torch.zeros(rows * S.RESULT_DTYPE.itemsize, dtype=torch.uint8, device=dev)
+    logits = torch.empty((rows, vocab), dtype=torch.float32, device=dev)
+    g = S.GpuSampler(vocab_max=vocab, rows_max=max(rows, 1), k_max=64)
+    fused_us = _timed(lambda i: g.sample_lmhead_q4_device(head, xs[i % ROTATE], pdev, res, stream=stream),
+                      args.steps, args.warmup, stream)
+
+    def unfused(i):
+        head.logits(xs[i % ROTATE], out=logits, stream=stream)
+        g.sample_device(logits, pdev, res, stream=stream)
+    unfused_us = _timed(unfused, args.steps, args.warmup, stream)
+    gemv_us = _timed(lambda i: head.logits(xs[i % ROTATE], out=logits, stream=stream),
+                     args.steps, args.warmup, stream)
+    # The answer of the fused call against the oracle (matmulQuantized, then the sampler).
+    fused = g.sample_lmhead_q4(head, xs[0], params)
+    g.close()
+    oracle = _oracle()
+    ref_logits = oracle.matmul_quantized(words, f32, xs[0].cpu().numpy(), vocab, hidden)
+    bad = [r for r in range(rows)
+           if oracle.sample_row(ref_logits[r], 40, 0.7, 0.9, float(params["uniform"][r]))["id"] != int(fused["id"][r])]
+    weight_bytes = words.nbytes + f16.nbytes
+    print(json.dumps({
+        "metric": f"lm_head + sampling per decode step, 151936x896 int4 (block 32), {rows} row(s)",
+        "value": round(fused_us, 2), "unit": "us", "higher_is_better": False,
+        "fused_us": round(fused_us, 2), "unfused_us": round(unfused_us, 2), "gemv_only_us": round(gemv_us, 2),
+        "weight_bytes": weight_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(weight_bytes / (fused_us * 1e-6) / 1e9, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(weight_bytes / (fused_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)},
+        "dtype": "int4 weights, f32 arithmetic",
+        "data": "random-init int4 weights (synth.lm_head_q4), randomF32 hidden states, 4 rotated",
+        "parity": {"rows_checked": rows, "mismatched_rows": bad}}), flush=True)
     return 1 if bad else 0
 
 
@@ -231,7 +290,7 @@ def main() -> int:
     args = parse_args()
     if args.copy_calibration:
         return copy_calibration()
-    if args.read_ceiling or args.greedy or args.softmax:
+    if args.read_ceiling or args.greedy or args.softmax or args.lmhead:
         if args.gpus != 1:
             print("bench.py measures one GPU only", file=sys.stderr)
             return 2

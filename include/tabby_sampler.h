@@ -155,6 +155,47 @@ TABBY_API int tabby_argmax_device(tabby_sampler *sampler, const void *logits_dev
 TABBY_API int tabby_softmax_rows_device(const float *x_dev, float *out_dev, int32_t n_rows,
                                         int32_t row_len, int32_t causal_period,
                                         int32_t causal_offset, void *stream);
+/*
+ * The lm_head's int4 weights (src/engine/forward.ts:408-428, encodeQuantMatmul :732-770;
+ * src/shaders/matvec_q4.wgsl), repacked once into this library's layout. Input: the
+ * reference's layout (tools/convert.py): words_dev u32 [vocab][hidden / 8] (eight 4-bit
+ * values per word, value j at bits 4j, dequant(q) = (q - 8) * scale) and scales_dev f16 bits
+ * [vocab][hidden / block_size]. Output: packed_dev u32 [hidden / 32][vocab][4] and
+ * packed_scales_dev f16 bits [hidden / block_size][vocab] (a wave's 64 output rows read
+ * contiguous bytes). hidden and block_size are multiples of 32, block_size divides hidden;
+ * word arrays 16-byte aligned. Asynchronous on `stream`.
+ */
+TABBY_API int tabby_lmhead_q4_pack_device(const uint32_t *words_dev, const uint16_t *scales_dev,
+                                          int32_t vocab, int32_t hidden, int32_t block_size,
+                                          uint32_t *packed_dev, uint16_t *packed_scales_dev,
+                                          void *stream);
+/*
+ * The lm_head matmul on its own (matvec_q4.wgsl's contract): logits_dev [rows][vocab] f32 =
+ * hidden_dev [rows][hidden] f32 times the packed weights (+ bias_dev [vocab], may be NULL),
+ * bit for bit the CPU reference matmulQuantized (src/reference/cpu.ts:352-393). Any number of
+ * rows (weights re-read per eight rows). Asynchronous on `stream`.
+ */
+TABBY_API int tabby_lmhead_q4_device(const uint32_t *packed_dev, const uint16_t *packed_scales_dev,
+                                     const float *bias_dev, const float *hidden_dev, int32_t rows,
+                                     int32_t vocab, int32_t hidden, int32_t block_size,
+                                     float *logits_dev, void *stream);
+/*
+ * The lm_head fused with sampling: for each of `rows` (1..8) hidden states, the logits of
+ * tabby_lmhead_q4_device are computed and sampled without being written to memory -- the
+ * composition of the reference's lm_head (forward.ts:408-428), encodeSampling
+ * (forward.ts:522-601) and sampleFromTopK (sampler.ts:147-212) in one pass over the weights.
+ * params_dev / results_dev as for tabby_sampler_sample_device. Pools of at most 64 (the
+ * reference's topK bound, forward.ts:348-351; top_k 0 or above 64 gives the row TABBY_EINVAL);
+ * no top-k lists. Uses the handle's scratch (vocab <= vocab_max, rows <= rows_max).
+ * Asynchronous on `stream`.
+ */
+TABBY_API int tabby_sampler_sample_lmhead_q4_device(tabby_sampler *sampler, const uint32_t *packed_dev,
+                                                    const uint16_t *packed_scales_dev,
+                                                    const float *bias_dev, const float *hidden_dev,
+                                                    int32_t rows, int32_t vocab, int32_t hidden,
+                                                    int32_t block_size,
+                                                    const tabby_row_params *params_dev,
+                                                    tabby_row_result *results_dev, void *stream);
 /* Message of the calling thread's last failure ("" if none). */
 TABBY_API const char *tabby_last_error(void);
 

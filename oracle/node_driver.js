@@ -11,6 +11,10 @@
  *                                                   ({x, nRows, rowLen, period, offset, out})
  *   node node_driver.js argmax SPEC.json            argmax of each row of an f32 file
  *                                                   ({logits, rows, vocab, out: JSON ids})
+ *   node node_driver.js matmulq SPEC.json           matmulQuantized ({words: u32 file, scales:
+ *                                                   f32 file, x: f32 file, bias: f32 file or
+ *                                                   null, nTokens, outDim, inDim, bits,
+ *                                                   blockSize, out: f32 file})
  *
  * SPEC.json: {logits: path (f32, row-major), rows, vocab, topK[], temperature[], topP[],
  *             uniform[], out: path (JSON outcomes), topkCap, threads, seconds}
@@ -124,6 +128,16 @@ function main() {
   } else if (cmd === 'argmax') {
     const spec = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
     fs.writeFileSync(spec.out, JSON.stringify(readRows(spec).map((row) => oracle.argmax(row))));
+  } else if (cmd === 'matmulq') {
+    const spec = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
+    const view = (file, T) => {
+      const b = fs.readFileSync(file);
+      return new T(b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength));
+    };
+    const y = oracle.matmulQuantized(view(spec.words, Uint32Array), view(spec.scales, Float32Array),
+                                     view(spec.x, Float32Array), spec.nTokens, spec.outDim, spec.inDim,
+                                     spec.bits, spec.blockSize, spec.bias ? view(spec.bias, Float32Array) : null);
+    fs.writeFileSync(spec.out, Buffer.from(y.buffer, y.byteOffset, y.byteLength));
   } else if (cmd === 'worker') {
     const { parentPort, workerData } = require('worker_threads');
     const rows = readRows(workerData);

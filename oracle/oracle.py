@@ -78,6 +78,11 @@ def load(path: str) -> ctypes.CDLL:
     L.tabby_oracle_softmax_rows.argtypes = [P(ctypes.c_float), P(ctypes.c_float), ctypes.c_int32,
                                             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
     L.tabby_oracle_softmax_rows.restype = None
+    L.tabby_oracle_matmul_quantized.argtypes = [P(ctypes.c_uint32), P(ctypes.c_float), P(ctypes.c_float),
+                                                ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                                ctypes.c_int32, ctypes.c_int32, P(ctypes.c_float),
+                                                P(ctypes.c_float)]
+    L.tabby_oracle_matmul_quantized.restype = None
     return L
 
 
@@ -129,6 +134,23 @@ def f16_to_f32(bits: int) -> float:
 def argmax(row: np.ndarray) -> int:
     row = np.ascontiguousarray(row, dtype=np.float32)
     return lib().tabby_oracle_argmax(_ptr(row, ctypes.c_float), row.size)
+
+
+def matmul_quantized(words: np.ndarray, scales: np.ndarray, x: np.ndarray, out_dim: int, in_dim: int,
+                     bits: int = 4, block_size: int = 32, bias=None) -> np.ndarray:
+    """matmulQuantized (src/reference/cpu.ts:352-393): y [n_tokens, out_dim] f32 for x
+    [n_tokens, in_dim] f32, words u32 [out_dim * in_dim * bits / 32], scales f32
+    [out_dim * in_dim / block_size]."""
+    words = np.ascontiguousarray(words, dtype=np.uint32).reshape(-1)
+    scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_dim)
+    y = np.empty((x.shape[0], out_dim), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    lib().tabby_oracle_matmul_quantized(_ptr(words, ctypes.c_uint32), _ptr(scales, ctypes.c_float),
+                                        _ptr(x, ctypes.c_float), x.shape[0], out_dim, in_dim, bits,
+                                        block_size, _ptr(b, ctypes.c_float) if b is not None else None,
+                                        _ptr(y, ctypes.c_float))
+    return y
 
 
 def softmax_rows(x: np.ndarray, n_rows: int, row_len: int, causal_period: int = 0,
@@ -296,3 +318,23 @@ def node_argmax(logits: np.ndarray) -> list:
         subprocess.run(["node", NODE_DRIVER, "argmax", sp], check=True)
         with open(out) as f:
             return json.load(f)
+
+
+def node_matmul_quantized(words, scales, x, out_dim: int, in_dim: int, bits: int = 4,
+                          block_size: int = 32, bias=None) -> np.ndarray:
+    """matmulQuantized restated in JS, run by Node (Math.fround)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_dim)
+    with tempfile.TemporaryDirectory() as d:
+        paths = {k: os.path.join(d, k) for k in ("w", "s", "x", "b", "y", "spec")}
+        np.ascontiguousarray(words, np.uint32).tofile(paths["w"])
+        np.ascontiguousarray(scales, np.float32).tofile(paths["s"])
+        x.tofile(paths["x"])
+        if bias is not None:
+            np.ascontiguousarray(bias, np.float32).tofile(paths["b"])
+        with open(paths["spec"], "w") as f:
+            json.dump({"words": paths["w"], "scales": paths["s"], "x": paths["x"],
+                       "bias": paths["b"] if bias is not None else None, "nTokens": int(x.shape[0]),
+                       "outDim": int(out_dim), "inDim": int(in_dim), "bits": int(bits),
+                       "blockSize": int(block_size), "out": paths["y"]}, f)
+        subprocess.run(["node", NODE_DRIVER, "matmulq", paths["spec"]], check=True)
+        return np.fromfile(paths["y"], dtype=np.float32).reshape(x.shape[0], out_dim)

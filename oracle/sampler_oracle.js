@@ -13,6 +13,7 @@
  *   sampleRow        encodeSampling (src/engine/forward.ts:522-601) + sampleFromTopK, with
  *                    topK = 0 meaning the whole vocabulary
  *   softmaxRows      src/reference/cpu.ts:238-264 (f32 = Math.fround)
+ *   matmulQuantized  src/reference/cpu.ts:352-393 (f32 = Math.fround)
  */
 
 class SeededRandom {
@@ -157,4 +158,40 @@ function softmaxRows(x, nRows, rowLen, causalPeriod, causalOffset) {
   return out;
 }
 
-module.exports = { SeededRandom, argmax, topK, sumExp, sampleFromTopK, sampleRow, softmaxRows };
+// y[t, m] = sum_k dequant(w[m, k]) * x[t, k] + bias[m]: per word, an f32 partial sum of its
+// values, scaled by the block's scale and added to the row's f32 accumulator.
+function matmulQuantized(words, scales, x, nTokens, outDim, inDim, bits, blockSize, bias) {
+  const f32 = Math.fround;
+  const perWord = bits === 4 ? 8 : 4;
+  const shift = 32 / perWord;
+  const mask = (1 << shift) - 1;
+  const wordsPerRow = inDim / perWord;
+  const wordsPerBlock = blockSize / perWord;
+  const blocksPerRow = inDim / blockSize;
+  const y = new Float32Array(nTokens * outDim);
+  for (let t = 0; t < nTokens; t++) {
+    const xBase = t * inDim;
+    for (let m = 0; m < outDim; m++) {
+      const wBase = m * wordsPerRow;
+      const sBase = m * blocksPerRow;
+      let acc = 0;
+      for (let w = 0; w < wordsPerRow; w++) {
+        const word = words[wBase + w];
+        const scale = scales[sBase + Math.floor(w / wordsPerBlock)];
+        const k0 = w * perWord;
+        let partial = 0;
+        for (let j = 0; j < perWord; j++) {
+          const raw = (word >>> (j * shift)) & mask;
+          const centred = bits === 4 ? raw - 8 : raw > 127 ? raw - 256 : raw;
+          partial = f32(partial + f32(centred * x[xBase + k0 + j]));
+        }
+        acc = f32(acc + f32(partial * scale));
+      }
+      if (bias) acc = f32(acc + bias[m]);
+      y[t * outDim + m] = acc;
+    }
+  }
+  return y;
+}
+
+module.exports = { SeededRandom, argmax, topK, sumExp, sampleFromTopK, sampleRow, softmaxRows, matmulQuantized };

@@ -386,3 +386,45 @@ void tabby_oracle_softmax_rows(const float *x, float *out, int32_t n_rows, int32
     for (int32_t i = valid; i < row_len; ++i) o[i] = 0.0f;
   }
 }
+
+/*
+ * matmulQuantized, src/reference/cpu.ts:352-393: y[t, m] = sum_k dequant(w[m, k]) * x[t, k]
+ * + bias[m] with block-quantized weights (bits 4: eight values per u32 word, nibble j at bits
+ * 4j, dequant(q) = (q - 8) * scale; bits 8: four signed bytes per word). Each word's partial
+ * sum is taken in f32 over its values in order, then scaled by its block's scale and added to
+ * the row's f32 accumulator -- the reference's order, every step rounded to f32.
+ */
+void tabby_oracle_matmul_quantized(const uint32_t *words, const float *scales, const float *x,
+                                   int32_t n_tokens, int32_t out_dim, int32_t in_dim,
+                                   int32_t bits, int32_t block_size, const float *bias,
+                                   float *y) {
+  const int32_t per_word = bits == 4 ? 8 : 4;
+  const int32_t shift = 32 / per_word;
+  const uint32_t mask = (1u << shift) - 1u;
+  const int32_t words_per_row = in_dim / per_word;
+  const int32_t words_per_block = block_size / per_word;
+  const int32_t blocks_per_row = in_dim / block_size;
+  for (int32_t t = 0; t < n_tokens; ++t) {
+    const float *xt = x + (int64_t)t * in_dim;
+    for (int32_t m = 0; m < out_dim; ++m) {
+      const uint32_t *wrow = words + (int64_t)m * words_per_row;
+      const float *srow = scales + (int64_t)m * blocks_per_row;
+      float acc = 0.0f;
+      for (int32_t w = 0; w < words_per_row; ++w) {
+        const uint32_t word = wrow[w];
+        const float scale = srow[w / words_per_block];
+        const int32_t k0 = w * per_word;
+        float block_sum = 0.0f;
+        for (int32_t lane = 0; lane < per_word; ++lane) {
+          const uint32_t raw = (word >> (lane * shift)) & mask;
+          const int32_t centred = bits == 4 ? (int32_t)raw - 8 : (raw > 127 ? (int32_t)raw - 256 : (int32_t)raw);
+          const float prod = (float)((double)centred * (double)xt[k0 + lane]);
+          block_sum = (float)((double)block_sum + (double)prod);
+        }
+        acc = (float)((double)acc + (double)(float)((double)block_sum * (double)scale));
+      }
+      if (bias) acc = (float)((double)acc + (double)bias[m]);
+      y[(int64_t)t * out_dim + m] = acc;
+    }
+  }
+}

@@ -19,6 +19,8 @@
  *   tabby_oracle_f16_to_f32     <- tests/support.ts:67-74 (exact widening)
  *   tabby_oracle_softmax_rows   <- src/reference/cpu.ts:238-264 (softmaxRows: f32 steps,
  *                                  Math.exp, causal prefix)
+ *   tabby_oracle_matmul_quantized <- src/reference/cpu.ts:352-393 (matmulQuantized: the
+ *                                  lm_head's block-quantized matmul, f32 steps)
  */
 #ifndef TABBY_ORACLE_H
 #define TABBY_ORACLE_H
@@ -79,6 +81,13 @@ int tabby_oracle_sample_batch(const float *logits, int32_t rows, int32_t n,
 /* softmaxRows over [n_rows, row_len] f32; out may equal x. */
 void tabby_oracle_softmax_rows(const float *x, float *out, int32_t n_rows, int32_t row_len,
                                int32_t causal_period, int32_t causal_offset);
+
+/* matmulQuantized over n_tokens rows of x [n_tokens, in_dim]; y [n_tokens, out_dim];
+ * bias may be NULL; bits 4 or 8. */
+void tabby_oracle_matmul_quantized(const uint32_t *words, const float *scales, const float *x,
+                                   int32_t n_tokens, int32_t out_dim, int32_t in_dim,
+                                   int32_t bits, int32_t block_size, const float *bias,
+                                   float *y);
 
 #ifdef __cplusplus
 }

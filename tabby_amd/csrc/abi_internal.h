@@ -33,6 +33,10 @@ struct HandleView {
 };
 int handle_view(const tabby_sampler *h, HandleView *out);
 
+// The int4 lm_head's shape rules (hidden and block_size multiples of 32, block_size dividing
+// hidden); TABBY_EINVAL with a message otherwise.
+int check_q4_shape(int32_t vocab, int32_t hidden, int32_t block);
+
 }  // namespace tabby
 
 #define TABBY_HIP_CHECK(expr)                                            \

@@ -42,6 +42,7 @@
 #include "block_ops.h"
 #include "device_math.h"
 #include "loads.h"
+#include "q4_gemv.h"
 #include "seqsum.h"
 #include "wave_ops.h"
 #include "tabby_sampler.h"
@@ -1940,6 +1941,187 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// The lm_head fused with the sampler's first pass (the next step after the sampler in the
+// reference's decode: forward.ts:408-430 writes the logits with the lm_head matmul and
+// encodeSampling re-reads them). Workgroup s takes vocab rows [s * len, s * len + len), one per
+// lane (len = 64 * waves, chosen so that the slices fill the chip: 238 slices of 640 rows for
+// 151,936), computes their logits for every activation row t < R with q4_dot_row (the CPU
+// reference's arithmetic, so these are exactly the logits the unfused product writes), and
+// turns them straight into slice s of sampled row t as wave_kernel leaves a slice for the
+// merge: the slice max, the slice's sum of exp(x - max), and its top min(k, 64) composites
+// (value key, ~id), sorted. The logits never reach HBM; the weights are read once for all R
+// rows. Pools of at most 64 only (the reference's bound, forward.ts:348-351): a row with a
+// larger or whole-vocabulary pool gets TABBY_EINVAL from the merge.
+// ---------------------------------------------------------------------------------------
+constexpr int kLhMaxWaves = 16;
+constexpr int kLhMaxRows = 8;
+constexpr int kLhKcap = kWaveSize;
+
+template <int R>
+__global__ __launch_bounds__(kLhMaxWaves *kWaveSize) void lmhead_slice_kernel(Launch L, Workspace W, Q4Matrix Q,
+                                                                              const float *x) {
+  __shared__ uint64_t lists[kLhMaxWaves][kWaveSize];
+  __shared__ float wmax[kLhMaxWaves];
+  __shared__ double wsum[kLhMaxWaves];
+  const int slice = (int)blockIdx.x;
+  const int nw = (int)(blockDim.x / kWaveSize);
+  const int w = wave_id(), lane = wave_lane();
+  const int r = slice * L.slice_len + (int)threadIdx.x;
+  const bool in = r < Q.vocab;
+  const int n = min(L.slice_len, Q.vocab - slice * L.slice_len);  // rows of this slice
+  // The merge tree below always pairs 16 lists: those of absent waves stay empty.
+  for (int i = (int)threadIdx.x; i < (kLhMaxWaves - nw) * kWaveSize; i += (int)blockDim.x)
+    lists[nw + i / kWaveSize][i % kWaveSize] = 0ull;
+  float logit[R];
+  if (in) q4_dot_row<R>(Q, x, r, logit);
+#pragma unroll
+  for (int t = 0; t < R; ++t) {
+    const tabby_row_params P = L.params[t];
+    const bool valid = params_valid(P, L.k_max);
+    const int keff = effective_k(P, L.vocab);
+    const int kk = valid && keff <= kLhKcap ? min(keff, n) : 0;
+    const float v = in ? logit[t] : -INFINITY;
+    // Slice max, then the sum of 2^(x*L - ml) against ml = fl(max*L), rebased exactly on the
+    // max at the end (rebase_sum): the sum's accuracy does not depend on where the logits sit.
+    const float m = wave_max(v);
+    if (lane == 0) wmax[w] = m;
+    // The slice's candidates: each wave's 64 composites sorted, then merged pairwise.
+    uint64_t c[1] = {in ? composite(key_of(v), (uint32_t)r) : 0ull};
+    wave_sort_desc<1>(c);
+    lists[w][lane] = c[0];
+    __syncthreads();
+    float M = wmax[0];
+    for (int i = 1; i < nw; ++i) M = fmaxf(M, wmax[i]);
+    const float ml = M * kLog2e;
+    const double term = in && M != -INFINITY ? (double)__builtin_amdgcn_exp2f(fmaf(v, kLog2e, -ml)) : 0.0;
+    const double ws = wave_sum(term);
+    if (lane == 0) wsum[w] = ws;
+#pragma unroll
+    for (int half = kLhMaxWaves / 2; half > 0; half >>= 1) {
+      if (w < half) {
+        // Top 64 of two descending lists: the larger of a[i] and b[63 - i] is a bitonic
+        // sequence holding them; a bitonic clean sorts it.
+        uint64_t a[1] = {tmax(lists[w][lane], lists[w + half][kWaveSize - 1 - lane])};
+        wave_bitonic_stages<1>(a, 0, kWaveSize);
+        wave_lds_sync();
+        lists[w][lane] = a[0];
+      }
+      __syncthreads();
+    }
+    if (w == 0) {
+      double S = 0.0;
+      for (int i = 0; i < nw; ++i) S += wsum[i];
+      S = rebase_sum(S, M, ml, M);
+      if (lane < kk) W.cands[(size_t)t * W.row_cand_stride + (size_t)slice * L.list_stride + lane] = lists[0][lane];
+      if (lane == 0) {
+        SliceStat st;
+        st.max = M;
+        st.count = (uint32_t)kk;
+        st.sum = S;
+        W.stats[(size_t)t * kMaxSplits + slice] = st;
+      }
+    }
+    __syncthreads();  // lists and statistics are reused by the next row
+  }
+}
+
+// The merge for the fused path's many slices (up to 256 lists of at most 64, one per slice).
+// A bound first: the K-th largest of the slices' first entries (K distinct elements lie at or
+// above it, so every element of the row's top K does too). Each slice's entries at or above
+// it -- usually its first one or two -- are gathered (at most 256), sorted in registers, and
+// the register tail (reg_tail) samples the row. More than 256 at or above the bound (rows
+// whose top crowds into a few slices, or ties) take the general merge (merge_row).
+struct LhMergeSmem {
+  WaveMergeSmem m;
+  uint64_t heads[kWaves][kWaveSize];
+  uint64_t surv[4 * kWaveSize];
+  BlockScratch bs;
+};
+
+__global__ __launch_bounds__(kBlock) void lmhead_merge_kernel(Launch L, Workspace W) {
+  __shared__ LhMergeSmem sm;
+  const int row = (int)blockIdx.x;
+  const int s = (int)threadIdx.x, w = wave_id(), lane = wave_lane();
+  const tabby_row_params P = L.params[row];
+  const RowPool rp = row_pool(L, P);
+  const SliceStat *stats = W.stats + (size_t)row * kMaxSplits;
+  const RowLists lists{W.cands + (size_t)row * W.row_cand_stride, L.splits, L.list_stride, W.row_cand_stride};
+  const int K = rp.K;
+  if (!(rp.valid && rp.finite && K > 0 && K <= kWaveSize)) {
+    merge_row<float>(sm.m, L, W, row, P, stats, lists);  // statuses of out-of-contract rows
+    return;
+  }
+  const uint64_t *list = lists.base + (size_t)s * L.list_stride;
+  const int cnt = s < L.splits ? (int)stats[s].count : 0;
+  uint64_t h[1] = {cnt > 0 ? list[0] : 0ull};
+  wave_sort_desc<1>(h);
+  sm.heads[w][lane] = h[0];
+  __syncthreads();
+  if (w < 2) {
+    uint64_t a[1] = {tmax(sm.heads[w][lane], sm.heads[w + 2][kWaveSize - 1 - lane])};
+    wave_bitonic_stages<1>(a, 0, kWaveSize);
+    wave_lds_sync();
+    sm.heads[w][lane] = a[0];
+  }
+  __syncthreads();
+  if (w == 0) {
+    uint64_t a[1] = {tmax(sm.heads[0][lane], sm.heads[1][kWaveSize - 1 - lane])};
+    wave_bitonic_stages<1>(a, 0, kWaveSize);
+    wave_lds_sync();
+    sm.heads[0][lane] = a[0];
+  }
+  __syncthreads();
+  const uint64_t theta = sm.heads[0][K - 1];
+  // This slice's entries at or above the bound (its list is sorted): eight loads at a time.
+  int take = 0;
+  for (int base = 0; base < cnt; base += 8) {
+    uint64_t e[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) e[u] = base + u < cnt ? list[base + u] : 0ull;
+    int n8 = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) n8 += (base + u < cnt && e[u] >= theta) ? 1 : 0;
+    take += n8;
+    if (n8 < 8) break;
+  }
+  uint32_t total_u = 0;
+  const uint32_t before = block_exclusive_scan((uint32_t)take, sm.bs, &total_u);
+  const int total = (int)total_u;
+  if (total > 4 * kWaveSize) {
+    merge_row<float>(sm.m, L, W, row, P, stats, lists);
+    return;
+  }
+  for (int i = 0; i < take; ++i) sm.surv[before + i] = list[i];
+  __syncthreads();
+  if (w != 0) return;
+  uint64_t v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = q * kWaveSize + lane < total ? sm.surv[q * kWaveSize + lane] : 0ull;
+  if (total <= kWaveSize) {
+    uint64_t v1[1] = {v[0]};
+    wave_sort_desc<1>(v1);
+    v[0] = v1[0];
+  } else {
+    wave_sort_desc<4>(v);
+  }
+  const RowStats rs = row_stats(stats, L.splits);
+  const float M = rs.max;
+  bool in_domain = (M > -INFINITY) && (M < INFINITY);
+  if (in_domain) {
+    reg_tail<float>(v[0], K, L, row, (const float *)nullptr, M,
+                    [&]() {
+                      in_domain = (rs.sum_exp > 0.0) && (rs.sum_exp < INFINITY);
+                      return rs.sum_exp;
+                    },
+                    P);
+  }
+  if (!in_domain && lane == 0) {
+    write_status(L, row, TABBY_EDOMAIN, M, rs.sum_exp);
+    W.row_state[row].status = TABBY_EDOMAIN;
+  }
+}
+
 // A row (or part of a row) whose pool is at most 64, after its waves' streaming: the waves'
 // lists are unsorted (every entry at or above the row's shared first bound), and the row's top
 // K is selected from their union without sorting them. If the union holds at most 64 entries
@@ -3010,6 +3192,65 @@ int tabby_sampler_sample_device(tabby_sampler *h, const void *logits_dev, int32_
   L.topk_logits = topk_logits_dev;
   HIP_TRY(hipSetDevice(h->device));
   HIP_TRY(dispatch(dtype, p, L, h->ws, h->cus, (hipStream_t)stream));
+  return TABBY_OK;
+}
+
+int tabby_sampler_sample_lmhead_q4_device(tabby_sampler *h, const uint32_t *packed_dev,
+                                          const uint16_t *packed_scales_dev, const float *bias_dev,
+                                          const float *hidden_dev, int32_t rows, int32_t vocab, int32_t hidden,
+                                          int32_t block_size, const tabby_row_params *params_dev,
+                                          tabby_row_result *results_dev, void *stream) {
+  if (!h) return fail(TABBY_EINVAL, "sampler handle is null");
+  if (!packed_dev || !packed_scales_dev || !hidden_dev || !params_dev || !results_dev)
+    return fail(TABBY_EINVAL, "null pointer");
+  int rc = check_q4_shape(vocab, hidden, block_size);
+  if (rc) return rc;
+  if ((uintptr_t)packed_dev % 16 != 0) return fail(TABBY_EINVAL, "packed weights must be 16-byte aligned");
+  if (rows < 1 || rows > std::min(h->rows_max, kLhMaxRows))
+    return fail(TABBY_EINVAL, "rows must be between 1 and " + std::to_string(std::min(h->rows_max, kLhMaxRows)) +
+                                  ", got " + std::to_string(rows));
+  if (vocab > h->vocab_max)
+    return fail(TABBY_EINVAL, "vocab must be at most " + std::to_string(h->vocab_max) + ", got " + std::to_string(vocab));
+  // Slices of 64 * waves rows: one slice for vocabularies up to 1,024; otherwise enough
+  // waves per slice (at least four) that at most 256 slices cover the vocabulary -- about one
+  // per CU (238 slices of 640 rows for 151,936).
+  const int waves = vocab <= kLhMaxWaves * kWaveSize
+                        ? (vocab + kWaveSize - 1) / kWaveSize
+                        : std::max(4, ((vocab + kMaxSplits - 1) / kMaxSplits + kWaveSize - 1) / kWaveSize);
+  const int slice_len = waves * kWaveSize;
+  const int slices = (vocab + slice_len - 1) / slice_len;
+  if ((int64_t)slices * kLhKcap > h->ws.row_cand_stride)
+    return fail(TABBY_ECAPACITY, "the handle's candidate region is too small for this vocab (create it with "
+                                 "vocab_max >= 64)");
+  Launch L{};
+  L.logits = nullptr;  // no logits: top-k lists are not written on this path
+  L.params = params_dev;
+  L.results = results_dev;
+  L.rows = rows;
+  L.vocab = vocab;
+  L.splits = slices;
+  L.slice_len = slice_len;
+  L.list_stride = kLhKcap;
+  L.topk_cap = 0;
+  L.k_max = h->k_max;
+  L.kcap = kLhKcap;
+  L.head_pass = 0;
+  const Q4Matrix Q{packed_dev, packed_scales_dev, bias_dev, vocab, hidden, block_size};
+  const hipStream_t s = (hipStream_t)stream;
+  HIP_TRY(hipSetDevice(h->device));
+  switch (rows) {
+    case 1: hipLaunchKernelGGL(lmhead_slice_kernel<1>, dim3(slices), dim3(slice_len), 0, s, L, h->ws, Q, hidden_dev); break;
+    case 2: hipLaunchKernelGGL(lmhead_slice_kernel<2>, dim3(slices), dim3(slice_len), 0, s, L, h->ws, Q, hidden_dev); break;
+    case 3: hipLaunchKernelGGL(lmhead_slice_kernel<3>, dim3(slices), dim3(slice_len), 0, s, L, h->ws, Q, hidden_dev); break;
+    case 4: hipLaunchKernelGGL(lmhead_slice_kernel<4>, dim3(slices), dim3(slice_len), 0, s, L, h->ws, Q, hidden_dev); break;
+    case 5: hipLaunchKernelGGL(lmhead_slice_kernel<5>, dim3(slices), dim3(slice_len), 0, s, L, h->ws, Q, hidden_dev); break;
+    case 6: hipLaunchKernelGGL(lmhead_slice_kernel<6>, dim3(slices), dim3(slice_len), 0, s, L, h->ws, Q, hidden_dev); break;
+    case 7: hipLaunchKernelGGL(lmhead_slice_kernel<7>, dim3(slices), dim3(slice_len), 0, s, L, h->ws, Q, hidden_dev); break;
+    default: hipLaunchKernelGGL(lmhead_slice_kernel<8>, dim3(slices), dim3(slice_len), 0, s, L, h->ws, Q, hidden_dev); break;
+  }
+  HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL(lmhead_merge_kernel, dim3(rows), dim3(kBlock), 0, s, L, h->ws);
+  HIP_TRY(hipGetLastError());
   return TABBY_OK;
 }
 

@@ -47,7 +47,8 @@ EXPORTED_SYMBOLS = (
     "tabby_sampler_sample", "tabby_last_error", "tabby_version", "tabby_debug_exp",
     "tabby_debug_seq_sum", "tabby_debug_first_above", "tabby_sampler_sample_device_noalloc",
     "tabby_argmax_device", "tabby_softmax_rows_device", "tabby_debug_stream_read",
-    "tabby_debug_exp_f32",
+    "tabby_debug_exp_f32", "tabby_lmhead_q4_pack_device", "tabby_lmhead_q4_device",
+    "tabby_sampler_sample_lmhead_q4_device",
 )
 
 
@@ -85,11 +86,15 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     L.tabby_softmax_rows_device.argtypes = [vp, vp, i32, i32, i32, i32, vp]
     L.tabby_debug_stream_read.argtypes = [vp, i32, i64, vp, vp]
     L.tabby_debug_exp_f32.argtypes = [vp, vp, i64, vp]
+    L.tabby_lmhead_q4_pack_device.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp]
+    L.tabby_lmhead_q4_device.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]
+    L.tabby_sampler_sample_lmhead_q4_device.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp]
     for name in ("tabby_sampler_create", "tabby_sampler_destroy", "tabby_sampler_sample_device",
                  "tabby_sampler_sample", "tabby_debug_exp", "tabby_debug_seq_sum",
                  "tabby_debug_first_above", "tabby_sampler_sample_device_noalloc",
                  "tabby_argmax_device", "tabby_softmax_rows_device", "tabby_debug_stream_read",
-                 "tabby_debug_exp_f32"):
+                 "tabby_debug_exp_f32", "tabby_lmhead_q4_pack_device", "tabby_lmhead_q4_device",
+                 "tabby_sampler_sample_lmhead_q4_device"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -323,6 +328,30 @@ class GpuSampler:
         out = [int(v) for v in ids.cpu().tolist()]
         return out[0] if logits.dim() == 1 else out
 
+    def sample_lmhead_q4_device(self, head: "LmHeadQ4", hidden_states, params_dev, results_dev,
+                                stream=None) -> None:
+        """The lm_head fused with sampling (tabby_sampler_sample_lmhead_q4_device): one call
+        samples each row of ``hidden_states`` (float32 CUDA [rows, hidden], rows <= 8) from the
+        logits ``head`` would produce, without writing them. Asynchronous."""
+        x = hidden_states if hidden_states.dim() == 2 else hidden_states.reshape(1, -1)
+        _check(self._lib.tabby_sampler_sample_lmhead_q4_device(
+            self._h, ctypes.c_void_p(head.packed.data_ptr()), ctypes.c_void_p(head.scales.data_ptr()),
+            ctypes.c_void_p(head.bias.data_ptr()) if head.bias is not None else None,
+            ctypes.c_void_p(x.data_ptr()), int(x.shape[0]), head.vocab, head.hidden, head.block,
+            ctypes.c_void_p(params_dev.data_ptr()), ctypes.c_void_p(results_dev.data_ptr()),
+            self._stream(stream)))
+
+    def sample_lmhead_q4(self, head: "LmHeadQ4", hidden_states, params: np.ndarray, stream=None):
+        """Host-parameter convenience over sample_lmhead_q4_device: returns the results
+        structured array (synchronises)."""
+        import torch
+        x = hidden_states if hidden_states.dim() == 2 else hidden_states.reshape(1, -1)
+        rows = int(x.shape[0])
+        p = torch.from_numpy(np.ascontiguousarray(params, dtype=PARAMS_DTYPE).view(np.uint8).copy()).to(x.device)
+        res = torch.zeros(rows * RESULT_DTYPE.itemsize, dtype=torch.uint8, device=x.device)
+        self.sample_lmhead_q4_device(head, x, p, res, stream=stream)
+        return res.cpu().numpy().view(RESULT_DTYPE)
+
     def sample(self, logits, params: SamplingParams, rng) -> SampleOutcome:
         """One row: sample(logits, {temperature, topK, topP}, rng) -> SampleOutcome."""
         res, _, _ = self.sample_params(logits, make_params(params, 1, rng))
@@ -407,6 +436,46 @@ def softmax_rows(x, n_rows: int, row_len: int, causal_period: int = 0, causal_of
         ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()), int(n_rows), int(row_len),
         int(causal_period), int(causal_offset), GpuSampler._stream(stream)))
     return out
+
+
+class LmHeadQ4:
+    """The lm_head's int4 weights on the device in this library's layout
+    (tabby_lmhead_q4_pack_device), made from the reference's layout: ``words`` u32
+    [vocab, hidden / 8] and ``scales_f16`` f16 bits [vocab, hidden / block] (numpy or CUDA
+    tensors), optional ``bias`` f32 [vocab]."""
+
+    def __init__(self, words, scales_f16, vocab: int, hidden: int, block: int = 32, bias=None,
+                 device: str = "cuda"):
+        import torch
+        w = torch.as_tensor(np.ascontiguousarray(words).view(np.int32) if isinstance(words, np.ndarray)
+                            else words).to(device).contiguous()
+        sc = torch.as_tensor(np.ascontiguousarray(scales_f16).view(np.int16)
+                             if isinstance(scales_f16, np.ndarray) else scales_f16).to(device).contiguous()
+        self.vocab, self.hidden, self.block = int(vocab), int(hidden), int(block)
+        if w.numel() != self.vocab * self.hidden // 8 or sc.numel() != self.vocab * self.hidden // self.block:
+            raise ValueError("words / scales do not match vocab x hidden / block")
+        self.packed = torch.empty_like(w)
+        self.scales = torch.empty_like(sc)
+        self.bias = None if bias is None else torch.as_tensor(np.asarray(bias, np.float32)).to(device).contiguous()
+        _check(load_library().tabby_lmhead_q4_pack_device(
+            ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(sc.data_ptr()), self.vocab, self.hidden,
+            self.block, ctypes.c_void_p(self.packed.data_ptr()), ctypes.c_void_p(self.scales.data_ptr()),
+            GpuSampler._stream(None)))
+
+    def logits(self, hidden_states, out=None, stream=None):
+        """The lm_head matmul (tabby_lmhead_q4_device): float32 CUDA [rows, vocab]."""
+        import torch
+        x = hidden_states if hidden_states.dim() == 2 else hidden_states.reshape(1, -1)
+        if x.dtype != torch.float32 or not x.is_contiguous():
+            raise ValueError("hidden states must be a contiguous float32 tensor")
+        rows = int(x.shape[0])
+        y = out if out is not None else torch.empty((rows, self.vocab), dtype=torch.float32, device=x.device)
+        _check(load_library().tabby_lmhead_q4_device(
+            ctypes.c_void_p(self.packed.data_ptr()), ctypes.c_void_p(self.scales.data_ptr()),
+            ctypes.c_void_p(self.bias.data_ptr()) if self.bias is not None else None,
+            ctypes.c_void_p(x.data_ptr()), rows, self.vocab, self.hidden, self.block,
+            ctypes.c_void_p(y.data_ptr()), GpuSampler._stream(stream)))
+        return y
 
 
 def stream_read(src, sink, stream=None) -> None:

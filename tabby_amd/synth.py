@@ -138,3 +138,55 @@ def random_workload(rows: int, vocab: int, seed: int, k_choices=(1, 5, 40, 64), 
     k = np.asarray(k_choices, dtype=np.int32)[(pick[:, 1] * len(k_choices)).astype(int)]
     p = np.asarray(top_ps, dtype=np.float64)[(pick[:, 2] * len(top_ps)).astype(int)]
     return Workload(f"random{seed}", logits, k, t, p, pick[:, 3].copy())
+
+
+# ---------------------------------------------------------------------------------------
+# The lm_head: int4 block-quantized weights and hidden states (the fused lm_head + sampling
+# path). Generated the way the reference's own tests generate them.
+# ---------------------------------------------------------------------------------------
+
+def random_f32(count: int, seed: int, scale: float = 1.0, start: int = 0) -> np.ndarray:
+    """tests/support.ts:19-24 (randomF32): fround((u * 2 - 1) * scale) for draws start.. of
+    SeededRandom(seed)."""
+    u = mulberry32_stream(seed, count, start)
+    return ((u * 2.0 - 1.0) * scale).astype(np.float32)
+
+
+def quantize_q4(values: np.ndarray, rows: int, cols: int, block: int = 32):
+    """tests/quant.test.ts:83-120 (quantizeQ4 + packScalesF16): per block, the value of
+    largest magnitude (the first such) gives scale = peak / -8; levels are
+    clamp(round(v / scale + 8), 0, 15) with JavaScript's Math.round, eight per u32 word
+    (value j at bits 4j); scales are rounded to f16 (round to nearest even).
+    Returns (words u32 [rows * cols / 8], scales_f16 bits u16 [rows * cols / block],
+    scales_f32 (the f16 values widened) [rows * cols / block])."""
+    v = np.asarray(values, np.float32).reshape(rows, cols // block, block).astype(np.float64)
+    first_peak = np.argmax(np.abs(v), axis=2)
+    peak = np.take_along_axis(v, first_peak[..., None], axis=2)[..., 0]
+    scale = peak / -8.0
+    inverse = np.divide(1.0, scale, out=np.zeros_like(scale), where=scale != 0.0)
+    level = np.clip(js_round(v * inverse[..., None] + 8.0), 0, 15).astype(np.uint32).reshape(-1, 8)
+    words = np.zeros(level.shape[0], dtype=np.uint32)
+    for j in range(8):
+        words |= level[:, j] << np.uint32(4 * j)
+    scales_f16 = scale.astype(np.float32).astype(np.float16).reshape(-1)
+    return words, scales_f16.view(np.uint16), scales_f16.astype(np.float32)
+
+
+def lm_head_q4(vocab: int, hidden: int, block: int = 32, seed: int = 7):
+    """A random-init int4 lm_head of vocab x hidden in the reference's layout: every 4-bit
+    code uniform in 0..15 (the words are mulberry32 draws), each block's scale
+    +-(0.04 .. 0.05) / 8 rounded to f16 -- the magnitude quantize_q4 gives weights drawn as
+    the reference's quant test draws them (randomF32 * 0.05). Returns (words u32
+    [vocab * hidden / 8], scales_f16 bits u16 [vocab * hidden / block], scales_f32)."""
+    words = (mulberry32_stream(seed, vocab * hidden // 8) * 4294967296.0).astype(np.uint32)
+    u = mulberry32_stream(seed ^ 0x5CA1E, vocab * hidden // block)
+    mag = (0.04 + 0.01 * u) / 8.0
+    sign = np.where(mulberry32_stream(seed ^ 0x519, u.size) < 0.5, 1.0, -1.0)
+    scales_f16 = (sign * mag).astype(np.float32).astype(np.float16)
+    return words, scales_f16.view(np.uint16), scales_f16.astype(np.float32)
+
+
+def hidden_states(rows: int, hidden: int, seed: int = 0x1234, scale: float = 6.0) -> np.ndarray:
+    """rows x hidden f32 activations, randomF32 * scale (scale 6 puts the lm_head's logits
+    near N(0, 3^2), the spread of the sampler's configurations)."""
+    return random_f32(rows * hidden, seed, scale).reshape(rows, hidden)

@@ -448,3 +448,64 @@ def test_exp_rounded_to_f32_on_hard_arguments(oracle):
     want = np.asarray(d["y_bits"], np.uint32)
     got = oracle.exp_array(x.astype(np.float64)).astype(np.float32).view(np.uint32)
     assert x.size >= 40 and np.array_equal(got, want)
+
+
+# ---- matmulQuantized (src/reference/cpu.ts:352-393) ----------------------------------------
+
+def _dequant_f64(words, scales, out_dim, in_dim, bits, block):
+    per = 8 if bits == 4 else 4
+    shift = 32 // per
+    raw = np.stack([(words >> np.uint32(shift * j)) & np.uint32((1 << shift) - 1) for j in range(per)], 1)
+    raw = raw.reshape(out_dim, in_dim).astype(np.float64)
+    centred = raw - 8 if bits == 4 else np.where(raw > 127, raw - 256, raw)
+    return centred * np.repeat(np.asarray(scales, np.float64).reshape(out_dim, in_dim // block), block, axis=1)
+
+
+def test_matmul_quantized_on_the_reference_test_shapes(oracle):
+    # tests/quant.test.ts:122-177: weights randomF32(rows * cols, seed, 0.05) quantized by
+    # quantizeQ4, f16-rounded scales, x = randomF32(cols, seed ^ 0x1234); the reference
+    # accepts a max abs error of 1e-4 against matmulQuantized. Here: the C restatement and
+    # the Node one (Math.fround) agree bit for bit, and both are within the f32 steps' error
+    # of the f64 product of the dequantized weights.
+    for rows, cols in ((8, 32), (17, 96), (64, 896), (896, 4864)):
+        seed = rows * 31 + cols
+        w = synth.random_f32(rows * cols, seed, 0.05)
+        words, _, scales = synth.quantize_q4(w, rows, cols, 32)
+        x = synth.random_f32(cols, seed ^ 0x1234)
+        y = oracle.matmul_quantized(words, scales, x, rows, cols)
+        if oracle.node_available():
+            yn = oracle.node_matmul_quantized(words, scales, x, rows, cols)
+            assert np.array_equal(y.view(np.uint32), yn.view(np.uint32)), (rows, cols)
+        W = _dequant_f64(words, scales, rows, cols, 4, 32)
+        ref = x.astype(np.float64) @ W.T
+        bound = (np.abs(x.astype(np.float64)) @ np.abs(W).T) * cols * 2.0 ** -23 + 1e-12
+        assert np.all(np.abs(y[0] - ref) <= bound), (rows, cols)
+        assert np.max(np.abs(y[0] - ref)) < 1e-4
+
+
+def test_matmul_quantized_bias_bits8_and_batches(oracle):
+    rng = np.random.default_rng(3)
+    out_dim, in_dim = 40, 128
+    for bits, block in ((4, 32), (4, 64), (8, 32), (8, 128)):
+        words = rng.integers(0, 2 ** 32, out_dim * in_dim * bits // 32, dtype=np.uint64).astype(np.uint32)
+        scales = rng.normal(0, 0.01, out_dim * in_dim // block).astype(np.float16).astype(np.float32)
+        bias = rng.normal(0, 1, out_dim).astype(np.float32)
+        x = rng.normal(0, 2, (3, in_dim)).astype(np.float32)
+        y = oracle.matmul_quantized(words, scales, x, out_dim, in_dim, bits, block, bias)
+        ref = x.astype(np.float64) @ _dequant_f64(words, scales, out_dim, in_dim, bits, block).T + bias
+        assert np.max(np.abs(y - ref)) < 1e-4, (bits, block)
+        if oracle.node_available():
+            yn = oracle.node_matmul_quantized(words, scales, x, out_dim, in_dim, bits, block, bias)
+            assert np.array_equal(y.view(np.uint32), yn.view(np.uint32)), (bits, block)
+
+
+def test_matmul_quantized_closed_form(oracle):
+    # One word of codes 0..7 (values -8..-1) against x = 1..8 and scale 0.5, and one of 8..15
+    # (values 0..7) against x = 1: partial sums are small integers, exact in f32.
+    words = np.array([0x76543210, 0xFEDCBA98, 0x00000000, 0x88888888], np.uint32)
+    scales = np.array([0.5], np.float32)
+    x = np.array([1, 2, 3, 4, 5, 6, 7, 8, 1, 1, 1, 1, 1, 1, 1, 1, 2, 2, 2, 2, 2, 2, 2, 2, 9, 9, 9, 9, 9, 9, 9, 9],
+                 np.float32)
+    y = oracle.matmul_quantized(words, scales, x, 1, 32)
+    # sum((j - 8) * (j + 1)) = -120; sum(j for j in 0..7) = 28; 8 * (-8) * 2 = -128; codes 8 -> 0.
+    assert y.tolist() == [[(-120 + 28 - 128 + 0) * 0.5]]

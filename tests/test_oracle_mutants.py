@@ -49,6 +49,12 @@ MUTANTS = {
                                         "causal_offset + (row % causal_period)"),
     "softmax without the max": ("(float)((double)o[i] - (double)max_v)", "(float)((double)o[i])"),
     "softmax tail not zeroed": ("for (int32_t i = valid; i < row_len; ++i) o[i] = 0.0f;", ""),
+    "q4 offset seven": ("(int32_t)raw - 8 :", "(int32_t)raw - 7 :"),
+    "q4 scale of the wrong block": ("const float scale = srow[w / words_per_block];",
+                                    "const float scale = srow[(w + 1) / words_per_block % blocks_per_row];"),
+    "q4 bias skipped": ("if (bias) acc = (float)((double)acc + (double)bias[m]);", ""),
+    "q4 products not rounded to f32": ("const float prod = (float)((double)centred * (double)xt[k0 + lane]);",
+                                       "const double prod = (double)centred * (double)xt[k0 + lane];"),
     "softmax sum skips the first exp": ("    o[i] = e;\n      sum = (float)((double)sum + (double)e);",
                                         "    o[i] = e;\n      if (i > 0) sum = (float)((double)sum + (double)e);"),
 }
@@ -77,6 +83,9 @@ def _battery(oracle, vectors, fixture):
         lambda: pins.test_softmax_reference_kernel_test_assertions(oracle),
         lambda: pins.test_softmax_rows_match_float64_math(oracle),
         lambda: pins.test_softmax_matches_node_vectors(oracle, pins._load("softmax_vectors.json")),
+        lambda: pins.test_matmul_quantized_closed_form(oracle),
+        lambda: pins.test_matmul_quantized_bias_bits8_and_batches(oracle),
+        lambda: pins.test_matmul_quantized_on_the_reference_test_shapes(oracle),
     ]
     for i, check in enumerate(checks):
         try:
