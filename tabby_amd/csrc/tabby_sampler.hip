@@ -77,21 +77,31 @@ struct RowState {
   uint32_t head_key;  // elements with key >= head_key form the row's head
   double sum_exp;
   int32_t status;
-  uint32_t pad;
+  uint32_t handoff;   // bits 16..: length N of the row's sorted top list in head_sorted (0: none);
+                      // bit 0: head_fast_kernel finished the row
+  double list_sum;    // T > 0: the sequential sum of the list's terms exp((l_i - M)/T)
 };
+
+// Whole-vocabulary rows hand at least this many of their largest composites, sorted, from the
+// merge to head_fast_kernel.
+constexpr int kHeadList = 64;
 
 struct Workspace {
   uint32_t *head_count;     // [rows_cap] head sizes
   SliceStat *stats;         // [rows_cap * kMaxSplits]
   uint64_t *cands;          // [rows_cap * row_cand_stride]
   RowState *row_state;      // [rows_cap]
-  uint64_t *head;           // [head_rows * head_stride] whole-vocabulary rows: the head
+  uint64_t *head;           // [head_rows * head_stride] whole-vocabulary rows: the head, slice s
+                            // of head_kernel at [s * h_slice_len, + head_slice_count)
   uint64_t *head_sorted;    // [head_rows * head_stride] the head, sorted
   double *head_s;           // [head_rows * head_stride] exp((l - max)/T) in sorted order
   double *head_c;           // [head_rows * head_stride] running sums of the weights
   uint32_t *head_plan;      // [head_rows * plan_stride] segment offsets of the sorted head
   double *head_part;        // [head_rows * 2 * (plan_stride - 2)] per-segment exp sums
+  double *head_acc;         // [head_rows * 3 * acc_stride] head_kernel's per-slice ulp counts
+  uint32_t *head_slice_count;  // [head_rows * acc_stride] head entries each slice stored
   int32_t plan_stride;
+  int32_t acc_stride;       // >= the head kernel's slices per row
   int64_t row_cand_stride;  // composites per row in cands
   int32_t head_stride;
 };
@@ -148,13 +158,14 @@ __device__ __forceinline__ bool params_valid(const tabby_row_params &p, int k_ma
 
 // How many of its largest elements a slice keeps as candidates: the row's pool for a row
 // whose pool fits the kernels (keff <= kcap); for a whole-vocabulary row, the top-k list the
-// caller asked for (topk_cap <= k_max <= kcap), which the merge uses to lower the row's head
-// threshold far enough that the head holds that list.
+// caller asked for (topk_cap <= k_max <= kcap) and at least kHeadList, which the merge uses
+// to lower the row's head threshold far enough that the head holds that list, and hands on
+// sorted to head_fast_kernel.
 __device__ __forceinline__ int slice_keep(bool valid, int keff, int n, int kcap, int head_pass,
                                           int topk_cap) {
   if (!valid) return 0;
   if (keff <= kcap) return min(keff, n);
-  return head_pass ? min(topk_cap, n) : 0;
+  return head_pass ? min(max(topk_cap, kHeadList), n) : 0;
 }
 
 // sampleFromTopK (src/engine/sampler.ts:147-212) over the `count` sorted candidates in
@@ -1301,10 +1312,10 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
       rs.max = row_max;
       rs.sum_exp = sum_exp;
       rs.status = TABBY_OK;
-      rs.pad = 0;
+      rs.handoff = 0;
+      rs.list_sum = 0.0;
       rs.head_key = min(head_threshold(row_max, P.temperature), list_key);
       W.row_state[row] = rs;
-      W.head_count[row] = 0u;
     }
     return;
   }
@@ -1688,7 +1699,7 @@ __device__ __forceinline__ RowPool row_pool(const Launch &L, const tabby_row_par
   rp.valid = params_valid(P, L.k_max);
   const int keff = effective_k(P, L.vocab);
   rp.finite = rp.valid && keff <= L.kcap;
-  rp.K = !rp.valid ? 0 : rp.finite ? keff : L.head_pass ? min(L.topk_cap, L.vocab) : 0;
+  rp.K = !rp.valid ? 0 : rp.finite ? keff : L.head_pass ? min(max(L.topk_cap, kHeadList), L.vocab) : 0;
   return rp;
 }
 
@@ -1777,18 +1788,28 @@ __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, 
     return;
   }
   if (!finite) {
-    // Whole-vocabulary row: hand max / sum-exp / the head threshold to the head kernels. The
-    // head also covers the caller's top-k list: sorted[K-1] is its K-th entry.
+    // Whole-vocabulary row: hand max / sum-exp / the head threshold to the head kernels, and
+    // the row's top K, sorted[0..K), to head_kernel and head_fast_kernel. The head also
+    // covers the caller's top-k list, the first topk_cap of them.
+    uint64_t *list = W.head_sorted + (size_t)row * W.head_stride;
+    const double T = P.temperature;
+    for (int i = lane; i < K; i += kWaveSize) {
+      list[i] = sm.sorted[i];
+      if (T > 0.0) sm.b[i] = fdlibm_exp_inline(((double)value_of(composite_key(sm.sorted[i])) - (double)row_max) / T);
+    }
+    wave_lds_sync();
+    const double list_sum = T > 0.0 && K > 0 ? wave_seq_sum(sm.b, K, nullptr, INFINITY).total : 0.0;
     if (lane == 0) {
       RowState st;
       st.max = row_max;
       st.sum_exp = sum_exp;
       st.status = TABBY_OK;
-      st.pad = 0;
-      const uint32_t list_key = K > 0 ? composite_key(sm.sorted[K - 1]) : 0xffffffffu;
+      st.handoff = (uint32_t)K << 16;
+      st.list_sum = list_sum;
+      const int kt = min(L.topk_cap, K);  // the caller's top-k list must lie in the head
+      const uint32_t list_key = kt > 0 ? composite_key(sm.sorted[kt - 1]) : 0xffffffffu;
       st.head_key = min(head_threshold(row_max, P.temperature), list_key);
       W.row_state[row] = st;
-      W.head_count[row] = 0u;
     }
     return;
   }
@@ -2314,23 +2335,58 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
 // or, divided by that total, to a running weight sum (>= the first weight), below half an
 // ulp of either, so it cannot change them (head_threshold). The merge computes head_key, the
 // smallest key with (l - M)/T >= -37.5 in f64 (or the max's key when T <= 0). head_kernel
-// collects the head; the plan, sort and finish kernels sort it and run the tail. poolMass
-// takes the head's terms plus the rest of sum-exp.
+// collects the head; head_fast_kernel finishes the row from the merge's sorted top list when
+// that provably decides it, else the sort and finish kernels sort the head and run the tail
+// (there poolMass takes the head's terms plus the rest of sum-exp).
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ bool is_head_row(const tabby_row_params &P, const Launch &L) {
   return params_valid(P, L.k_max) && effective_k(P, L.vocab) > L.kcap;
 }
 
-// Appends the wave's list to the row's head buffer and empties it.
-__device__ __forceinline__ void flush_head(uint64_t *list, int count, uint32_t *head_count, uint64_t *head) {
-  wave_lds_sync();
-  uint32_t base = 0;
-  if (wave_lane() == 0) base = atomicAdd(head_count, (uint32_t)count);
-  base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
-  for (int i = wave_lane(); i < count; i += kWaveSize) head[base + i] = list[i];
-  wave_lds_sync();
+
+// The whole-vocabulary tail without sorting the head, when that is provably the same.
+// sampleFromTopK over the sorted head needs three sequential f64 sums: the scaled total S and
+// the running sums of w_i = s_i / S up to the cut (s_i = exp((l_i - M)/T), V8's exp). The
+// merge hands over the row's top N sorted (N = max(topk_cap, 64), finish_pool). Once a
+// partial sum P lies in [2^E, 2^(E+1)), adding a term s gives P + u * rint(s / u) exactly
+// (u = 2^(E-52)) unless s / u lies exactly halfway between integers (then the parity of P
+// decides). So if P_N, the sequential sum of the top N, is in binade E, every later term --
+// each smaller than the top N -- adds rint(s / u) ulps whatever the order, provided none ties
+// and the total stays below 2^(E+1), and then S = P_N + u * (sum of rint(s / u) over the
+// rest of the head). head_kernel counts those ulps (and the ties) for the head entries it
+// collects; both conditions are checked exactly (the counts are integers below 2^53, exact
+// in f64 in any order, and a total that reaches 2^53 stays there). A term's s / u comes from
+// the fast exp when it is below 2^36 and at least 2^-9 from a half: exp_nonpos is within 8
+// ulp of e^x and V8's exp within 1, so the two differ by under 9 * 2^-52 * 2^36 < 2^-12
+// there and round alike; other terms take V8's exp. When the running sums also reach the cut
+// within the top N (or the head holds nothing beyond them), head_fast_kernel finishes the
+// row -- bit for bit what the sorted head gives -- and marks it (RowState.handoff bit 0) so
+// that the sort and finish kernels skip it; otherwise it plans the sorted head. (Terms just
+// below P's binade tie often -- s in [2^(E-1), 2^E) has one bit below the ulp -- which is
+// why the top N are summed in order.)
+
+// 2^(52 - E) for P in [2^E, 2^(E+1)): s * ulp_scale(P) is s in ulps of P.
+__device__ __forceinline__ double ulp_scale(double P) {
+  const int E = (int)(((uint64_t)__double_as_longlong(P) >> 52) & 0x7ff) - 1023;
+  return __builtin_ldexp(1.0, 52 - E);
 }
 
+// Adds rint(s / u) for the term of composite v to r, and 1 to ties if s / u is a half-integer.
+__device__ __forceinline__ void add_ulps(uint64_t v, double M, double T, double scale, double &r, double &ties) {
+  const double dt = ((double)value_of(composite_key(v)) - M) / T;
+  double q = exp_nonpos(dt) * scale;
+  if (!(q < 68719476736.0 && __builtin_fabs(q - __builtin_floor(q) - 0.5) > 0x1p-9)) q = fdlibm_exp(dt) * scale;
+  ties += q - __builtin_floor(q) == 0.5 ? 1.0 : 0.0;
+  r += __builtin_rint(q);
+}
+
+// head_kernel's slices: two wave chunks, both loaded before either is used.
+constexpr int kHeadSlice = 2 * kWChunk;
+
+// Collects the head (elements with key >= head_key) of one slice of a row into the row's head
+// buffer and, when the merge handed over the row's top N and T > 0, writes the slice's ulp
+// counts for head_fast_kernel: the sum of rint(s / u) over its head entries below the top N,
+// their number of ties, and their count.
 template <typename In, int VEC>
 __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) {
   __shared__ uint64_t list[kWListCap];
@@ -2340,22 +2396,47 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
   if (!is_head_row(P, L)) return;
   const RowState rs = W.row_state[row];
   if (rs.status != TABBY_OK) return;
-  const int V = L.vocab;
+  const int V = L.vocab, lane = wave_lane();
   const int begin = slice * L.h_slice_len;
   const int n = min(L.h_slice_len, V - begin);
   const int nchunks = (n + kWChunk - 1) / kWChunk;
   const int full_chunks = n / kWChunk;
   const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
   const float hv = value_of(rs.head_key);
-  uint32_t *head_count = W.head_count + row;
-  uint64_t *head = W.head + (size_t)row * W.head_stride;
+  // This slice's part of the head goes to its own range of the row's head buffer (no
+  // atomics: a row's slices appending to one counter serialised on it).
+  uint64_t *head = W.head + (size_t)row * W.head_stride + begin;
+  int stored = 0;
 
-  int count = 0;
   float x[kWChunkPerLane], y[kWChunkPerLane];
-  if (full_chunks > 0) wave_load_full<In, VEC>(src, 0, x); else wave_load<In, VEC>(src, n, 0, x);
+  auto load = [&](int c, float(&dst)[kWChunkPerLane]) {
+    if (c < full_chunks) wave_load_full<In, VEC>(src, c, dst); else wave_load<In, VEC>(src, n, c, dst);
+  };
+  load(0, x);
+  if (nchunks > 1) load(1, y);
+  // The ulp of P_N (the sequential sum of the top N's terms, from the merge).
+  const int N = (int)(rs.handoff >> 16);
+  const double T = P.temperature, M = (double)rs.max;
+  const bool count_ulps = T > 0.0 && N > 0 && N <= kWaveKcap;
+  const double scale = ulp_scale(rs.list_sum);
+  const uint64_t last = count_ulps ? W.head_sorted[(size_t)row * W.head_stride + N - 1] : 0ull;
+  double r = 0.0, ties = 0.0, outside = 0.0;
+  int count = 0;
+  auto flush = [&]() {
+    wave_lds_sync();
+    for (int i = lane; i < count; i += kWaveSize) {
+      const uint64_t v = list[i];
+      head[stored + i] = v;
+      if (count_ulps && v < last) {
+        add_ulps(v, M, T, scale, r, ties);
+        outside += 1.0;
+      }
+    }
+    stored += count;
+    count = 0;
+    wave_lds_sync();
+  };
   for (int c = 0; c < nchunks; ++c) {
-    const int nc = min(c + 1, nchunks - 1);
-    if (nc < full_chunks) wave_load_full<In, VEC>(src, nc, y); else wave_load<In, VEC>(src, n, nc, y);
     if (c >= full_chunks) {
 #pragma unroll
       for (int e = 0; e < kWChunkPerLane; ++e)
@@ -2363,10 +2444,7 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
     }
 #pragma unroll
     for (int e = 0; e < kWChunkPerLane; ++e) {
-      if (count > kWListCap - kWaveSize) {
-        flush_head(list, count, head_count, head);
-        count = 0;
-      }
+      if (count > kWListCap - kWaveSize) flush();
       const bool take = x[e] >= hv;
       const uint64_t mask = __ballot(take);
       if (mask) {
@@ -2374,18 +2452,33 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
         count = __builtin_amdgcn_readfirstlane(count + (int)__popcll(mask));
       }
     }
+    if (c + 1 < nchunks) {
 #pragma unroll
-    for (int e = 0; e < kWChunkPerLane; ++e) x[e] = y[e];
+      for (int e = 0; e < kWChunkPerLane; ++e) x[e] = y[e];
+      if (c + 2 < nchunks) load(c + 2, y);
+    }
   }
-  if (count > 0) flush_head(list, count, head_count, head);
+  if (count > 0) flush();
+  if (lane == 0) W.head_slice_count[(size_t)row * W.acc_stride + slice] = (uint32_t)stored;
+  if (count_ulps) {
+    r = wave_sum(r);  // integers: exact below 2^53, and at least 2^53 once the total is
+    ties = wave_sum(ties);
+    outside = wave_sum(outside);
+    if (lane == 0) {
+      double *acc = W.head_acc + ((size_t)row * W.acc_stride + slice) * 3;
+      acc[0] = r;
+      acc[1] = ties;
+      acc[2] = outside;
+    }
+  }
 }
 
-// The sorted head is built by two kernels. head_plan_kernel (one workgroup per row) bins the
-// head by key into 4096 buckets (bucket = (max_key - key) >> shift, so bucket order is
-// descending key order), scatters it into bucket order, and cuts the bucket sequence into
-// segments: a new segment starts at each bucket whose start offset crosses the next
-// multiple of kSegCap. head_sort_kernel (one workgroup per segment) sorts each segment in
-// place -- in LDS when it fits (at most kSegCap plus one bucket, normally), otherwise by
+// For a row that head_fast_kernel cannot finish, the sorted head is built in two steps.
+// plan_head (that kernel's workgroup for the row) bins the head by key into 4096 buckets
+// (bucket = (max_key - key) >> shift, so bucket order is descending key order), scatters it
+// into bucket order, and cuts the bucket sequence into segments: a new segment starts at each
+// bucket whose start offset crosses the next multiple of kSegCap. head_sort_kernel (one
+// workgroup per segment) sorts each segment in place -- in LDS when it fits (at most kSegCap plus one bucket, normally), otherwise by
 // batches in descending order. The concatenation of the sorted segments is the sorted head.
 // kSegCap leaves room below 1,024 for the bucket that crosses a segment's end, so that a
 // segment is normally sorted as 1,024 entries: at 1,024 segments of 1,025-1,032 entries were
@@ -2400,25 +2493,29 @@ constexpr int kHeadBatch = 4096;
 __host__ __device__ __forceinline__ int plan_slots(int vocab_max) { return vocab_max / kSegCap + 2; }
 
 constexpr int kPlanThreads = 1024;  // a 13 K-entry head took 24.5 us on 256 lanes
+static_assert(kMaxSplits * kChunk <= kPlanThreads * kHeadSlice, "head_fast_kernel takes one slice per thread");
 
 struct PlanSmem {
+  uint32_t starts[kPlanThreads + 1];  // head offset of each head_kernel slice's entries
   uint32_t wave_total[kPlanThreads / kWaveSize];
   uint32_t hist[kHeadBuckets];
   uint32_t start[kHeadBuckets];
 };
 
-__global__ __launch_bounds__(kPlanThreads) void head_plan_kernel(Launch L, Workspace W) {
-  __shared__ PlanSmem sm;
-  const int row = (int)blockIdx.x;
-  uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
-  const tabby_row_params P = L.params[row];
-  const RowState rs = W.row_state[row];
-  if (!is_head_row(P, L) || rs.status != TABBY_OK) {
-    if (threadIdx.x == 0) plan[0] = 0u;
-    return;
-  }
-  const int H = (int)W.head_count[row];
-  const uint64_t *head = W.head + (size_t)row * W.head_stride;
+// The plan of one row's sorted head, by a workgroup of kPlanThreads (head_fast_kernel).
+__device__ __forceinline__ void plan_head(PlanSmem &sm, const Launch &L, const Workspace &W, int row,
+                                          const RowState &rs, uint32_t *plan) {
+  const int H = (int)sm.starts[L.h_splits];
+  const uint64_t *head_base = W.head + (size_t)row * W.head_stride;
+  // Entry i of the head: in the slice s with starts[s] <= i < starts[s + 1].
+  auto head_at = [&](int i) {
+    int lo = 0, hi = L.h_splits;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (sm.starts[mid] <= (uint32_t)i) lo = mid; else hi = mid;
+    }
+    return head_base[(size_t)lo * L.h_slice_len + (uint32_t)i - sm.starts[lo]];
+  };
   uint64_t *sorted = W.head_sorted + (size_t)row * W.head_stride;
   const uint32_t kmax = key_of(rs.max);
   const uint32_t range = kmax - min(rs.head_key, kmax);
@@ -2435,7 +2532,7 @@ __global__ __launch_bounds__(kPlanThreads) void head_plan_kernel(Launch L, Works
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       const int i = base0 + u * kPlanThreads + (int)threadIdx.x;
-      v[u] = i < H ? head[i] : 0ull;
+      v[u] = i < H ? head_at(i) : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < B; ++u)
@@ -2479,7 +2576,7 @@ __global__ __launch_bounds__(kPlanThreads) void head_plan_kernel(Launch L, Works
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       const int i = base0 + u * kPlanThreads + (int)threadIdx.x;
-      v[u] = i < H ? head[i] : 0ull;
+      v[u] = i < H ? head_at(i) : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < B; ++u)
@@ -2493,14 +2590,10 @@ struct SortSmem {
   uint64_t buf[kSegLds];
 };
 
-__global__ __launch_bounds__(kBlock) void head_sort_kernel(Launch L, Workspace W) {
-  __shared__ SortSmem sm;
+// Sorts segment g of a row's plan in place (one workgroup).
+__device__ __forceinline__ void sort_segment(SortSmem &sm, const Launch &L, const Workspace &W, int row, int g,
+                                             int slots, const uint32_t *plan) {
   const int slots_max = W.plan_stride - 2;
-  const int row = (int)blockIdx.x / slots_max;
-  const int g = (int)blockIdx.x - row * slots_max;
-  const uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
-  const int slots = (int)plan[0];
-  if (g >= slots) return;
   const uint32_t lo = plan[2 + g];
   if (lo == ~0u) return;
   const int H = (int)plan[1];
@@ -2596,6 +2689,23 @@ __global__ __launch_bounds__(kBlock) void head_sort_kernel(Launch L, Workspace W
   terms(out);
 }
 
+// Workgroups per row of head_sort_kernel; each sorts every kSortGroups-th segment. (One per
+// segment slot cost 7.5 us on config 4 when no row needed a sort: 171 slots per row, each
+// workgroup reserving 66 KB of LDS.)
+constexpr int kSortGroups = 16;
+
+__global__ __launch_bounds__(kBlock) void head_sort_kernel(Launch L, Workspace W) {
+  __shared__ SortSmem sm;
+  const int row = (int)blockIdx.x / kSortGroups;
+  const int first = (int)blockIdx.x - row * kSortGroups;
+  const uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
+  const int slots = (int)plan[0];
+  for (int g = first; g < slots; g += kSortGroups) {
+    sort_segment(sm, L, W, row, g, slots, plan);
+    __syncthreads();  // sm is reused by the next segment
+  }
+}
+
 // Heads up to this many entries run their sums from LDS (padded, 139 KB of the 160 KB a
 // gfx950 workgroup may use); larger ones from global memory.
 constexpr int kHeadLds = 16384;
@@ -2647,7 +2757,7 @@ __global__ __launch_bounds__(kFinishThreads) void head_finish_kernel(Launch L, W
   const tabby_row_params P = L.params[row];
   if (!is_head_row(P, L)) return;
   const RowState rs = W.row_state[row];
-  if (rs.status != TABBY_OK) return;
+  if (rs.status != TABBY_OK || (rs.handoff & 1u)) return;  // head_fast_kernel finished it
   const int V = L.vocab;
   const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V;
   const int H = (int)W.head_count[row];
@@ -2752,6 +2862,125 @@ __global__ __launch_bounds__(kFinishThreads) void head_finish_kernel(Launch L, W
       L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(V - 1)));
     }
   }
+}
+
+// The fast finish of a whole-vocabulary row (see add_ulps above), by wave 0: true when the
+// row is finished (result and top-k list written, RowState marked).
+struct HeadFastSmem {
+  uint64_t top[kWaveKcap];
+  double s[kWaveKcap];  // s_i = exp((l_i - M) / T) with V8's exp, then w_i = s_i / S
+  double c[kWaveKcap];  // running sums
+  int done;
+};
+
+template <typename In>
+__device__ __forceinline__ bool head_fast_finish(HeadFastSmem &sm, const Launch &L, const Workspace &W, int row,
+                                                 const tabby_row_params &P, const RowState &rs, int H) {
+  const int N = (int)(rs.handoff >> 16);
+  if (N == 0 || N > kWaveKcap) return false;  // no list handed over (pools above 256)
+  const int V = L.vocab, lane = wave_lane();
+  const uint64_t *list = W.head_sorted + (size_t)row * W.head_stride;
+  const double M = (double)rs.max, S1 = rs.sum_exp, T = P.temperature, top_p = P.top_p;
+  for (int i = lane; i < N; i += kWaveSize) {
+    const uint64_t v = list[i];
+    sm.top[i] = v;
+    if (T > 0.0) sm.s[i] = fdlibm_exp(((double)value_of(composite_key(v)) - M) / T);
+  }
+  wave_lds_sync();
+  int chosen = 0, cut = 1;
+  if (T > 0.0) {
+    const double PN = rs.list_sum;
+    // head_kernel's counts over the head entries below the top N, slice by slice.
+    double r = 0.0, ties = 0.0, outside = 0.0;
+    const double *acc = W.head_acc + (size_t)row * W.acc_stride * 3;
+    for (int i = lane; i < L.h_splits; i += kWaveSize) {
+      r += acc[3 * i];
+      ties += acc[3 * i + 1];
+      outside += acc[3 * i + 2];
+    }
+    r = wave_sum(r);
+    ties = wave_sum(ties);
+    outside = wave_sum(outside);
+    const double scale = ulp_scale(PN);
+    const double m = PN * scale;  // P_N in ulps: an integer in [2^52, 2^53)
+    if (ties > 0.0 || m + r >= 9007199254740992.0) return false;
+    const double S = (m + r) / scale;
+    for (int i = lane; i < N; i += kWaveSize) sm.s[i] = sm.s[i] / S;
+    wave_lds_sync();
+    const SeqSum run = wave_seq_sum(sm.s, N, sm.c, top_p < 1.0 ? top_p : INFINITY);
+    const bool reached = top_p < 1.0 && run.total >= top_p;
+    // Without the cut among the top N, the running sums must end there: nothing in the head
+    // beyond them (every smaller term is below half an ulp of every running sum).
+    if (!reached && outside > 0.0) return false;
+    wave_lds_sync();
+    chosen = wave_first_above(sm.c, run.count, P.uniform * run.total);
+    cut = reached ? run.count : V;
+  }
+  if (lane == 0) {
+    tabby_row_result res;
+    res.max_logit = rs.max;
+    res.sum_exp = S1;
+    // The pool is the whole row: poolMass = sum of exp(l_i - M) / sumExp over every element,
+    // 1 up to rounding (a sequential sum of n such terms is within n * 2^-53 of it).
+    res.pool_mass = 1.0;
+    res.status = TABBY_OK;
+    res.topk_count = min(H, L.topk_cap);
+    res.considered = (uint32_t)cut;
+    res.pool_exhausted = 0;  // poolMass 1 is never below top_p
+    res.id = (int32_t)composite_index(sm.top[chosen]);
+    res.probability = fdlibm_exp((double)value_of(composite_key(sm.top[chosen])) - M) / S1;
+    L.results[row] = res;
+    W.row_state[row].handoff = rs.handoff | 1u;
+  }
+  if (L.topk_cap > 0) {
+    // The caller's top-k list: the first topk_cap <= N entries (finish_pool).
+    const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V;
+    const int m = min(H, L.topk_cap);
+    for (int i = lane; i < m; i += kWaveSize) {
+      const uint32_t idx = composite_index(sm.top[i]);
+      L.topk_ids[(size_t)row * L.topk_cap + i] = (int32_t)idx;
+      L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(V - 1)));
+    }
+  }
+  return true;
+}
+
+// One workgroup per whole-vocabulary row: the fast finish (wave 0), else the plan of the
+// sorted head for head_sort_kernel and head_finish_kernel.
+template <typename In>
+__global__ __launch_bounds__(kPlanThreads) void head_fast_kernel(Launch L, Workspace W) {
+  __shared__ PlanSmem psm;
+  __shared__ HeadFastSmem sm;
+  const int row = (int)blockIdx.x;
+  uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
+  const tabby_row_params P = L.params[row];
+  const RowState rs = W.row_state[row];
+  if (!is_head_row(P, L) || rs.status != TABBY_OK) {
+    if (threadIdx.x == 0) plan[0] = 0u;
+    return;
+  }
+  // The head's size and where each slice's entries start (every thread holds one slice).
+  const int ns = L.h_splits;
+  const uint32_t c = (int)threadIdx.x < ns ? W.head_slice_count[(size_t)row * W.acc_stride + threadIdx.x] : 0u;
+  const uint32_t inc = wave_inclusive_scan_u32(c);
+  if (wave_lane() == kWaveSize - 1) psm.wave_total[wave_id()] = inc;
+  __syncthreads();
+  uint32_t below = inc;
+  for (int k = 0; k < wave_id(); ++k) below += psm.wave_total[k];
+  if ((int)threadIdx.x < ns) psm.starts[threadIdx.x + 1] = below;
+  if (threadIdx.x == 0) psm.starts[0] = 0u;
+  __syncthreads();
+  if (threadIdx.x == 0) W.head_count[row] = psm.starts[ns];
+  if (wave_id() == 0) {
+    const bool done = head_fast_finish<In>(sm, L, W, row, P, rs, (int)psm.starts[ns]);
+    if (wave_lane() == 0) sm.done = done ? 1 : 0;
+  }
+  __syncthreads();
+  if (sm.done) {
+    if (threadIdx.x == 0) plan[0] = 0u;
+    return;
+  }
+  plan_head(psm, L, W, row, rs, plan);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2957,9 +3186,8 @@ template <typename In, int VEC>
 hipError_t launch_head(const Launch &L, const Workspace &W, hipStream_t stream) {
   hipLaunchKernelGGL((head_kernel<In, VEC>), dim3((unsigned)(L.rows * L.h_splits)), dim3(kWaveSize), 0,
                      stream, L, W);
-  hipLaunchKernelGGL(head_plan_kernel, dim3((unsigned)L.rows), dim3(kPlanThreads), 0, stream, L, W);
-  hipLaunchKernelGGL(head_sort_kernel, dim3((unsigned)(L.rows * (W.plan_stride - 2))), dim3(kBlock), 0,
-                     stream, L, W);
+  hipLaunchKernelGGL((head_fast_kernel<In>), dim3((unsigned)L.rows), dim3(kPlanThreads), 0, stream, L, W);
+  hipLaunchKernelGGL(head_sort_kernel, dim3((unsigned)(L.rows * kSortGroups)), dim3(kBlock), 0, stream, L, W);
   hipLaunchKernelGGL((head_finish_kernel<In>), dim3((unsigned)L.rows), dim3(kFinishThreads), 0, stream, L, W);
   return hipGetLastError();
 }
@@ -2993,9 +3221,8 @@ Plan plan_launch(int rows, int vocab, int dtype, const void *logits, int k_max, 
   L.k_max = k_max;
   L.kcap = kcap;
   L.head_pass = head_pass ? 1 : 0;
-  const Plan hp = make_plan(rows, vocab, dtype, logits, true);
-  L.h_splits = hp.splits;
-  L.h_slice_len = hp.slice_len;
+  L.h_slice_len = kHeadSlice;
+  L.h_splits = (vocab + kHeadSlice - 1) / kHeadSlice;
   L.parts = 0;
   L.row_waves = 0;
   if (per_row_launch(L, cus)) {
@@ -3169,11 +3396,17 @@ int tabby_sampler_sample_device(tabby_sampler *h, const void *logits_dev, int32_
       const size_t per = (size_t)rows * (size_t)h->vocab_max;
       const int plan_stride = plan_slots(h->vocab_max) + 2;
       const size_t plan_bytes = ((size_t)rows * plan_stride * 4 + 255) & ~(size_t)255;
-      HIP_TRY(hipMalloc(&h->head_base, per * 32 + plan_bytes + (size_t)rows * (plan_stride - 2) * 16));
+      const size_t part_bytes = ((size_t)rows * (plan_stride - 2) * 16 + 255) & ~(size_t)255;
+      const int acc_stride = (h->vocab_max + kHeadSlice - 1) / kHeadSlice;
+      const size_t acc_bytes = (size_t)rows * acc_stride * 24;
+      HIP_TRY(hipMalloc(&h->head_base, per * 32 + plan_bytes + part_bytes + acc_bytes + (size_t)rows * acc_stride * 4));
       char *b = (char *)h->head_base;
       h->ws.head_plan = (uint32_t *)(b + per * 32);
       h->ws.head_part = (double *)(b + per * 32 + plan_bytes);
+      h->ws.head_acc = (double *)(b + per * 32 + plan_bytes + part_bytes);
+      h->ws.head_slice_count = (uint32_t *)(b + per * 32 + plan_bytes + part_bytes + acc_bytes);
       h->ws.plan_stride = plan_stride;
+      h->ws.acc_stride = acc_stride;
       h->ws.head = (uint64_t *)b;
       h->ws.head_sorted = (uint64_t *)(b + per * 8);
       h->ws.head_s = (double *)(b + per * 16);

@@ -248,6 +248,49 @@ def test_full_vocab_mixed_with_finite_rows(oracle):
     compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+@pytest.mark.parametrize("topk_cap", [0, 16])
+def test_full_vocab_fast_finish_edges(oracle, dtype, topk_cap):
+    # Whole-vocabulary rows that the merge's sorted top list may finish (head_fast_kernel) or
+    # must hand to the sorted head: fewer finite entries than the list (the rest -inf), a spike
+    # over a band of ~150 distinct small terms under top-p 0.5 (their ulp counts tie now and
+    # then: the sorted head decides those rows), a plateau whose mass pushes the total past its
+    # binade, and greedy rows.
+    rows, vocab = 32, 30000
+    w = synth.random_workload(rows=rows, vocab=vocab, seed=5150 + topk_cap, k_choices=(0,),
+                              temperatures=(0.7,), top_ps=(0.95,), sigma=2.0)
+    rng = np.random.default_rng(5150)
+    for r in range(rows):
+        kind = r % 4
+        if kind == 0:  # ten finite entries
+            keep = rng.choice(vocab, 10, replace=False)
+            row = np.full(vocab, -np.inf, np.float32)
+            row[keep] = rng.normal(0, 2, 10).astype(np.float32)
+            w.logits[r] = row
+            w.temperature[r], w.top_p[r] = (0.7, 1.0) if r % 8 == 0 else (0.0, 0.9)
+        elif kind == 1:  # spike + band of distinct terms in [2^-8, 2^-7): P_N < 2 with the band
+            row = rng.normal(-20, 1, vocab).astype(np.float32)
+            row[rng.integers(vocab)] = 10.0
+            band = rng.choice(vocab, 150, replace=False)
+            row[band] = (10.0 + rng.uniform(np.log(2.0 ** -8), np.log(2.0 ** -7), 150)).astype(np.float32)
+            w.logits[r] = row
+            w.temperature[r], w.top_p[r] = 1.0, 0.5
+        elif kind == 2:  # a plateau of 3,000 near the max: its mass leaves P_N's binade
+            row = rng.normal(0, 2, vocab).astype(np.float32)
+            row[rng.choice(vocab, 3000, replace=False)] = (12.0 - rng.uniform(0, 0.5, 3000)).astype(np.float32)
+            row[rng.integers(vocab)] = 12.0
+            w.logits[r] = row
+            w.temperature[r], w.top_p[r] = 1.0, 0.05 + 0.1 * (r % 3)
+        else:  # config-4-like spikes, greedy every other row
+            w.temperature[r] = 0.0 if r % 8 == 3 else 0.3
+    w.logits[:] = w.logits.astype(dtype).astype(np.float32)
+    if dtype == np.float16:
+        w.logits = w.logits.astype(np.float16)
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=topk_cap)
+    _log(f"full vocab fast finish {dtype.__name__} cap={topk_cap}",
+         compare(w, res, ids, vals, run_oracle(oracle, w, topk_cap), topk_cap))
+
+
 def test_full_vocab_rejects_list_above_k_max():
     import torch
     x = torch.zeros(1, 5000, device="cuda")
