@@ -84,7 +84,7 @@ struct RowState {
 
 // Whole-vocabulary rows hand at least this many of their largest composites, sorted, from the
 // merge to head_fast_kernel.
-constexpr int kHeadList = 64;
+constexpr int kHeadList = 32;
 
 struct Workspace {
   uint32_t *head_count;     // [rows_cap] head sizes
@@ -2692,7 +2692,7 @@ __device__ __forceinline__ void sort_segment(SortSmem &sm, const Launch &L, cons
 // Workgroups per row of head_sort_kernel; each sorts every kSortGroups-th segment. (One per
 // segment slot cost 7.5 us on config 4 when no row needed a sort: 171 slots per row, each
 // workgroup reserving 66 KB of LDS.)
-constexpr int kSortGroups = 16;
+constexpr int kSortGroups = 8;
 
 __global__ __launch_bounds__(kBlock) void head_sort_kernel(Launch L, Workspace W) {
   __shared__ SortSmem sm;
@@ -2864,8 +2864,9 @@ __global__ __launch_bounds__(kFinishThreads) void head_finish_kernel(Launch L, W
   }
 }
 
-// The fast finish of a whole-vocabulary row (see add_ulps above), by wave 0: true when the
-// row is finished (result and top-k list written, RowState marked).
+// The fast finish of a whole-vocabulary row (see add_ulps above), by wave 0, with the top
+// list already in sm.top and this lane's share of head_kernel's counts (r, ties, outside):
+// true when the row is finished (result and top-k list written, RowState marked).
 struct HeadFastSmem {
   uint64_t top[kWaveKcap];
   double s[kWaveKcap];  // s_i = exp((l_i - M) / T) with V8's exp, then w_i = s_i / S
@@ -2875,29 +2876,18 @@ struct HeadFastSmem {
 
 template <typename In>
 __device__ __forceinline__ bool head_fast_finish(HeadFastSmem &sm, const Launch &L, const Workspace &W, int row,
-                                                 const tabby_row_params &P, const RowState &rs, int H) {
+                                                 const tabby_row_params &P, const RowState &rs, int H, double r,
+                                                 double ties, double outside) {
   const int N = (int)(rs.handoff >> 16);
   if (N == 0 || N > kWaveKcap) return false;  // no list handed over (pools above 256)
   const int V = L.vocab, lane = wave_lane();
-  const uint64_t *list = W.head_sorted + (size_t)row * W.head_stride;
   const double M = (double)rs.max, S1 = rs.sum_exp, T = P.temperature, top_p = P.top_p;
-  for (int i = lane; i < N; i += kWaveSize) {
-    const uint64_t v = list[i];
-    sm.top[i] = v;
-    if (T > 0.0) sm.s[i] = fdlibm_exp(((double)value_of(composite_key(v)) - M) / T);
-  }
-  wave_lds_sync();
   int chosen = 0, cut = 1;
   if (T > 0.0) {
+    for (int i = lane; i < N; i += kWaveSize)
+      sm.s[i] = fdlibm_exp(((double)value_of(composite_key(sm.top[i])) - M) / T);
     const double PN = rs.list_sum;
-    // head_kernel's counts over the head entries below the top N, slice by slice.
-    double r = 0.0, ties = 0.0, outside = 0.0;
-    const double *acc = W.head_acc + (size_t)row * W.acc_stride * 3;
-    for (int i = lane; i < L.h_splits; i += kWaveSize) {
-      r += acc[3 * i];
-      ties += acc[3 * i + 1];
-      outside += acc[3 * i + 2];
-    }
+    // head_kernel's counts over the head entries below the top N.
     r = wave_sum(r);
     ties = wave_sum(ties);
     outside = wave_sum(outside);
@@ -2959,6 +2949,22 @@ __global__ __launch_bounds__(kPlanThreads) void head_fast_kernel(Launch L, Works
     if (threadIdx.x == 0) plan[0] = 0u;
     return;
   }
+  // Wave 0 starts the fast finish's loads -- the top list and head_kernel's counts, slice by
+  // slice -- before the scan below.
+  const int N = (int)(rs.handoff >> 16);
+  double r = 0.0, ties = 0.0, outside = 0.0;
+  if (wave_id() == 0 && N > 0 && N <= kWaveKcap) {
+    const uint64_t *list = W.head_sorted + (size_t)row * W.head_stride;
+    for (int i = wave_lane(); i < N; i += kWaveSize) sm.top[i] = list[i];
+    if (P.temperature > 0.0) {
+      const double *acc = W.head_acc + (size_t)row * W.acc_stride * 3;
+      for (int i = wave_lane(); i < L.h_splits; i += kWaveSize) {
+        r += acc[3 * i];
+        ties += acc[3 * i + 1];
+        outside += acc[3 * i + 2];
+      }
+    }
+  }
   // The head's size and where each slice's entries start (every thread holds one slice).
   const int ns = L.h_splits;
   const uint32_t c = (int)threadIdx.x < ns ? W.head_slice_count[(size_t)row * W.acc_stride + threadIdx.x] : 0u;
@@ -2972,7 +2978,7 @@ __global__ __launch_bounds__(kPlanThreads) void head_fast_kernel(Launch L, Works
   __syncthreads();
   if (threadIdx.x == 0) W.head_count[row] = psm.starts[ns];
   if (wave_id() == 0) {
-    const bool done = head_fast_finish<In>(sm, L, W, row, P, rs, (int)psm.starts[ns]);
+    const bool done = head_fast_finish<In>(sm, L, W, row, P, rs, (int)psm.starts[ns], r, ties, outside);
     if (wave_lane() == 0) sm.done = done ? 1 : 0;
   }
   __syncthreads();
