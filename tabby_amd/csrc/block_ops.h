@@ -19,13 +19,16 @@ constexpr int kBins = 2048;  // 11-bit radix digits
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
-// LDS words the helpers below communicate through. One per workgroup.
-struct BlockScratch {
-  float f[kWaves];
-  double d[kWaves];
-  uint32_t u[kWaves];
+// LDS words the helpers below communicate through. One per workgroup of NW waves; the
+// helpers take the workgroup's size from it (kBlock lanes unless stated).
+template <int NW>
+struct BlockScratchT {
+  float f[NW];
+  double d[NW];
+  uint32_t u[NW];
   uint32_t bin, above, count, slot;
 };
+using BlockScratch = BlockScratchT<kWaves>;
 
 __device__ __forceinline__ float block_max(float v, BlockScratch &s) {
   v = wave_max(v);
@@ -51,7 +54,8 @@ __device__ __forceinline__ double block_sum(double v, BlockScratch &s) {
 }
 
 // Exclusive prefix sum in thread order; *total receives the workgroup sum.
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, BlockScratch &s,
+template <int NW>
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, BlockScratchT<NW> &s,
                                                          uint32_t *total) {
   const int lane = lane_id();
   const uint32_t inc = wave_inclusive_scan_u32(v);
@@ -60,7 +64,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, BlockScratc
   __syncthreads();
   uint32_t base = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < kWaves; ++i) {
+  for (int i = 0; i < NW; ++i) {
     const uint32_t w = s.u[i];
     base += (i < wave_id()) ? w : 0u;
     tot += w;
@@ -73,8 +77,9 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, BlockScratc
 // from the top: above(b) < need <= above(b) + hist[b]. Thread t owns the PER bins just
 // below kBins - t*PER, so thread order is descending bin order. Publishes b, above(b) and
 // hist[b] in s.bin / s.above / s.count.
-__device__ __forceinline__ void find_bin(const uint32_t *hist, uint32_t need, BlockScratch &s) {
-  constexpr int PER = kBins / kBlock;
+template <int NW>
+__device__ __forceinline__ void find_bin(const uint32_t *hist, uint32_t need, BlockScratchT<NW> &s) {
+  constexpr int PER = kBins / (NW * 64);
   const int top = kBins - 1 - (int)threadIdx.x * PER;
   uint32_t c[PER];
   uint32_t sum = 0;
@@ -118,15 +123,15 @@ __device__ __forceinline__ int digit_shift(int pass) {
 
 // max_passes < 6 stops early: the result then only bounds the need-th largest from below
 // (every selected element is still >= prefix, and at least `need` elements are selected).
-template <class ForEach>
+template <int NW, class ForEach>
 __device__ __forceinline__ SelectResult radix_select(ForEach for_each, uint32_t need, uint32_t *hist,
-                                     BlockScratch &s, int max_passes = 6) {
+                                     BlockScratchT<NW> &s, int max_passes = 6) {
   uint64_t prefix = 0;
   int done = 64;
   for (int pass = 0; pass < max_passes; ++pass) {
     const int shift = digit_shift(pass);
     const uint32_t dmask = (pass == 2 || pass == 5) ? 0x3ffu : 0x7ffu;
-    for (int i = threadIdx.x; i < kBins; i += kBlock) hist[i] = 0u;
+    for (int i = threadIdx.x; i < kBins; i += NW * 64) hist[i] = 0u;
     __syncthreads();
     const bool first = pass == 0;
     const int cmp_shift = first ? 0 : done;

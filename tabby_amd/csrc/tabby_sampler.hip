@@ -125,6 +125,7 @@ struct Launch {
   int32_t parts;      // row_kernel: 1 = one workgroup per row; > 1 = workgroups per row (each
                       // a part of slice_len elements, finished by wave_merge_kernel); 0 = unused
   int32_t row_waves;  // row_kernel: waves per workgroup
+  int32_t pool_rows;  // 1: pool_row_kernel streams each row (pools above 256, rows >= CUs)
   int32_t list_stride;  // pools <= 256: entries between the sorted lists of consecutive slices
                         // (or parts) of a row in cands -- slice_len, or kWaveKcap when the
                         // lists are packed (a list never holds more than the pool)
@@ -174,10 +175,126 @@ __device__ __forceinline__ int slice_keep(bool valid, int keff, int n, int kcap,
 // f64 sum on lane 0. The running sums of the draw (sampler.ts:195-203) are the same
 // numbers as the top-p cumulative sums (sampler.ts:178-185), and `total` (:191-192) is the
 // last of them, so lane 0 computes that sequence once and keeps it.
+// The first index in [0, n) (n <= kBlock * PER; thread t holds entries PER*t .. PER*t + PER - 1)
+// for which pred holds, or n: a workgroup minimum through sm.bs.slot.
+template <int PER, class Smem, class Pred>
+__device__ __forceinline__ int block_first(Smem &sm, int n, Pred pred) {
+  if (threadIdx.x == 0) sm.bs.slot = (uint32_t)n;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = (int)threadIdx.x * PER + j;
+    if (i < n && pred(i, j)) {
+      atomicMin(&sm.bs.slot, (uint32_t)i);
+      break;
+    }
+  }
+  __syncthreads();
+  const int r = (int)sm.bs.slot;
+  __syncthreads();
+  return r;
+}
+
+// The fast form of finish_row for pools of 257..KCAP (as reg_tail for pools up to 64): terms
+// from exp_nonpos (within 8 ulp of exp), the scaled total a workgroup sum and the running sums
+// a workgroup scan (thread t holds consecutive entries; each partial sum a tree of at most 12
+// roundings). Against the reference's sequential sums of its exact terms -- whose own rounding
+// is at most n * 2^-53 relative -- the running sums then differ by less than 2^-42 of their
+// value for n <= 1024, so when every comparison that decides the cut and the draw clears its
+// threshold by more than 2^-36 relative, the reference decides the same way: returns true with
+// the result written. Otherwise (or for a greedy row) returns false and finish_row computes the
+// row bit for bit. poolMass and the probability (compared within 1e-5) take the fast terms.
+template <int KCAP, typename In, class Smem>
+__device__ bool finish_row_fast(Smem &sm, const Launch &L, int row, const In *row_src, int count,
+                                float max_logit, double sum_exp, const tabby_row_params &P) {
+  constexpr int PER = KCAP / kBlock;
+  const double T = P.temperature, top_p = P.top_p;
+  if (!(T > 0.0)) return false;
+  double *run = sm.u.tail.w;  // running sums, by index
+  double e[PER], s[PER], e_sum = 0.0, s_sum = 0.0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = (int)threadIdx.x * PER + j;
+    const bool in = i < count;
+    const double d = in ? (double)value_of(composite_key(sm.sorted[i])) - (double)max_logit : 0.0;
+    e[j] = in ? exp_nonpos(d) : 0.0;
+    s[j] = !in ? 0.0 : T == 1.0 ? e[j] : exp_nonpos(d / T);
+    e_sum += e[j];
+    s_sum += s[j];
+  }
+  const double pool = block_sum(e_sum, sm.bs) / sum_exp;
+  const double scaled = block_sum(s_sum, sm.bs);
+  // Running sums: within the thread, then across lanes and waves.
+  double c[PER], acc = 0.0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    acc += s[j] / scaled;
+    c[j] = acc;
+  }
+  const double incl = wave_inclusive_scan(acc);
+  __syncthreads();
+  if (lane_id() == kWaveSize - 1) sm.bs.d[wave_id()] = incl;
+  __syncthreads();
+  double base = incl - acc;
+  for (int k = 0; k < wave_id(); ++k) base += sm.bs.d[k];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = (int)threadIdx.x * PER + j;
+    if (i < count) run[i] = base + c[j];
+  }
+  __syncthreads();
+  const int cut_at = top_p < 1.0 ? block_first<PER>(sm, count, [&](int i, int j) { return base + c[j] >= top_p; }) : count;
+  const int cut = cut_at < count ? cut_at + 1 : count;
+  const double total = run[cut - 1];
+  const double target = P.uniform * total;
+  const int hit = block_first<PER>(sm, cut, [&](int i, int j) { return target < base + c[j]; });
+  const int chosen = hit < cut ? hit : cut - 1;
+  // Margins of every comparison that fixed the cut and the draw (running sums are
+  // non-decreasing, so the neighbours of each boundary are the only ones to check).
+  constexpr double kMargin = 1.0 / 68719476736.0;  // 2^-36
+  bool clear = true;
+  if (top_p < 1.0) {
+    const double m = kMargin * top_p;
+    const double r_cut = run[cut - 1], r_before = cut >= 2 ? run[cut - 2] : 0.0;
+    clear = (cut < count || r_cut < top_p - m) &&
+            (cut == count || (r_cut >= top_p + m && (cut == 1 || r_before < top_p - m)));
+  }
+  const double m2 = kMargin * total;
+  clear = clear && run[chosen] > target + m2 && (chosen == 0 || run[chosen - 1] < target - m2);
+  if (!clear) {
+    __syncthreads();  // finish_row reuses the arrays
+    return false;
+  }
+  const uint64_t cv = sm.sorted[chosen];
+  if (threadIdx.x == 0) {
+    tabby_row_result r;
+    r.max_logit = max_logit;
+    r.sum_exp = sum_exp;
+    r.pool_mass = pool;
+    r.status = TABBY_OK;
+    r.topk_count = min(count, L.topk_cap);
+    r.considered = (uint32_t)cut;
+    r.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
+    r.id = (int32_t)composite_index(cv);
+    r.probability = exp_nonpos((double)value_of(composite_key(cv)) - (double)max_logit) / sum_exp;
+    L.results[row] = r;
+  }
+  if (L.topk_cap > 0) {
+    const int m = min(count, L.topk_cap);
+    for (int i = threadIdx.x; i < m; i += kBlock) {
+      const uint32_t idx = composite_index(sm.sorted[i]);
+      L.topk_ids[(size_t)row * L.topk_cap + i] = (int32_t)idx;
+      L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(L.vocab - 1)));
+    }
+  }
+  return true;
+}
+
 template <int KCAP, typename In, class Smem>
 __device__ void finish_row(Smem &sm, const Launch &L, int row, const In *row_src,
                            int count, float max_logit, double sum_exp,
                            const tabby_row_params &P) {
+  if (finish_row_fast<KCAP, In>(sm, L, row, row_src, count, max_logit, sum_exp, P)) return;
   const double T = P.temperature;
   double *exact = sm.u.tail.exact;
   double *w = sm.u.tail.w;
@@ -392,9 +509,9 @@ __device__ __forceinline__ void write_status(const Launch &L, int row, int32_t s
 // HBM exactly once, in chunks of 16 elements per lane (4096 per workgroup) with the next
 // chunk's loads in flight while the current one is processed. Per lane it keeps an online
 // max and an f64 sum of exp(x - max). It also collects the slice's candidates: every
-// element >= theta, where theta is the kk-th largest lane maximum (or, for kk > 256, vector
-// maximum) of the first chunk -- a lower bound on the slice's kk-th largest value, since at
-// least kk distinct elements reach it. Candidates go to an LDS list with one atomic per
+// element >= theta, where theta starts at a lower bound on the first chunk's kk-th largest
+// element (a radix select on the top 22 bits of the key) -- so at least kk distinct elements
+// reach it, and it never exceeds the slice's kk-th largest value. Candidates go to an LDS list with one atomic per
 // wave; a list that would overflow is flushed to the slice's region of global memory. The
 // exact selection happens once per row, in the merge.
 //
@@ -426,6 +543,20 @@ __device__ __forceinline__ float theta_of(uint64_t prefix) {
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// This lane's position in a buffer filled through the LDS counter *slot, for lanes that
+// take: one atomic per wave for all of its taking lanes (a counter that every lane
+// increments serialises them -- 4,096 in a row cost a config-5 list prune ~5 us). Callers
+// may be divergent: only active lanes count.
+__device__ __forceinline__ uint32_t wave_slot(bool take, uint32_t *slot) {
+  const uint64_t mask = __ballot(take);
+  if (!mask) return 0u;
+  const int leader = __ffsll((unsigned long long)mask) - 1;
+  uint32_t base = 0u;
+  if ((int)lane_id() == leader) base = atomicAdd(slot, (uint32_t)__popcll(mask));
+  base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
+  return base + lanes_below(mask);
 }
 
 // Raw loads of chunk `chunk` (no masking, so nothing consumes them until the next
@@ -495,7 +626,9 @@ __device__ __forceinline__ uint32_t prune_list(SliceSmem &sm, uint32_t have, uin
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const uint32_t i = (uint32_t)(q * kBlock) + threadIdx.x;
-    if (i < have && composite_key(v[q]) >= key) sm.list[atomicAdd(&sm.bs.slot, 1u)] = v[q];
+    const bool keep = i < have && composite_key(v[q]) >= key;
+    const uint32_t at = wave_slot(keep, &sm.bs.slot);
+    if (keep) sm.list[at] = v[q];
   }
   __syncthreads();
   const uint32_t kept = sm.bs.slot;
@@ -568,7 +701,8 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
 
     if (kk > 0) {
       if (c == 0 && kk < min(n, kChunk)) {
-        // theta: the exact kk-th largest element of the first chunk (its padding excluded).
+        // theta: a lower bound on the kk-th largest element of the first chunk (its padding
+        // excluded).
         auto elems = [&](auto &&f) {
 #pragma unroll
           for (int e = 0; e < kChunkPerLane; ++e) {
@@ -576,7 +710,9 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
             if (local < n) f(composite(key_of(x[e]), (uint32_t)local));
           }
         };
-        const SelectResult r = radix_select(elems, (uint32_t)kk, sm.hist, sm.bs);
+        // Two passes: the top 22 bits of the key. The bin's lower edge still has kk
+        // elements at or above it (ties on the key would need the index digits).
+        const SelectResult r = radix_select(elems, (uint32_t)kk, sm.hist, sm.bs, 2);
         if (threadIdx.x == 0) sm.theta = theta_of(r.prefix);
         __syncthreads();
       }
@@ -1323,14 +1459,13 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
     if (C > keff) {
       const SelectResult r = radix_select(each, (uint32_t)keff, sm.u.hist, sm.bs);
       each([&](uint64_t v) {
-        if (selected(v, r)) {
-          const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
-          if (at < (uint32_t)keff) sm.sorted[at] = v;
-        }
+        const bool take = selected(v, r);
+        const uint32_t at = wave_slot(take, &sm.bs.slot);
+        if (take && at < (uint32_t)keff) sm.sorted[at] = v;
       });
     } else {
       each([&](uint64_t v) {
-        const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
+        const uint32_t at = wave_slot(true, &sm.bs.slot);
         if (at < (uint32_t)keff) sm.sorted[at] = v;
       });
     }
@@ -2665,14 +2800,13 @@ __device__ __forceinline__ void sort_segment(SortSmem &sm, const Launch &L, cons
     if (n - pos > b) {
       const SelectResult r = radix_select(below, (uint32_t)b, sm.hist, sm.bs);
       below([&](uint64_t v) {
-        if (selected(v, r)) {
-          const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
-          if (at < (uint32_t)b) sm.buf[at] = v;
-        }
+        const bool take = selected(v, r);
+        const uint32_t at = wave_slot(take, &sm.bs.slot);
+        if (take && at < (uint32_t)b) sm.buf[at] = v;
       });
     } else {
       below([&](uint64_t v) {
-        const uint32_t at = atomicAdd(&sm.bs.slot, 1u);
+        const uint32_t at = wave_slot(true, &sm.bs.slot);
         if (at < (uint32_t)b) sm.buf[at] = v;
       });
     }
@@ -3170,6 +3304,204 @@ int row_parts(int rows, int vocab, int cus, int &part_len) {
   return (vocab + part_len - 1) / part_len;
 }
 
+// ---------------------------------------------------------------------------------------
+// Pools of 257..1024 (k_max > 256) in batches of at least as many rows as CUs: one 16-wave
+// workgroup per row streams it as row_kernel does (each wave's first chunk, then chunks
+// claimed from an LDS counter) with the lane max and sum-exp, and appends every element at
+// or above the row's first bound to one LDS list shared by its waves: a wave reserves room
+// for a chunk's candidates with one LDS atomic, with no barrier, and past kPoolListCap
+// entries they go to the row's region of global memory. The first bound: the maxima of four
+// groups of eight elements of each lane's first two chunks are 4,096 distinct elements; the
+// kk-th largest of their keys (its top 22 bits: a lower bound) has kk elements at or above
+// it, so it never exceeds the row's kk-th largest. (The 4-wave slice kernel started from
+// the first chunk's kk-th largest -- a quarter of that chunk at kk = 1,024 -- and pruned its
+// list with two workgroup barriers per chunk: config 5 took 135 us there.) At the end the
+// workgroup selects the row's exact top kk from the list (radix select over composites) and
+// writes it, unsorted, with the row's statistics, as slice 0 for merge_kernel.
+// ---------------------------------------------------------------------------------------
+constexpr int kPoolWaves = 16;
+constexpr int kPoolThreads = kPoolWaves * kWaveSize;
+constexpr int kPoolListCap = 8192;
+constexpr int kPoolBoundKeys = 4 * kPoolThreads;
+
+struct PoolSmem {
+  union {
+    uint64_t list[kPoolListCap];
+    uint32_t keys[kPoolBoundKeys];  // the first bound's keys, before anything is appended
+  } u;
+  uint32_t hist[kBins];
+  SliceStat stats[kPoolWaves];
+  BlockScratchT<kPoolWaves> bs;
+  uint32_t count;
+  int next_chunk;
+};
+
+// Two workgroups per CU (74 KB of LDS and at most 64 VGPRs each): one's bound and selection
+// overlap the other's streaming, and 512 rows run in one round.
+template <typename In, int VEC>
+__global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Workspace W) {
+  __shared__ PoolSmem sm;
+  const int row = (int)blockIdx.x;
+  const int w = wave_id(), lane = wave_lane();
+  const tabby_row_params P = L.params[row];
+  const int n = L.vocab;
+  const int nchunks = (n + kWChunk - 1) / kWChunk;
+  const int full_chunks = n / kWChunk;
+  const bool valid_params = params_valid(P, L.k_max);
+  const int keff = effective_k(P, n);
+  const int kk = slice_keep(valid_params, keff, n, L.kcap, L.head_pass, L.topk_cap);
+  const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * n;
+  uint64_t *region = W.cands + (size_t)row * W.row_cand_stride;
+  if (threadIdx.x == 0) {
+    sm.next_chunk = kPoolWaves;
+    sm.count = 0u;
+  }
+  __syncthreads();
+  auto load = [&](int c, float(&v)[kWChunkPerLane]) {
+    if (c < full_chunks) wave_load_full<In, VEC>(src, c, v);
+    else if (c < nchunks) wave_load<In, VEC>(src, n, c, v);
+  };
+  auto claim = [&]() {
+    int c = 0;
+    if (lane == 0) c = atomicAdd(&sm.next_chunk, 1);
+    return __builtin_amdgcn_readfirstlane(c);
+  };
+  // Elements past the row's end (or a chunk past its last) become -inf for the statistics.
+  auto mask_tail = [&](int c, float(&v)[kWChunkPerLane]) {
+    if (c >= full_chunks) {
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e)
+        if (wave_local<VEC>(c, e) >= n) v[e] = -INFINITY;
+    }
+  };
+  float x[kWChunkPerLane], y[kWChunkPerLane];
+  const int a = w;
+  load(a, x);
+  int b = claim();
+  load(b, y);
+  mask_tail(a, x);
+  mask_tail(b, y);
+  float theta = -INFINITY;
+  if (kk > 0 && kk < n) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float gm = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) gm = fmaxf(gm, fmaxf(x[4 * g + q], y[4 * g + q]));
+      sm.u.keys[threadIdx.x * 4 + g] = min(max(key_of(gm), kNegInfKey), 0xff800000u);
+    }
+    __syncthreads();
+    auto keys = [&](auto &&f) {
+      for (int i = threadIdx.x; i < kPoolBoundKeys; i += kPoolThreads) f((uint64_t)sm.u.keys[i] << 32);
+    };
+    theta = theta_of(radix_select(keys, (uint32_t)kk, sm.hist, sm.bs, 2).prefix);
+    __syncthreads();  // the keys are read before the list overwrites them
+  }
+
+  float lane_max = -INFINITY;
+  float lane_ml = 0.0f;   // the reference of lane_sum's terms (as in wave_slice)
+  double lane_sum = 0.0;
+  auto step = [&](int c, float(&cur)[kWChunkPerLane]) {
+    mask_tail(c, cur);
+    float cm = cur[0];
+#pragma unroll
+    for (int e = 1; e < kWChunkPerLane; ++e) cm = fmaxf(cm, cur[e]);
+    const float nm = fmaxf(lane_max, cm);
+    if (nm != -INFINITY) {
+      const float ml = nm * kLog2e;
+      float t[kWChunkPerLane];
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e) t[e] = __builtin_amdgcn_exp2f(fmaf(cur[e], kLog2e, -ml));
+#pragma unroll
+      for (int h = kWChunkPerLane / 2; h > 0; h >>= 1) {
+#pragma unroll
+        for (int e = 0; e < h; ++e) t[e] += t[e + h];
+      }
+      const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f(lane_ml - ml);
+      lane_sum = lane_sum * rescale + (double)t[0];
+      lane_max = nm;
+      lane_ml = ml;
+    }
+    if (kk == 0 || !__ballot(cm >= theta)) return;
+    // The chunk's candidates: counted first, then one reservation for the wave.
+    const bool partial = c >= full_chunks;
+    uint64_t masks[kWChunkPerLane];
+    uint32_t total = 0;
+#pragma unroll
+    for (int e = 0; e < kWChunkPerLane; ++e) {
+      masks[e] = __ballot(cur[e] >= theta && (!partial || wave_local<VEC>(c, e) < n));
+      total += (uint32_t)__popcll(masks[e]);
+    }
+    if (total == 0u) return;
+    uint32_t at = 0u;
+    if (lane == 0) at = atomicAdd(&sm.count, total);
+    at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
+#pragma unroll
+    for (int e = 0; e < kWChunkPerLane; ++e) {
+      const uint64_t mask = masks[e];
+      if (mask) {
+        if ((mask >> lane) & 1ull) {
+          const uint32_t pos = at + lanes_below(mask);
+          const uint64_t v = composite(key_of(cur[e]), (uint32_t)wave_local<VEC>(c, e));
+          if (pos < (uint32_t)kPoolListCap) sm.u.list[pos] = v; else region[pos] = v;
+        }
+        at += (uint32_t)__popcll(mask);
+      }
+    }
+  };
+  if (a < nchunks) step(a, x);  // chunk b is already in flight
+  while (b < nchunks) {
+    const int c = claim();
+    load(c, x);
+    step(b, y);
+    if (c >= nchunks) break;
+    b = claim();
+    load(b, y);
+    step(c, x);
+  }
+  const float ms = wave_max(lane_max);
+  const double ss = wave_sum(rebase_sum(lane_sum, lane_max, lane_ml, ms));
+  if (lane == 0) {
+    SliceStat st;
+    st.max = ms;
+    st.count = 0u;
+    st.sum = ss;
+    sm.stats[w] = st;
+  }
+  __syncthreads();
+  // The row's exact top kk of the candidates, unsorted, to region[0 .. kept).
+  const uint32_t C = sm.count;
+  uint32_t kept = 0u;
+  if (kk > 0 && C > (uint32_t)kk) {
+    auto each = [&](auto &&f) {
+      for (uint32_t i = threadIdx.x; i < C; i += kPoolThreads) f(i < (uint32_t)kPoolListCap ? sm.u.list[i] : region[i]);
+    };
+    const SelectResult r = radix_select(each, (uint32_t)kk, sm.hist, sm.bs);
+    if (threadIdx.x == 0) sm.bs.slot = 0u;
+    __syncthreads();
+    // region[0 .. kk) lies below the overflow entries (kk <= 1,024 < kPoolListCap).
+    each([&](uint64_t v) {
+      const bool take = selected(v, r);
+      const uint32_t at = wave_slot(take, &sm.bs.slot);
+      if (take && at < (uint32_t)kk) region[at] = v;
+    });
+    kept = (uint32_t)kk;
+  } else if (kk > 0) {
+    for (uint32_t i = threadIdx.x; i < C; i += kPoolThreads) region[i] = sm.u.list[i];  // C <= kk: in LDS
+    kept = C;
+  }
+  if (w == 0) {
+    const RowStats rs = row_stats(sm.stats, kPoolWaves);
+    if (lane == 0) {
+      SliceStat st;
+      st.max = rs.max;
+      st.count = kept;
+      st.sum = rs.sum_exp;
+      W.stats[(size_t)row * kMaxSplits] = st;
+    }
+  }
+}
+
 template <typename In, int VEC>
 hipError_t launch_pair(const Launch &L, const Workspace &W, int cus, hipStream_t stream) {
   const dim3 slices((unsigned)(L.rows * L.splits)), rows((unsigned)L.rows);
@@ -3181,6 +3513,9 @@ hipError_t launch_pair(const Launch &L, const Workspace &W, int cus, hipStream_t
   } else if (L.kcap <= kWaveKcap) {
     hipLaunchKernelGGL((wave_kernel<In, VEC>), slices, dim3(kWaveSize), 0, stream, L, W);
     hipLaunchKernelGGL((wave_merge_kernel<In>), rows, dim3(kBlock), 0, stream, L, W);
+  } else if (L.pool_rows) {
+    hipLaunchKernelGGL((pool_row_kernel<In, VEC>), rows, dim3(kPoolThreads), 0, stream, L, W);
+    hipLaunchKernelGGL((merge_kernel<kKcapLarge, In>), rows, dim3(kBlock), 0, stream, L, W);
   } else {
     hipLaunchKernelGGL((slice_kernel<In, VEC>), slices, dim3(kBlock), 0, stream, L, W);
     hipLaunchKernelGGL((merge_kernel<kKcapLarge, In>), rows, dim3(kBlock), 0, stream, L, W);
@@ -3231,7 +3566,13 @@ Plan plan_launch(int rows, int vocab, int dtype, const void *logits, int k_max, 
   L.h_splits = (vocab + kHeadSlice - 1) / kHeadSlice;
   L.parts = 0;
   L.row_waves = 0;
-  if (per_row_launch(L, cus)) {
+  L.pool_rows = 0;
+  if (kcap > kWaveKcap && rows >= cus) {
+    // One pool_row_kernel workgroup per row; merge_kernel reads its list as slice 0.
+    L.pool_rows = 1;
+    L.splits = 1;
+    L.slice_len = vocab;
+  } else if (per_row_launch(L, cus)) {
     L.parts = 1;
     L.row_waves = std::max(L.splits, kRowMinWaves);  // at least the five the merge uses
   } else if (kcap <= kWaveKcap) {

@@ -510,6 +510,32 @@ def test_headline_workload_device_form(oracle):
     _log("headline device form", compare(w, res, None, None, run_oracle(oracle, w, 0), 0))
 
 
+def test_exact_boundary_draws_large_pools(oracle):
+    # The same boundaries for pools of 257..1024 (the merge kernel's workgroup tail): equal top
+    # values make every running sum j/K, so top-p and the target sit on them and the fast
+    # sums must hand over to the exact ones; other rows have clear margins.
+    V = 30000
+    rows = 12
+    w = synth.random_workload(rows=rows, vocab=V, seed=977, k_choices=(300,), temperatures=(1.0,),
+                              top_ps=(0.5,), sigma=1.0)
+    for r in range(rows):
+        K = (300, 512, 1024)[r % 3]
+        w.top_k[r] = K
+        if r < 6:
+            w.logits[r, :] = np.minimum(w.logits[r, :], 3.0)
+            pos = (np.arange(K) * 997 + r * 13) % V
+            w.logits[r, pos] = 7.5
+            j = 1 + (r * 37) % (K - 1)
+            w.top_p[r] = j / K
+            w.uniform[r] = ((r * 53) % K) / K
+            w.temperature[r] = (1.0, 0.5, 2.0)[r % 3]
+        else:
+            w.temperature[r] = (0.7, 1.0, 1.5)[r % 3]
+            w.top_p[r] = (0.9, 0.98, 1.0)[(r // 3) % 3]
+    res, ids, vals = run_gpu(w, k_max=1024, topk_cap=32)
+    _log("exact boundaries, large pools", compare(w, res, ids, vals, run_oracle(oracle, w, 32), 32))
+
+
 @pytest.mark.parametrize("rows", [256, 4])
 def test_exact_boundary_draws(oracle, rows):
     # Pools whose running sums land exactly on top-p and on the draw's target: the top K
