@@ -671,10 +671,10 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
   float lane_ml = 0.0f;   // fl(lane_max * L): the reference of lane_sum's terms (rebase_sum)
   double lane_sum = 0.0;  // sum of 2^(x*L - lane_ml) over this lane's elements so far
 
-  float x[kChunkPerLane], y[kChunkPerLane];
-  load_chunk<In, VEC>(src, n, 0, x);
-  for (int c = 0; c < nchunks; ++c) {
-    load_chunk<In, VEC>(src, n, min(c + 1, nchunks - 1), y);  // in flight during this chunk
+  // Chunk c held in x, with the next chunk's loads in flight (issued unconditionally on each
+  // path of the loop below and into their own registers, so the compiler's wait before
+  // chunk c leaves them in flight).
+  auto body = [&](int c, float(&x)[kChunkPerLane]) {
     mask_chunk<VEC>(n, c, x);
 
     // Online max / sum-exp for this lane.
@@ -763,8 +763,22 @@ __global__ __launch_bounds__(kBlock) void slice_kernel(Launch L, Workspace W) {
         if (threadIdx.x == 0) sm.committed = have + incoming;  // read after the next barrier
       }
     }
-#pragma unroll
-    for (int e = 0; e < kChunkPerLane; ++e) x[e] = y[e];
+  };
+  float x[kChunkPerLane], y[kChunkPerLane];
+  load_chunk<In, VEC>(src, n, 0, x);
+  for (int c = 0; c < nchunks; c += 2) {
+    if (c + 1 >= nchunks) {
+      body(c, x);
+      break;
+    }
+    load_chunk<In, VEC>(src, n, c + 1, y);
+    body(c, x);
+    if (c + 2 >= nchunks) {
+      body(c + 1, y);
+      break;
+    }
+    load_chunk<In, VEC>(src, n, c + 2, x);
+    body(c + 1, y);
   }
 
   // Slice statistics (their barriers also publish `committed`).
@@ -831,6 +845,26 @@ __device__ __forceinline__ void wave_load_full(const In *src, int chunk, float (
   for (int j = 0; j < ITEMS; ++j) {
     float v[VEC];
     Loader<In, VEC>::load(base + j * kWaveSize * VEC, v);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) x[j * VEC + c] = v[c];
+  }
+}
+
+// Chunk `chunk` by one code path whatever the chunk: lanes past the slice's end reread its
+// last vector, and a chunk past the last (chunk >= nchunks) loads the slice's first vector
+// into every lane (one line, never used). Branching between wave_load_full and wave_load
+// made the compiler land the loads in temporaries and copy them at once -- waiting for the
+// prefetched chunk right after issuing it.
+template <typename In, int VEC>
+__device__ __forceinline__ void wave_load_any(const In *src, int n, int chunk, int nchunks,
+                                              float (&x)[kWChunkPerLane]) {
+  constexpr int ITEMS = kWChunkPerLane / VEC;
+  const bool live = chunk < nchunks;
+#pragma unroll
+  for (int j = 0; j < ITEMS; ++j) {
+    const int le = chunk * kWChunk + (j * kWaveSize + wave_lane()) * VEC;
+    float v[VEC];
+    Loader<In, VEC>::load(src + (live ? min(le, n - VEC) : 0), v);
 #pragma unroll
     for (int c = 0; c < VEC; ++c) x[j * VEC + c] = v[c];
   }
@@ -1067,12 +1101,11 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
   float theta = -INFINITY;  // == value_of(theta_key)
   uint32_t union_top = kNegInfKey;  // CLAIM: the largest key of the first bound's union
 
-  // Processes chunk c held in `cur` while chunk nc, if any, loads into `nxt`. (A load past
-  // the last chunk would be waited for by the end-of-slice prune.) `first`: the wave's first
-  // chunk.
-  auto step = [&](int c, int nc, bool first, float (&cur)[kWChunkPerLane], float (&nxt)[kWChunkPerLane]) {
-    if (nc < full_chunks) wave_load_full<In, VEC>(src, nc, nxt);
-    else if (nc < nchunks) wave_load<In, VEC>(src, n, nc, nxt);
+  // Processes chunk c held in `cur` (the next chunk's loads are already in flight). `first`:
+  // the wave's first chunk. The loops below issue each load unconditionally on their path,
+  // so that the compiler's wait before a chunk's use leaves the next chunk in flight (a load
+  // that is only conditionally issued makes it wait for every load).
+  auto step = [&](int c, bool first, float (&cur)[kWChunkPerLane]) {
     const bool partial = c >= full_chunks;  // only the slice's last chunk can be partial
     if (partial) {
 #pragma unroll
@@ -1154,11 +1187,9 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
       return __builtin_amdgcn_readfirstlane(c);
     };
     const int a = slice;
-    if (a < full_chunks) wave_load_full<In, VEC>(src, a, x);
-    else if (a < nchunks) wave_load<In, VEC>(src, n, a, x);
+    wave_load_any<In, VEC>(src, n, a, nchunks, x);
     int b = next();
-    if (b < full_chunks) wave_load_full<In, VEC>(src, b, y);
-    else if (b < nchunks) wave_load<In, VEC>(src, n, b, y);
+    wave_load_any<In, VEC>(src, n, b, nchunks, y);
     // The row's first bound, shared by its waves. A wave's 64 lane maxima over its first two
     // chunks are 64 distinct elements of the row; each wave publishes its m largest, and the
     // kk-th largest of the union (waves * m >= kk keys) has kk distinct elements at or above
@@ -1208,19 +1239,39 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
     } else {
       __syncthreads();
     }
-    if (a < nchunks) step(a, nchunks, false, x, y);  // chunk b is already in flight
+    if (a < nchunks) step(a, false, x);  // chunk b is already in flight
+    // y holds chunk b in flight at the top of each iteration.
     while (b < nchunks) {
       const int c = next();
-      step(b, c, false, y, x);
-      if (c >= nchunks) break;
+      if (c >= nchunks) {
+        step(b, false, y);
+        break;
+      }
+      wave_load_any<In, VEC>(src, n, c, nchunks, x);
+      step(b, false, y);
       b = next();
-      step(c, b, false, x, y);
+      if (b >= nchunks) {
+        step(c, false, x);
+        break;
+      }
+      wave_load_any<In, VEC>(src, n, b, nchunks, y);
+      step(c, false, x);
     }
   } else {
-    if (full_chunks > 0) wave_load_full<In, VEC>(src, 0, x); else wave_load<In, VEC>(src, n, 0, x);
+    wave_load_any<In, VEC>(src, n, 0, nchunks, x);
     for (int c = 0; c < nchunks; c += 2) {
-      step(c, c + 1, c == 0, x, y);
-      if (c + 1 < nchunks) step(c + 1, c + 2, false, y, x);
+      if (c + 1 >= nchunks) {
+        step(c, c == 0, x);
+        break;
+      }
+      wave_load_any<In, VEC>(src, n, c + 1, nchunks, y);
+      step(c, c == 0, x);
+      if (c + 2 >= nchunks) {
+        step(c + 1, false, y);
+        break;
+      }
+      wave_load_any<In, VEC>(src, n, c + 2, nchunks, x);
+      step(c + 1, false, y);
     }
   }
 
@@ -2543,12 +2594,10 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
   uint64_t *head = W.head + (size_t)row * W.head_stride + begin;
   int stored = 0;
 
+  // Both chunks' loads at once (a slice's second chunk past the row's end loads a dummy line).
   float x[kWChunkPerLane], y[kWChunkPerLane];
-  auto load = [&](int c, float(&dst)[kWChunkPerLane]) {
-    if (c < full_chunks) wave_load_full<In, VEC>(src, c, dst); else wave_load<In, VEC>(src, n, c, dst);
-  };
-  load(0, x);
-  if (nchunks > 1) load(1, y);
+  wave_load_any<In, VEC>(src, n, 0, nchunks, x);
+  wave_load_any<In, VEC>(src, n, 1, nchunks, y);
   // The ulp of P_N (the sequential sum of the top N's terms, from the merge).
   const int N = (int)(rs.handoff >> 16);
   const double T = P.temperature, M = (double)rs.max;
@@ -2571,28 +2620,26 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
     count = 0;
     wave_lds_sync();
   };
-  for (int c = 0; c < nchunks; ++c) {
+  auto collect = [&](int c, float(&cur)[kWChunkPerLane]) {
     if (c >= full_chunks) {
 #pragma unroll
       for (int e = 0; e < kWChunkPerLane; ++e)
-        if (wave_local<VEC>(c, e) >= n) x[e] = __builtin_nanf("");  // fails x >= hv
+        if (wave_local<VEC>(c, e) >= n) cur[e] = __builtin_nanf("");  // fails cur >= hv
     }
 #pragma unroll
     for (int e = 0; e < kWChunkPerLane; ++e) {
       if (count > kWListCap - kWaveSize) flush();
-      const bool take = x[e] >= hv;
+      const bool take = cur[e] >= hv;
       const uint64_t mask = __ballot(take);
       if (mask) {
-        if (take) list[count + (int)lanes_below(mask)] = composite(key_of(x[e]), (uint32_t)(begin + wave_local<VEC>(c, e)));
+        if (take) list[count + (int)lanes_below(mask)] = composite(key_of(cur[e]), (uint32_t)(begin + wave_local<VEC>(c, e)));
         count = __builtin_amdgcn_readfirstlane(count + (int)__popcll(mask));
       }
     }
-    if (c + 1 < nchunks) {
-#pragma unroll
-      for (int e = 0; e < kWChunkPerLane; ++e) x[e] = y[e];
-      if (c + 2 < nchunks) load(c + 2, y);
-    }
-  }
+  };
+  static_assert(kHeadSlice == 2 * kWChunk, "head_kernel's slices are two chunks");
+  collect(0, x);
+  if (nchunks > 1) collect(1, y);
   if (count > 0) flush();
   if (lane == 0) W.head_slice_count[(size_t)row * W.acc_stride + slice] = (uint32_t)stored;
   if (count_ulps) {
@@ -3423,22 +3470,20 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       lane_ml = ml;
     }
     if (kk == 0 || !__ballot(cm >= theta)) return;
-    // The chunk's candidates: counted first, then one reservation for the wave.
+    // The chunk's candidates: counted first, then one reservation for the wave, then the
+    // same ballots again for the appends (keeping sixteen 64-bit masks live spilled registers).
     const bool partial = c >= full_chunks;
-    uint64_t masks[kWChunkPerLane];
+    auto takes = [&](int e) { return cur[e] >= theta && (!partial || wave_local<VEC>(c, e) < n); };
     uint32_t total = 0;
 #pragma unroll
-    for (int e = 0; e < kWChunkPerLane; ++e) {
-      masks[e] = __ballot(cur[e] >= theta && (!partial || wave_local<VEC>(c, e) < n));
-      total += (uint32_t)__popcll(masks[e]);
-    }
+    for (int e = 0; e < kWChunkPerLane; ++e) total += (uint32_t)__popcll(__ballot(takes(e)));
     if (total == 0u) return;
     uint32_t at = 0u;
     if (lane == 0) at = atomicAdd(&sm.count, total);
     at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
 #pragma unroll
     for (int e = 0; e < kWChunkPerLane; ++e) {
-      const uint64_t mask = masks[e];
+      const uint64_t mask = __ballot(takes(e));
       if (mask) {
         if ((mask >> lane) & 1ull) {
           const uint32_t pos = at + lanes_below(mask);
@@ -3450,6 +3495,8 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     }
   };
   if (a < nchunks) step(a, x);  // chunk b is already in flight
+  // (Unlike row_kernel, the loads stay conditional here: the unconditional form needs more
+  // than the 64 VGPRs that two workgroups per CU leave, and spilled.)
   while (b < nchunks) {
     const int c = claim();
     load(c, x);
