@@ -3211,146 +3211,6 @@ __global__ void exp_kernel(const double *x, double *y, int64_t n) {
   if (i < n) y[i] = fdlibm_exp(x[i]);
 }
 
-}  // namespace tabby
-
-// Scratch of the allocation-free entry (tabby_sampler_sample_device_noalloc), per GPU.
-constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
-static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
-
-// =========================================================================================
-// Host side.
-// =========================================================================================
-using namespace tabby;
-
-struct tabby_sampler {
-  int device = 0;
-  int cus = 0;  // compute units of the device
-  int32_t vocab_max = 0, rows_max = 0, k_max = 0;
-  Workspace ws{};
-  void *ws_base = nullptr;
-  size_t head_rows_cap = 0;  // rows the head buffers are sized for (0: not allocated)
-  void *head_base = nullptr;
-  tabby_row_params *params_dev = nullptr;
-  tabby_row_result *results_dev = nullptr;
-  tabby_row_params *params_pinned = nullptr;
-  tabby_row_result *results_pinned = nullptr;
-  int32_t *topk_ids_dev = nullptr;
-  float *topk_logits_dev = nullptr;
-  size_t topk_elems_cap = 0;
-};
-
-namespace tabby {
-
-thread_local std::string g_last_error;
-
-int record_failure(int status, const std::string &msg) {
-  g_last_error = msg;
-  return status;
-}
-
-int device_cus(int device, int *cus) {
-  static std::mutex mu;
-  static int cached[64] = {0};
-  if (device < 0 || device >= 64) return record_failure(TABBY_EINVAL, "device ordinal out of range");
-  std::lock_guard<std::mutex> lock(mu);
-  if (cached[device] == 0) {
-    int n = 0;
-    const hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
-    if (e != hipSuccess) return record_hip_failure(e, "hipDeviceGetAttribute(multiprocessor count)");
-    cached[device] = n;
-  }
-  *cus = cached[device];
-  return TABBY_OK;
-}
-
-int handle_view(const tabby_sampler *h, HandleView *out) {
-  if (!h) return record_failure(TABBY_EINVAL, "sampler handle is null");
-  out->device = h->device;
-  out->cus = h->cus;
-  out->vocab_max = h->vocab_max;
-  out->rows_max = h->rows_max;
-  out->k_max = h->k_max;
-  out->scratch = h->ws.cands;
-  out->scratch_bytes = (size_t)h->rows_max * (size_t)h->ws.row_cand_stride * sizeof(uint64_t);
-  return TABBY_OK;
-}
-
-}  // namespace tabby
-
-namespace {
-
-int fail(int status, const std::string &msg) { return record_failure(status, msg); }
-
-int hip_fail(hipError_t e, const char *what) {
-  return fail(TABBY_EHIP, std::string(what) + ": " + hipGetErrorString(e));
-}
-
-#define HIP_TRY(expr)                                  \
-  do {                                                 \
-    hipError_t e_ = (expr);                            \
-    if (e_ != hipSuccess) return hip_fail(e_, #expr);  \
-  } while (0)
-
-struct Plan {
-  int slice_len;
-  int splits;
-  int vec;
-};
-
-// Enough slices per row that the batch fills the chip about once: 256 CUs x 3 resident
-// 256-lane workgroups of the slice kernel (its 41.5 KB of LDS leaves room for three; a
-// larger grid ran in two rounds -- config 5, 512 rows: 3 slices per row took 225 us, one
-// 200 us), rounded down, or 256 CUs x 4 SIMDs x 4 one-wave workgroups for the wave kernel
-// (measured at 256 rows: 16 slices per row, 39.9 us per call, beat 12 per row, 41.4 us --
-// the SIMDs issue their oldest wave first and a fourth wave hides more of the others'
-// waits -- and 18 or 20 per row, which no longer fit at once, ~50 us). Each
-// slice is at least one chunk long (two for the wave kernel) and aligned to the vector
-// loads. A row's wave slices are capped at kMaxWaveSplits: with few rows the chip is idle
-// anyway and the latency is one slice's chain plus the merge, whose cost grows with the
-// number of lists (measured on one row: 24 slices of 2048 beat 12 of 4096 and 48 of 1024
-// at vocab 49152; 37 slices of 4096 beat 46 and 74 at vocab 151936).
-constexpr int kTargetGroups = 768;
-constexpr int kTargetWaves = 4096;
-constexpr int kMaxWaveSplits = 36;
-
-Plan make_plan(int rows, int vocab, int dtype, const void *logits, bool wave) {
-  Plan p;
-  const int vec_elems = dtype == TABBY_F32 ? 4 : 8;
-  const bool aligned = ((uintptr_t)logits % 16u) == 0 && vocab % vec_elems == 0;
-  p.vec = aligned ? vec_elems : 1;
-  const int chunk = wave ? 2 * kWChunk : kChunk;
-  const int target = wave ? kTargetWaves : kTargetGroups;
-  const int most = std::min(wave ? kMaxWaveSplits : kMaxSplits, (vocab + chunk - 1) / chunk);
-  const int want = std::max(1, std::min(most, wave ? (target + rows - 1) / rows : target / rows));
-  const int granule = (wave ? kWaveSize : kBlock) * p.vec;
-  const int per = (vocab + want - 1) / want;
-  p.slice_len = (per + granule - 1) / granule * granule;
-  p.splits = (vocab + p.slice_len - 1) / p.slice_len;
-  return p;
-}
-
-// One workgroup per row (row_kernel) once the rows alone fill the CUs and a row's slices
-// fit one workgroup.
-bool per_row_launch(const Launch &L, int cus) { return L.kcap <= kWaveKcap && L.rows >= cus && L.splits <= kRowWaves; }
-
-// Up to half as many rows as CUs (pools <= 256): each row is cut into parts of at least
-// kMinPart elements, one 16-wave row_kernel workgroup each, about one workgroup per CU in all;
-// wave_merge_kernel then merges the parts' sorted lists (one row of 151,936: 14.8 us in ten
-// parts against 18.8 us in 37 one-wave slices; 32 rows: 17.2 against 22.9 us). Returns the
-// number of parts (< 2: not used) and sets part_len (a multiple of a wave chunk, so parts
-// start on vector boundaries).
-constexpr int kMinPart = kRowWaves * kWChunk;
-constexpr int kMaxParts = 16;
-int row_parts(int rows, int vocab, int cus, int &part_len) {
-  const int by_cus = cus / std::max(rows, 1);
-  const int by_len = (vocab + kMinPart - 1) / kMinPart;
-  int parts = std::min(std::min(by_cus, by_len), kMaxParts);
-  if (parts < 2) return 0;
-  const int per = (vocab + parts - 1) / parts;
-  part_len = (per + kWChunk - 1) / kWChunk * kWChunk;
-  return (vocab + part_len - 1) / part_len;
-}
-
 // ---------------------------------------------------------------------------------------
 // Pools of 257..1024 (k_max > 256) in batches of at least as many rows as CUs: one 16-wave
 // workgroup per row streams it as row_kernel does (each wave's first chunk, then chunks
@@ -3547,6 +3407,146 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       W.stats[(size_t)row * kMaxSplits] = st;
     }
   }
+}
+
+}  // namespace tabby
+
+// Scratch of the allocation-free entry (tabby_sampler_sample_device_noalloc), per GPU.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// =========================================================================================
+// Host side.
+// =========================================================================================
+using namespace tabby;
+
+struct tabby_sampler {
+  int device = 0;
+  int cus = 0;  // compute units of the device
+  int32_t vocab_max = 0, rows_max = 0, k_max = 0;
+  Workspace ws{};
+  void *ws_base = nullptr;
+  size_t head_rows_cap = 0;  // rows the head buffers are sized for (0: not allocated)
+  void *head_base = nullptr;
+  tabby_row_params *params_dev = nullptr;
+  tabby_row_result *results_dev = nullptr;
+  tabby_row_params *params_pinned = nullptr;
+  tabby_row_result *results_pinned = nullptr;
+  int32_t *topk_ids_dev = nullptr;
+  float *topk_logits_dev = nullptr;
+  size_t topk_elems_cap = 0;
+};
+
+namespace tabby {
+
+thread_local std::string g_last_error;
+
+int record_failure(int status, const std::string &msg) {
+  g_last_error = msg;
+  return status;
+}
+
+int device_cus(int device, int *cus) {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  if (device < 0 || device >= 64) return record_failure(TABBY_EINVAL, "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[device] == 0) {
+    int n = 0;
+    const hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return record_hip_failure(e, "hipDeviceGetAttribute(multiprocessor count)");
+    cached[device] = n;
+  }
+  *cus = cached[device];
+  return TABBY_OK;
+}
+
+int handle_view(const tabby_sampler *h, HandleView *out) {
+  if (!h) return record_failure(TABBY_EINVAL, "sampler handle is null");
+  out->device = h->device;
+  out->cus = h->cus;
+  out->vocab_max = h->vocab_max;
+  out->rows_max = h->rows_max;
+  out->k_max = h->k_max;
+  out->scratch = h->ws.cands;
+  out->scratch_bytes = (size_t)h->rows_max * (size_t)h->ws.row_cand_stride * sizeof(uint64_t);
+  return TABBY_OK;
+}
+
+}  // namespace tabby
+
+namespace {
+
+int fail(int status, const std::string &msg) { return record_failure(status, msg); }
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(TABBY_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr)                                  \
+  do {                                                 \
+    hipError_t e_ = (expr);                            \
+    if (e_ != hipSuccess) return hip_fail(e_, #expr);  \
+  } while (0)
+
+struct Plan {
+  int slice_len;
+  int splits;
+  int vec;
+};
+
+// Enough slices per row that the batch fills the chip about once: 256 CUs x 3 resident
+// 256-lane workgroups of the slice kernel (its 41.5 KB of LDS leaves room for three; a
+// larger grid ran in two rounds -- config 5, 512 rows: 3 slices per row took 225 us, one
+// 200 us), rounded down, or 256 CUs x 4 SIMDs x 4 one-wave workgroups for the wave kernel
+// (measured at 256 rows: 16 slices per row, 39.9 us per call, beat 12 per row, 41.4 us --
+// the SIMDs issue their oldest wave first and a fourth wave hides more of the others'
+// waits -- and 18 or 20 per row, which no longer fit at once, ~50 us). Each
+// slice is at least one chunk long (two for the wave kernel) and aligned to the vector
+// loads. A row's wave slices are capped at kMaxWaveSplits: with few rows the chip is idle
+// anyway and the latency is one slice's chain plus the merge, whose cost grows with the
+// number of lists (measured on one row: 24 slices of 2048 beat 12 of 4096 and 48 of 1024
+// at vocab 49152; 37 slices of 4096 beat 46 and 74 at vocab 151936).
+constexpr int kTargetGroups = 768;
+constexpr int kTargetWaves = 4096;
+constexpr int kMaxWaveSplits = 36;
+
+Plan make_plan(int rows, int vocab, int dtype, const void *logits, bool wave) {
+  Plan p;
+  const int vec_elems = dtype == TABBY_F32 ? 4 : 8;
+  const bool aligned = ((uintptr_t)logits % 16u) == 0 && vocab % vec_elems == 0;
+  p.vec = aligned ? vec_elems : 1;
+  const int chunk = wave ? 2 * kWChunk : kChunk;
+  const int target = wave ? kTargetWaves : kTargetGroups;
+  const int most = std::min(wave ? kMaxWaveSplits : kMaxSplits, (vocab + chunk - 1) / chunk);
+  const int want = std::max(1, std::min(most, wave ? (target + rows - 1) / rows : target / rows));
+  const int granule = (wave ? kWaveSize : kBlock) * p.vec;
+  const int per = (vocab + want - 1) / want;
+  p.slice_len = (per + granule - 1) / granule * granule;
+  p.splits = (vocab + p.slice_len - 1) / p.slice_len;
+  return p;
+}
+
+// One workgroup per row (row_kernel) once the rows alone fill the CUs and a row's slices
+// fit one workgroup.
+bool per_row_launch(const Launch &L, int cus) { return L.kcap <= kWaveKcap && L.rows >= cus && L.splits <= kRowWaves; }
+
+// Up to half as many rows as CUs (pools <= 256): each row is cut into parts of at least
+// kMinPart elements, one 16-wave row_kernel workgroup each, about one workgroup per CU in all;
+// wave_merge_kernel then merges the parts' sorted lists (one row of 151,936: 14.8 us in ten
+// parts against 18.8 us in 37 one-wave slices; 32 rows: 17.2 against 22.9 us). Returns the
+// number of parts (< 2: not used) and sets part_len (a multiple of a wave chunk, so parts
+// start on vector boundaries).
+constexpr int kMinPart = kRowWaves * kWChunk;
+constexpr int kMaxParts = 16;
+int row_parts(int rows, int vocab, int cus, int &part_len) {
+  const int by_cus = cus / std::max(rows, 1);
+  const int by_len = (vocab + kMinPart - 1) / kMinPart;
+  int parts = std::min(std::min(by_cus, by_len), kMaxParts);
+  if (parts < 2) return 0;
+  const int per = (vocab + parts - 1) / parts;
+  part_len = (per + kWChunk - 1) / kWChunk * kWChunk;
+  return (vocab + part_len - 1) / part_len;
 }
 
 template <typename In, int VEC>
