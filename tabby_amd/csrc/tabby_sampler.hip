@@ -1485,7 +1485,7 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
     uint32_t list_key = 0xffffffffu;
     const int need = min(L.topk_cap, V);
     if (need > 0) {
-      if (C > need) {
+      if (C >= need) {  // the candidates hold the row's top `need`: select the need-th largest
         const SelectResult r = staged ? radix_select(from_lds, (uint32_t)need, sm.u.hist, sm.bs)
                                       : radix_select(from_global, (uint32_t)need, sm.u.hist, sm.bs);
         // Every selected composite is >= r.prefix, whose low bits below r.shift are zero.

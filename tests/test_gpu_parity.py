@@ -44,7 +44,7 @@ def test_config5_ties_neg_inf_k1024(oracle):
 
 
 def test_config5_sorted_slice_lists(oracle):
-    # 256 rows: three slices per row of the 256-lane slice kernel.
+    # 256 rows: one pool_row_kernel workgroup per row (its list selected in the kernel).
     w = synth.config(5, rows=256)
     res, ids, vals = run_gpu(w, k_max=1024, topk_cap=1024)
     _log("config5[256 rows]", compare(w, res, ids, vals, run_oracle(oracle, w, 1024), 1024))
@@ -57,6 +57,28 @@ def test_large_pool_capacity_mixed_k(oracle):
                               k_choices=(1, 64, 300, 1024))
     res, ids, vals = run_gpu(w, k_max=1024, topk_cap=1024)
     _log("k_max 1024 mixed", compare(w, res, ids, vals, run_oracle(oracle, w, 1024), 1024))
+
+
+@pytest.mark.parametrize("dtype,vocab", [(np.float32, 20000), (np.float16, 20000), (np.float16, 20001),
+                                         (np.float32, 3000)])
+def test_pool_row_kernel_batches(oracle, dtype, vocab):
+    # Batches of >= 256 rows with k_max 1024 take pool_row_kernel: k from 1 to 1024 with ties
+    # and -inf, rows whose every element is a candidate (all equal: the shared list spills past
+    # its 8,192 LDS entries to global memory), whole-vocabulary rows (handed to the head path),
+    # a vocabulary shorter than the 16 waves' first chunks (3,000), and f16 rows of odd length
+    # (one-element loads).
+    rows = 256
+    w = synth.random_workload(rows=rows, vocab=vocab, seed=vocab + rows, ties=True, neg_inf_frac=0.2,
+                              k_choices=(1, 64, 300, 1024), temperatures=(0.0, 0.7, 1.0, 2.0),
+                              top_ps=(0.5, 0.9, 0.98, 1.0))
+    for r in range(0, rows, 16):
+        w.logits[r, :] = 1.25  # all equal
+        w.top_k[r] = 1024
+    w.top_k[5::32] = 0  # whole vocabulary
+    if dtype == np.float16:
+        w.logits = w.logits.astype(np.float16)
+    res, ids, vals = run_gpu(w, k_max=1024, topk_cap=64)
+    _log(f"pool row kernel {dtype.__name__} V={vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
 
 
 def test_f16_input_finite_k(oracle):
