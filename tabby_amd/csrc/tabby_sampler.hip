@@ -1479,12 +1479,43 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
     }
   };
   if (!finite) {
-    // Whole-vocabulary row: hand max / sum-exp / the head threshold to the head kernels.
-    // The threshold also covers the caller's top-k list: the candidates hold the row's
-    // top topk_cap elements, and the key of the topk_cap-th largest bounds the head below.
-    uint32_t list_key = 0xffffffffu;
+    // Whole-vocabulary row: hand max / sum-exp / the head threshold to the head kernels. The
+    // candidates hold the row's top Nw = max(topk_cap, kHeadList) (slice_keep): when Nw fits a
+    // wave's register sort (<= 256) they go on sorted, with the sequential sum of their terms,
+    // to head_kernel and head_fast_kernel, as from finish_pool; the head also covers the
+    // caller's top-k list, the first topk_cap of them.
+    const int Nw = min(max(L.topk_cap, kHeadList), V);
     const int need = min(L.topk_cap, V);
-    if (need > 0) {
+    uint32_t list_key = 0xffffffffu;
+    int handed = 0;
+    if (Nw <= kWaveKcap && C >= Nw) {
+      auto pick = [&](auto &&each) {
+        if (threadIdx.x == 0) sm.bs.slot = 0u;
+        __syncthreads();
+        if (C > Nw) {
+          const SelectResult r = radix_select(each, (uint32_t)Nw, sm.u.hist, sm.bs);
+          each([&](uint64_t v) {
+            const bool take = selected(v, r);
+            const uint32_t at = wave_slot(take, &sm.bs.slot);
+            if (take && at < (uint32_t)Nw) sm.sorted[at] = v;
+          });
+        } else {
+          each([&](uint64_t v) {
+            const uint32_t at = wave_slot(true, &sm.bs.slot);
+            if (at < (uint32_t)Nw) sm.sorted[at] = v;
+          });
+        }
+      };
+      if (staged) pick(from_lds); else pick(from_global);
+      const int npow = next_pow2(Nw);
+      for (int i = Nw + (int)threadIdx.x; i < npow; i += kBlock) sm.sorted[i] = 0ull;
+      __syncthreads();
+      block_sort_desc(sm.sorted, npow);
+      uint64_t *list = W.head_sorted + (size_t)row * W.head_stride;
+      for (int i = threadIdx.x; i < Nw; i += kBlock) list[i] = sm.sorted[i];
+      if (need > 0) list_key = composite_key(sm.sorted[need - 1]);
+      handed = Nw;
+    } else if (need > 0) {
       if (C >= need) {  // the candidates hold the row's top `need`: select the need-th largest
         const SelectResult r = staged ? radix_select(from_lds, (uint32_t)need, sm.u.hist, sm.bs)
                                       : radix_select(from_global, (uint32_t)need, sm.u.hist, sm.bs);
@@ -1494,13 +1525,23 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
         list_key = kNegInfKey;  // fewer candidates than the list: take the whole row
       }
     }
-    if (threadIdx.x == 0) {
+    if (wave_id() != 0) return;
+    const double T = P.temperature;
+    double list_sum = 0.0;
+    if (handed > 0 && T > 0.0) {
+      double *terms = sm.u.tail.w;  // the histogram is no longer needed
+      for (int i = lane_id(); i < handed; i += kWaveSize)
+        terms[i] = fdlibm_exp(((double)value_of(composite_key(sm.sorted[i])) - (double)row_max) / T);
+      wave_lds_sync();
+      list_sum = wave_seq_sum(terms, handed, nullptr, INFINITY).total;
+    }
+    if (lane_id() == 0) {
       RowState rs;
       rs.max = row_max;
       rs.sum_exp = sum_exp;
       rs.status = TABBY_OK;
-      rs.handoff = 0;
-      rs.list_sum = 0.0;
+      rs.handoff = (uint32_t)handed << 16;
+      rs.list_sum = list_sum;
       rs.head_key = min(head_threshold(row_max, P.temperature), list_key);
       W.row_state[row] = rs;
     }

@@ -271,8 +271,8 @@ def test_full_vocab_mixed_with_finite_rows(oracle):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
-@pytest.mark.parametrize("topk_cap", [0, 16])
-def test_full_vocab_fast_finish_edges(oracle, dtype, topk_cap):
+@pytest.mark.parametrize("topk_cap,k_max", [(0, 64), (16, 64), (16, 1024), (300, 1024)])
+def test_full_vocab_fast_finish_edges(oracle, dtype, topk_cap, k_max):
     # Whole-vocabulary rows that the merge's sorted top list may finish (head_fast_kernel) or
     # must hand to the sorted head: fewer finite entries than the list (the rest -inf), a spike
     # over a band of ~150 distinct small terms under top-p 0.5 (their ulp counts tie now and
@@ -308,8 +308,10 @@ def test_full_vocab_fast_finish_edges(oracle, dtype, topk_cap):
     w.logits[:] = w.logits.astype(dtype).astype(np.float32)
     if dtype == np.float16:
         w.logits = w.logits.astype(np.float16)
-    res, ids, vals = run_gpu(w, k_max=64, topk_cap=topk_cap)
-    _log(f"full vocab fast finish {dtype.__name__} cap={topk_cap}",
+    # k_max 1024: the list comes from merge_kernel (pools above 256); a 300-entry list is too
+    # long to hand over, and those rows take the sorted head.
+    res, ids, vals = run_gpu(w, k_max=k_max, topk_cap=topk_cap)
+    _log(f"full vocab fast finish {dtype.__name__} cap={topk_cap} k_max={k_max}",
          compare(w, res, ids, vals, run_oracle(oracle, w, topk_cap), topk_cap))
 
 
