@@ -205,7 +205,7 @@ __device__ __forceinline__ int block_first(Smem &sm, int n, Pred pred) {
 // the result written. Otherwise (or for a greedy row) returns false and finish_row computes the
 // row bit for bit. poolMass and the probability (compared within 1e-5) take the fast terms.
 template <int KCAP, typename In, class Smem>
-__device__ bool finish_row_fast(Smem &sm, const Launch &L, int row, const In *row_src, int count,
+__device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int row, const In *row_src, int count,
                                 float max_logit, double sum_exp, const tabby_row_params &P) {
   constexpr int PER = KCAP / kBlock;
   const double T = P.temperature, top_p = P.top_p;
@@ -291,7 +291,7 @@ __device__ bool finish_row_fast(Smem &sm, const Launch &L, int row, const In *ro
 }
 
 template <int KCAP, typename In, class Smem>
-__device__ void finish_row(Smem &sm, const Launch &L, int row, const In *row_src,
+__device__ __forceinline__ void finish_row(Smem &sm, const Launch &L, int row, const In *row_src,
                            int count, float max_logit, double sum_exp,
                            const tabby_row_params &P) {
   if (finish_row_fast<KCAP, In>(sm, L, row, row_src, count, max_logit, sum_exp, P)) return;
@@ -389,7 +389,7 @@ __device__ __forceinline__ double readlane_f64(double v, int lane) {
 // top-p scan (each lane keeps its own element's) and the draw is a ballot over
 // "target < running".
 template <int R, typename In>
-__device__ void wave_finish(const uint64_t *pool_in, int count, const Launch &L, int row,
+__device__ __forceinline__ void wave_finish(const uint64_t *pool_in, int count, const Launch &L, int row,
                             const In *row_src, float max_logit, double sum_exp,
                             const tabby_row_params &P) {
   const int lane = wave_lane();
