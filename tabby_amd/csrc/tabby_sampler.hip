@@ -3272,17 +3272,113 @@ constexpr int kPoolThreads = kPoolWaves * kWaveSize;
 constexpr int kPoolListCap = 8192;
 constexpr int kPoolBoundKeys = 4 * kPoolThreads;
 
+constexpr int kPoolHistPad = kBins + kBins / 32;  // one pad word per 32 bins (pool_pass)
+
 struct PoolSmem {
   union {
     uint64_t list[kPoolListCap];
     uint32_t keys[kPoolBoundKeys];  // the first bound's keys, before anything is appended
   } u;
-  uint32_t hist[kBins];
+  uint32_t hist[kPoolHistPad];
   SliceStat stats[kPoolWaves];
   BlockScratchT<kPoolWaves> bs;
   uint32_t count;
   int next_chunk;
 };
+
+// One histogram pass of the pool kernel's selections, by the whole workgroup: the entries
+// that bin_of admits (bin >= 0; bin 0 holds the largest) are counted, and wave 0 finds the
+// bin where the count from the top reaches `need` (each lane scans 32 consecutive bins,
+// stored one pad word per 32 so that the lanes' reads fall in different banks). Returns the
+// bin, the entries in the bins above it and the entries in it.
+struct PoolBin {
+  uint32_t bin, above, count;
+};
+
+__device__ __forceinline__ int pool_hist_at(int b) { return b + (b >> 5); }
+
+template <class Each, class BinOf>
+__device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Each each, BinOf bin_of, uint32_t need) {
+  for (int i = threadIdx.x; i < kPoolHistPad; i += kPoolThreads) sm.hist[i] = 0u;
+  __syncthreads();
+  each([&](uint64_t v) {
+    const int b = bin_of(v);
+    if (b >= 0) atomicAdd(&sm.hist[pool_hist_at(b)], 1u);
+  });
+  __syncthreads();
+  if (wave_id() == 0) {
+    // Lane sums, their scan, then the owning lane walks its bins again (keeping 32 counts
+    // per lane in registers spilled under the kernel's 64-VGPR budget).
+    constexpr int PER = kBins / kWaveSize;
+    const int lane = wave_lane();
+    uint32_t sum = 0u;
+    static_assert(PER == 32, "pool_hist_at pads one word per 32 bins: a lane's bins are lane * 33 + q");
+    const uint32_t *mine = sm.hist + lane * (PER + 1);
+#pragma unroll 4
+    for (int q = 0; q < PER; ++q) sum += mine[q];
+    const uint32_t inc = wave_inclusive_scan_u32(sum);
+    const uint32_t before = inc - sum;
+    if (before < need && need <= inc) {
+      uint32_t acc = before;
+      int q = 0;
+      for (; q < PER - 1; ++q) {  // the lane's last bin holds it if none before does
+        const uint32_t c = mine[q];
+        if (need <= acc + c) break;
+        acc += c;
+      }
+      sm.bs.bin = (uint32_t)(lane * PER + q);
+      sm.bs.above = acc;
+      sm.bs.count = mine[q];
+    }
+  }
+  __syncthreads();
+  const PoolBin r{sm.bs.bin, sm.bs.above, sm.bs.count};
+  __syncthreads();  // sm.bs and sm.hist are reused
+  return r;
+}
+
+// The composite T with exactly `need` entries >= T (1 <= need <= entries), given that every
+// entry's key lies in [lo, hi]: key passes over the live key range, 2,048 bins each, until one
+// key remains (a quantized row resolves in one), then the ~index digits of that key's
+// entries (bits 20..10, 9..0; bits 31..21 of ~index are ones below 2^21 indices). A pass
+// that leaves its bin exactly taken ends early.
+template <class Each>
+__device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Each each, uint32_t need, uint32_t lo, uint32_t hi) {
+  for (;;) {
+    const uint32_t range = hi - lo;
+    const int bits = range == 0u ? 0 : 32 - __builtin_clz(range);
+    const int shift = bits > 11 ? bits - 11 : 0;
+    const uint32_t top_key = hi, low_key = lo;
+    const PoolBin r = pool_pass(sm, each, [&](uint64_t v) {
+      const uint32_t k = composite_key(v);
+      return (k >= low_key && k <= top_key) ? (int)((top_key - k) >> shift) : -1;
+    }, need);
+    need -= r.above;
+    const uint32_t bin_top = hi - (r.bin << shift);
+    const uint32_t bin_low = bin_top - min((1u << shift) - 1u, bin_top - lo);
+    if (r.count == need) return (uint64_t)bin_low << 32;  // the whole bin is taken
+    hi = bin_top;
+    lo = bin_low;
+    if (shift == 0) break;
+  }
+  uint64_t prefix = ((uint64_t)lo << 32) | 0xffe00000ull;
+  int done = 21;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int sh = p == 0 ? 10 : 0;
+    const uint32_t mask = p == 0 ? 0x7ffu : 0x3ffu;
+    const uint64_t want = prefix >> done;
+    const int d = done;
+    const PoolBin r = pool_pass(sm, each, [&](uint64_t v) {
+      return (v >> d) == want ? (int)(mask - ((uint32_t)(v >> sh) & mask)) : -1;
+    }, need);
+    need -= r.above;
+    prefix |= (uint64_t)(mask - r.bin) << sh;
+    done = sh;
+    if (r.count == need) return prefix;
+  }
+  return prefix;
+}
 
 // Two workgroups per CU (74 KB of LDS and at most 64 VGPRs each): one's bound and selection
 // overlap the other's streaming, and 512 rows run in one round.
@@ -3424,12 +3520,15 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     auto each = [&](auto &&f) {
       for (uint32_t i = threadIdx.x; i < C; i += kPoolThreads) f(i < (uint32_t)kPoolListCap ? sm.u.list[i] : region[i]);
     };
-    const SelectResult r = radix_select(each, (uint32_t)kk, sm.hist, sm.bs);
+    // Every candidate's key lies between theta's and the row max's.
+    float mx = lane < kPoolWaves ? sm.stats[lane].max : -INFINITY;
+    mx = wave_max(mx);
+    const uint64_t thr = pool_select(sm, each, (uint32_t)kk, key_of(theta), key_of(mx));
     if (threadIdx.x == 0) sm.bs.slot = 0u;
     __syncthreads();
     // region[0 .. kk) lies below the overflow entries (kk <= 1,024 < kPoolListCap).
     each([&](uint64_t v) {
-      const bool take = selected(v, r);
+      const bool take = v >= thr;
       const uint32_t at = wave_slot(take, &sm.bs.slot);
       if (take && at < (uint32_t)kk) region[at] = v;
     });
