@@ -25,31 +25,34 @@ template <int NW>
 struct BlockScratchT {
   float f[NW];
   double d[NW];
+  double d2[NW];
   uint32_t u[NW];
-  uint32_t bin, above, count, slot;
+  uint32_t bin, above, count, slot, slot2;
 };
 using BlockScratch = BlockScratchT<kWaves>;
 
-__device__ __forceinline__ float block_max(float v, BlockScratch &s) {
+template <int NW>
+__device__ __forceinline__ float block_max(float v, BlockScratchT<NW> &s) {
   v = wave_max(v);
   __syncthreads();
   if (lane_id() == 0) s.f[wave_id()] = v;
   __syncthreads();
   float r = s.f[0];
 #pragma unroll
-  for (int i = 1; i < kWaves; ++i) r = fmaxf(r, s.f[i]);
+  for (int i = 1; i < NW; ++i) r = fmaxf(r, s.f[i]);
   return r;
 }
 
 // Fixed reduction tree, so the result is bit-identical from run to run.
-__device__ __forceinline__ double block_sum(double v, BlockScratch &s) {
+template <int NW>
+__device__ __forceinline__ double block_sum(double v, BlockScratchT<NW> &s) {
   v = wave_sum(v);
   __syncthreads();
   if (lane_id() == 0) s.d[wave_id()] = v;
   __syncthreads();
   double r = s.d[0];
 #pragma unroll
-  for (int i = 1; i < kWaves; ++i) r += s.d[i];
+  for (int i = 1; i < NW; ++i) r += s.d[i];
   return r;
 }
 
@@ -155,11 +158,13 @@ __device__ __forceinline__ bool selected(uint64_t v, SelectResult r) {
   return (v >> r.shift) >= (r.prefix >> r.shift);
 }
 
-// In-place descending bitonic sort of a[0..n), n a power of two, by the whole workgroup.
+// In-place descending bitonic sort of a[0..n), n a power of two, by the whole workgroup of
+// NW waves.
+template <int NW = kWaves>
 __device__ __forceinline__ void bitonic_sort_desc(uint64_t *a, int n) {
   for (int size = 2; size <= n; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < (n >> 1); i += kBlock) {
+      for (int i = threadIdx.x; i < (n >> 1); i += NW * 64) {
         const int lo = 2 * i - (i & (stride - 1));
         const int hi = lo + stride;
         const bool desc = (lo & size) == 0;
@@ -177,15 +182,16 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t *a, int n) {
 // In-place descending sort of a[0..n) in LDS, n a power of two, by the whole workgroup:
 // each wave sorts 256-entry chunks in registers (the network's stages below 256 need no
 // barrier), and only the strides of 256 and above go through LDS with a barrier each.
+template <int NW = kWaves>
 __device__ __forceinline__ void block_sort_desc(uint64_t *a, int n) {
   constexpr int R = 4, kChunkN = kWaveSize * R;  // 256 entries per wave pass
   if (n < kChunkN) {
-    bitonic_sort_desc(a, n);
+    bitonic_sort_desc<NW>(a, n);
     return;
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   auto chunk_pass = [&](int size, bool full) {
-    for (int base = wave * kChunkN; base < n; base += kWaves * kChunkN) {
+    for (int base = wave * kChunkN; base < n; base += NW * kChunkN) {
       uint64_t v[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) v[r] = a[base + r * kWaveSize + lane];
@@ -202,7 +208,7 @@ __device__ __forceinline__ void block_sort_desc(uint64_t *a, int n) {
   chunk_pass(0, true);
   for (int size = 2 * kChunkN; size <= n; size <<= 1) {
     for (int stride = size >> 1; stride >= kChunkN; stride >>= 1) {
-      for (int i = threadIdx.x; i < (n >> 1); i += kBlock) {
+      for (int i = threadIdx.x; i < (n >> 1); i += NW * 64) {
         const int lo = 2 * i - (i & (stride - 1));
         const int hi = lo + stride;
         const bool desc = (lo & size) == 0;

@@ -169,85 +169,81 @@ __device__ __forceinline__ int slice_keep(bool valid, int keff, int n, int kcap,
   return head_pass ? min(max(topk_cap, kHeadList), n) : 0;
 }
 
-// sampleFromTopK (src/engine/sampler.ts:147-212) over the `count` sorted candidates in
-// sm.sorted, f64 throughout, with the reference's order of operations: the per-element
-// terms are independent and computed by all lanes; every sum is a sequential left-to-right
-// f64 sum on lane 0. The running sums of the draw (sampler.ts:195-203) are the same
-// numbers as the top-p cumulative sums (sampler.ts:178-185), and `total` (:191-192) is the
-// last of them, so lane 0 computes that sequence once and keeps it.
-// The first index in [0, n) (n <= kBlock * PER; thread t holds entries PER*t .. PER*t + PER - 1)
-// for which pred holds, or n: a workgroup minimum through sm.bs.slot.
-template <int PER, class Smem, class Pred>
-__device__ __forceinline__ int block_first(Smem &sm, int n, Pred pred) {
-  if (threadIdx.x == 0) sm.bs.slot = (uint32_t)n;
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = (int)threadIdx.x * PER + j;
-    if (i < n && pred(i, j)) {
-      atomicMin(&sm.bs.slot, (uint32_t)i);
-      break;
-    }
-  }
-  __syncthreads();
-  const int r = (int)sm.bs.slot;
-  __syncthreads();
-  return r;
-}
-
 // The fast form of finish_row for pools of 257..KCAP (as reg_tail for pools up to 64): terms
-// from exp_nonpos (within 8 ulp of exp), the scaled total a workgroup sum and the running sums
-// a workgroup scan (thread t holds consecutive entries; each partial sum a tree of at most 12
-// roundings). Against the reference's sequential sums of its exact terms -- whose own rounding
+// from exp_nonpos (within 8 ulp of exp), the running sums of the scaled terms a workgroup scan
+// divided by their total (each partial sum a tree of at most 12 roundings, then one
+// division). Against the reference's sequential sums of its exact terms -- whose own rounding
 // is at most n * 2^-53 relative -- the running sums then differ by less than 2^-42 of their
 // value for n <= 1024, so when every comparison that decides the cut and the draw clears its
 // threshold by more than 2^-36 relative, the reference decides the same way: returns true with
 // the result written. Otherwise (or for a greedy row) returns false and finish_row computes the
 // row bit for bit. poolMass and the probability (compared within 1e-5) take the fast terms.
+// Three barriers: one exchange of the waves' totals, then one per first-index search (one LDS
+// atomic per wave: the first lane that holds a match).
 template <int KCAP, typename In, class Smem>
 __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int row, const In *row_src, int count,
                                 float max_logit, double sum_exp, const tabby_row_params &P) {
   constexpr int PER = KCAP / kBlock;
   const double T = P.temperature, top_p = P.top_p;
   if (!(T > 0.0)) return false;
+  const int lane = lane_id(), wave = wave_id();
   double *run = sm.u.tail.w;  // running sums, by index
-  double e[PER], s[PER], e_sum = 0.0, s_sum = 0.0;
+  double c[PER], e_sum = 0.0, acc = 0.0;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int i = (int)threadIdx.x * PER + j;
     const bool in = i < count;
     const double d = in ? (double)value_of(composite_key(sm.sorted[i])) - (double)max_logit : 0.0;
-    e[j] = in ? exp_nonpos(d) : 0.0;
-    s[j] = !in ? 0.0 : T == 1.0 ? e[j] : exp_nonpos(d / T);
-    e_sum += e[j];
-    s_sum += s[j];
-  }
-  const double pool = block_sum(e_sum, sm.bs) / sum_exp;
-  const double scaled = block_sum(s_sum, sm.bs);
-  // Running sums: within the thread, then across lanes and waves.
-  double c[PER], acc = 0.0;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    acc += s[j] / scaled;
-    c[j] = acc;
+    const double e = in ? exp_nonpos(d) : 0.0;
+    e_sum += e;
+    acc += !in ? 0.0 : T == 1.0 ? e : exp_nonpos(d / T);
+    c[j] = acc;  // the thread's running sum of the scaled terms
   }
   const double incl = wave_inclusive_scan(acc);
+  const double e_wave = wave_sum(e_sum);
+  if (lane == kWaveSize - 1) sm.bs.d[wave] = incl;
+  if (lane == 0) sm.bs.d2[wave] = e_wave;
+  if (threadIdx.x == 0) {
+    sm.bs.slot = (uint32_t)count;
+    sm.bs.slot2 = (uint32_t)count;
+  }
   __syncthreads();
-  if (lane_id() == kWaveSize - 1) sm.bs.d[wave_id()] = incl;
-  __syncthreads();
-  double base = incl - acc;
-  for (int k = 0; k < wave_id(); ++k) base += sm.bs.d[k];
+  double scaled = 0.0, e_total = 0.0, base = incl - acc;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) {
+    scaled += sm.bs.d[k];
+    e_total += sm.bs.d2[k];
+    if (k < wave) base += sm.bs.d[k];
+  }
+  const double pool = e_total / sum_exp;
+  double r[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int i = (int)threadIdx.x * PER + j;
-    if (i < count) run[i] = base + c[j];
+    r[j] = (base + c[j]) / scaled;
+    if (i < count) run[i] = r[j];
   }
+  // The first index whose running sum satisfies pred: the thread's first, the wave's first
+  // lane with one, one atomic per wave.
+  auto first_of = [&](uint32_t *slot, int n, auto pred) {
+    int mine = n;
+#pragma unroll
+    for (int j = PER - 1; j >= 0; --j) {
+      const int i = (int)threadIdx.x * PER + j;
+      if (i < n && pred(r[j])) mine = i;
+    }
+    const uint64_t m = __ballot(mine < n);
+    if (m && lane == __ffsll((unsigned long long)m) - 1) atomicMin(slot, (uint32_t)mine);
+  };
+  if (top_p < 1.0) first_of(&sm.bs.slot, count, [&](double x) { return x >= top_p; });
   __syncthreads();
-  const int cut_at = top_p < 1.0 ? block_first<PER>(sm, count, [&](int i, int j) { return base + c[j] >= top_p; }) : count;
+  const int cut_at = (int)sm.bs.slot;
   const int cut = cut_at < count ? cut_at + 1 : count;
   const double total = run[cut - 1];
   const double target = P.uniform * total;
-  const int hit = block_first<PER>(sm, cut, [&](int i, int j) { return target < base + c[j]; });
+  first_of(&sm.bs.slot2, cut, [&](double x) { return target < x; });
+  __syncthreads();
+  const int hit = (int)sm.bs.slot2;
   const int chosen = hit < cut ? hit : cut - 1;
   // Margins of every comparison that fixed the cut and the draw (running sums are
   // non-decreasing, so the neighbours of each boundary are the only ones to check).
@@ -267,17 +263,17 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
   }
   const uint64_t cv = sm.sorted[chosen];
   if (threadIdx.x == 0) {
-    tabby_row_result r;
-    r.max_logit = max_logit;
-    r.sum_exp = sum_exp;
-    r.pool_mass = pool;
-    r.status = TABBY_OK;
-    r.topk_count = min(count, L.topk_cap);
-    r.considered = (uint32_t)cut;
-    r.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
-    r.id = (int32_t)composite_index(cv);
-    r.probability = exp_nonpos((double)value_of(composite_key(cv)) - (double)max_logit) / sum_exp;
-    L.results[row] = r;
+    tabby_row_result res;
+    res.max_logit = max_logit;
+    res.sum_exp = sum_exp;
+    res.pool_mass = pool;
+    res.status = TABBY_OK;
+    res.topk_count = min(count, L.topk_cap);
+    res.considered = (uint32_t)cut;
+    res.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
+    res.id = (int32_t)composite_index(cv);
+    res.probability = exp_nonpos((double)value_of(composite_key(cv)) - (double)max_logit) / sum_exp;
+    L.results[row] = res;
   }
   if (L.topk_cap > 0) {
     const int m = min(count, L.topk_cap);
@@ -290,6 +286,12 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
   return true;
 }
 
+// sampleFromTopK (src/engine/sampler.ts:147-212) over the `count` sorted candidates in
+// sm.sorted, f64 throughout, in the reference's order of operations: the per-element terms
+// are independent and computed by all lanes; the sums are sequential left-to-right f64 sums,
+// evaluated bit for bit by a wave (seqsum.h). The running sums of the draw (sampler.ts:195-203)
+// are the top-p cumulative sums (sampler.ts:178-185), and `total` (:191-192) is the last of
+// them. The fast form above is tried first.
 template <int KCAP, typename In, class Smem>
 __device__ __forceinline__ void finish_row(Smem &sm, const Launch &L, int row, const In *row_src,
                            int count, float max_logit, double sum_exp,

@@ -69,7 +69,7 @@ def test_pool_row_kernel_batches(oracle, dtype, vocab):
     # (one-element loads).
     rows = 256
     w = synth.random_workload(rows=rows, vocab=vocab, seed=vocab + rows, ties=True, neg_inf_frac=0.2,
-                              k_choices=(1, 64, 300, 1024), temperatures=(0.0, 0.7, 1.0, 2.0),
+                              k_choices=(1, 64, 100, 200, 300, 1024), temperatures=(0.0, 0.7, 1.0, 2.0),
                               top_ps=(0.5, 0.9, 0.98, 1.0))
     for r in range(0, rows, 16):
         w.logits[r, :] = 1.25  # all equal
@@ -79,6 +79,36 @@ def test_pool_row_kernel_batches(oracle, dtype, vocab):
         w.logits = w.logits.astype(np.float16)
     res, ids, vals = run_gpu(w, k_max=1024, topk_cap=64)
     _log(f"pool row kernel {dtype.__name__} V={vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
+def test_pool_row_kernel_rows_outside_contract(oracle):
+    # The pool kernel ends every row but a head pass's whole-vocabulary ones: rows with -inf
+    # only, NaN or +inf report EDOMAIN, topK above k_max and whole-vocabulary rows without
+    # TABBY_FLAG_FULL_VOCAB report EINVAL, and the other rows (pools of 40 to 600) are sampled.
+    import torch
+    rows, vocab = 256, 3000
+    x = torch.randn(rows, vocab, device="cuda")
+    x[5] = float("-inf")
+    x[77, 1234] = float("nan")
+    x[200, 9] = float("inf")
+    p = S.make_params(S.SamplingParams(0.7, 40, 0.9), rows, 0.25)
+    p["top_k"] = np.array([40, 100, 200, 600], np.int32)[np.arange(rows) % 4]
+    p["uniform"] = (np.arange(rows) * 0.618034) % 1.0
+    p["top_k"][[9, 130]] = 2000
+    p["top_k"][[13, 250]] = 0
+    with S.GpuSampler(vocab_max=vocab, rows_max=rows, k_max=1024) as g:
+        pd = torch.from_numpy(p.view(np.uint8).copy()).cuda()
+        rd = torch.zeros(rows * S.RESULT_DTYPE.itemsize, dtype=torch.uint8, device="cuda")
+        g.sample_device(x, pd, rd)
+        res = rd.cpu().numpy().view(S.RESULT_DTYPE)
+    logits = x.cpu().numpy()
+    for r in range(rows):
+        want = (S.TABBY_EDOMAIN if r in (5, 77, 200) else S.TABBY_EINVAL if r in (9, 130, 13, 250) else 0)
+        assert res["status"][r] == want, f"row {r}"
+        if want == 0:
+            o = oracle.sample_row(logits[r], int(p[r]["top_k"]), float(p[r]["temperature"]),
+                                  float(p[r]["top_p"]), float(p[r]["uniform"]))
+            assert (int(res["id"][r]), int(res["considered"][r])) == (o["id"], o["considered"]), f"row {r}"
 
 
 def test_f16_input_finite_k(oracle):
