@@ -1932,10 +1932,14 @@ __device__ __forceinline__ RowPool row_pool(const Launch &L, const tabby_row_par
   return rp;
 }
 
-template <typename In>
+template <typename In, bool REG = false>
 __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, const Workspace &W, int row,
                                             const tabby_row_params &P, const RowPool &rp, float row_max,
                                             double sum_exp);
+
+template <typename In, class SumExp>
+__device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int row, const In *row_src,
+                                         float M, SumExp sum_exp_of, const tabby_row_params &P);
 
 // The row's top K, sorted, into sm.sorted[0..K) from its sorted lists (merge_lists_4 in the
 // register class of K; m1: the first 64 entries' loads, already issued). No barrier when
@@ -1971,13 +1975,15 @@ __device__ __forceinline__ void merge_row(WaveMergeSmem &sm, const Launch &L, co
   auto count_of = [&](int s) { return list_count(rs, s); };
   const RowPool rp = row_pool(L, P);
   merge_pool(sm, lists, m1, count_of, rp.K);
-  finish_pool<In>(sm, L, W, row, P, rp, rs.max, rs.sum_exp);
+  finish_pool<In, true>(sm, L, W, row, P, rp, rs.max, rs.sum_exp);
 }
 
 // The rest of a row once its pool, sm.sorted[0..K), and its max and sum-exp are known: the
 // f64 tail of sampleFromTopK, the hand-over to the head kernels, or an error status. Wave 0
-// and wave 1 work; every wave of the workgroup must call it.
-template <typename In>
+// and wave 1 work; every wave of the workgroup must call it. REG: pools of at most 64 take
+// wave 0's reg_tail (the merge kernels; row_kernel's pools of at most 64 end in
+// finish_small_pool, and its code stays as it is).
+template <typename In, bool REG>
 __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, const Workspace &W, int row,
                                             const tabby_row_params &P, const RowPool &rp, float row_max,
                                             double sum_exp) {
@@ -1987,6 +1993,12 @@ __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, 
   const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * L.vocab;
   const bool in_domain = (row_max > -INFINITY) && (row_max < INFINITY) && (sum_exp > 0.0) &&
                          (sum_exp < INFINITY);
+  if (REG && valid_params && in_domain && finite && K <= kWaveSize) {
+    // Pools of at most 64: one register per lane, wave 0's reg_tail.
+    if (wave_id() != 0) return;
+    reg_tail<In>(lane < K ? sm.sorted[lane] : 0ull, K, L, row, row_src, row_max, [&]() { return sum_exp; }, P);
+    return;
+  }
   if (valid_params && in_domain && finite) {
     // sampleFromTopK's two independent passes over the pool (sampler.ts:156-157, 170-172)
     // on two waves: wave 0 the exact terms and poolMass, wave 1 the scaled terms and their

@@ -464,6 +464,19 @@ def test_row_kernel_parts(oracle, rows):
     _log(f"row kernel parts, {rows} rows", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
 
 
+def test_row_kernel_parts_across_calls(oracle):
+    # Calls on one handle whose rows are cut into different numbers of parts (ten for a row
+    # of 151,936, seven and four for rows of 100,000): each call's part lists and statistics
+    # replace the previous call's in the handle's scratch, whatever their number.
+    with S.GpuSampler(vocab_max=151936, rows_max=64, k_max=64) as g:
+        for i, (rows, vocab) in enumerate([(1, 151936), (5, 100000), (1, 151936), (64, 100000),
+                                           (3, 151936), (1, 151936)]):
+            w = synth.random_workload(rows=rows, vocab=vocab, seed=900 + i, k_choices=(1, 20, 50, 64),
+                                      temperatures=(0.0, 0.7, 1.0), top_ps=(0.9, 1.0))
+            res, ids, vals = run_gpu(w, k_max=64, topk_cap=50, sampler=g)
+            _log(f"parts call {i}: {rows} x {vocab}", compare(w, res, ids, vals, run_oracle(oracle, w, 50), 50))
+
+
 @pytest.mark.parametrize("vocab", [33000, 49152])
 def test_row_kernel_one_workgroup_few_rows(oracle, vocab):
     # Rows of two or three parts' length with few rows: one 16-wave workgroup per row

@@ -67,6 +67,15 @@ def test_no_alloc_matches_device_entry_two_calls():
     _one(w2, 256, 64, "call 2, parts")
 
 
+def test_no_alloc_parts_across_calls():
+    # Calls whose rows are cut into different numbers of parts share the scratch: ten parts
+    # (a row of 151,936), then four (17 rows of 100,000), then ten again.
+    _one(synth.config(2), 64, 50, "parts: one row of 151,936")
+    w = synth.random_workload(rows=17, vocab=100000, seed=17, k_choices=(1, 50, 64), temperatures=(0.0, 0.8))
+    _one(w, 64, 50, "parts: 17 rows of 100,000")
+    _one(synth.config(2), 64, 50, "parts: one row of 151,936 again")
+
+
 def test_no_alloc_per_row_kernel_and_statuses():
     # 256 rows: one workgroup per row, no lists in scratch; a -inf row and a whole-vocabulary
     # row come back with their statuses as from the handle's entry.
