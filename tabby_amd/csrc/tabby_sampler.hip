@@ -1331,14 +1331,29 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
 // enters: the scaled total, which is >= 1 (its first term is exp(0)), and a running sum of
 // the weights divided by that total, which is >= its first term 1/total while every later
 // weight is < 2^-54/total. So it changes neither, and the draw never reaches it.
+// The predicate is monotone in the key, so the answer is found from the f32 rounding of
+// max - 37.5 T, which lies within a key or two of it, by stepping to the boundary (at most one
+// step in 3 million random and edge-case (max, T) pairs checked against a bisection over the
+// keys); a bisection of (kNegInfKey, top] stays as the fallback past 64 steps.
 __device__ __forceinline__ uint32_t head_threshold(float row_max, double T) {
   const uint32_t top = key_of(row_max);
   if (!(T > 0.0)) return top;
+  auto in_head = [&](uint32_t k) { return ((double)value_of(k) - (double)row_max) / T >= -37.5; };
+  uint32_t c = min(max(key_of((float)((double)row_max - 37.5 * T)), kNegInfKey + 1u), top);
+  int steps = 0;
+  while (c < top && !in_head(c) && steps < 64) {
+    ++c;
+    ++steps;
+  }
+  while (c > kNegInfKey + 1u && in_head(c - 1u) && steps < 64) {
+    --c;
+    ++steps;
+  }
+  if (steps < 64) return c;
   uint32_t lo = kNegInfKey, hi = top;
   while (hi - lo > 1u) {
     const uint32_t mid = lo + (hi - lo) / 2u;
-    const double q = ((double)value_of(mid) - (double)row_max) / T;
-    if (q >= -37.5) hi = mid; else lo = mid;
+    if (in_head(mid)) hi = mid; else lo = mid;
   }
   return hi;
 }
