@@ -2649,9 +2649,8 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
   int row, slice;
   row_slice_of((int)blockIdx.x, L.rows, L.h_splits, row, slice);
   const tabby_row_params P = L.params[row];
-  if (!is_head_row(P, L)) return;
-  const RowState rs = W.row_state[row];
-  if (rs.status != TABBY_OK) return;
+  const RowState rs = W.row_state[row];  // requested with the parameters: one round trip
+  if (!is_head_row(P, L) || rs.status != TABBY_OK) return;
   const int V = L.vocab, lane = wave_lane();
   const int begin = slice * L.h_slice_len;
   const int n = min(L.h_slice_len, V - begin);
@@ -3196,6 +3195,9 @@ __global__ __launch_bounds__(kPlanThreads) void head_fast_kernel(Launch L, Works
   uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
   const tabby_row_params P = L.params[row];
   const RowState rs = W.row_state[row];
+  // Every slice's head count is requested with them (one slice per thread).
+  const int ns = L.h_splits;
+  const uint32_t c = (int)threadIdx.x < ns ? W.head_slice_count[(size_t)row * W.acc_stride + threadIdx.x] : 0u;
   if (!is_head_row(P, L) || rs.status != TABBY_OK) {
     if (threadIdx.x == 0) plan[0] = 0u;
     return;
@@ -3217,8 +3219,6 @@ __global__ __launch_bounds__(kPlanThreads) void head_fast_kernel(Launch L, Works
     }
   }
   // The head's size and where each slice's entries start (every thread holds one slice).
-  const int ns = L.h_splits;
-  const uint32_t c = (int)threadIdx.x < ns ? W.head_slice_count[(size_t)row * W.acc_stride + threadIdx.x] : 0u;
   const uint32_t inc = wave_inclusive_scan_u32(c);
   if (wave_lane() == kWaveSize - 1) psm.wave_total[wave_id()] = inc;
   __syncthreads();
