@@ -42,7 +42,8 @@ __global__ __launch_bounds__(kGemvBlock) void q4_gemv_kernel(Q4Matrix W, const f
   const int r = (int)(blockIdx.x * kGemvBlock + threadIdx.x);
   if (r >= W.vocab) return;
   float acc[R];
-  q4_dot_row<R>(W, x, r, acc);
+  if constexpr (R >= 4) q4_dot_row_serial<R>(W, x, r, acc);
+  else q4_dot_row<R>(W, x, r, acc);
 #pragma unroll
   for (int t = 0; t < R; ++t) y[(size_t)t * W.vocab + r] = acc[t];
 }
