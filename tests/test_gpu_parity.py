@@ -277,6 +277,21 @@ def test_full_vocab_temperatures(oracle, temperature):
     _log(f"full vocab T={temperature}", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
 
 
+def test_full_vocab_head_threshold_extremes(oracle):
+    # The head's threshold (the smallest key with (l - max)/T >= -37.5 in f64) for
+    # temperatures from 1e-4 (a head of ties at the max) to 1e3 (the whole row) and rows whose
+    # max sits at 0, +300, -500 and +1e4 (keys far from 1.0 in both directions).
+    temps, offsets = (1e-4, 0.01, 3.0, 1e3), (0.0, 300.0, -500.0, 1e4)
+    w = synth.random_workload(rows=16, vocab=20000, seed=77, k_choices=(0,), temperatures=(1.0,),
+                              top_ps=(0.9,), ties=True, sigma=2.0)
+    for r in range(16):
+        w.temperature[r] = temps[r % 4]
+        w.top_p[r] = (0.5, 0.9, 0.99, 1.0)[(r // 4 + r) % 4]
+        w.logits[r] = (w.logits[r].astype(np.float64) + offsets[r // 4]).astype(np.float32)
+    res, ids, vals = run_gpu(w, k_max=64, topk_cap=64)
+    _log("full vocab head threshold extremes", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
 def test_full_vocab_flat_row_takes_batched_head(oracle):
     # A hot temperature puts every element in the head: H = V, several sort batches.
     w = synth.random_workload(rows=2, vocab=20000, seed=31, k_choices=(0,), temperatures=(50.0,),
