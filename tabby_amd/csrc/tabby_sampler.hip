@@ -38,6 +38,7 @@
 #include <algorithm>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "block_ops.h"
 #include "device_math.h"
@@ -1047,6 +1048,7 @@ __device__ __forceinline__ uint32_t union_kth(const uint32_t *keys, int total, i
 // counted down from `top` (the largest key of the row's first bound's union; larger keys go
 // to bin 0) to the row's first bound, below which no list entry lies.
 constexpr int kSelBins = 256;
+constexpr int kSmallTake = 2 * kWaveSize;  // finish_small_pool: pools and takes of at most 128
 
 struct SelBins {
   uint32_t top;
@@ -2107,7 +2109,7 @@ struct RowSmem {
   // Pools of at most 64 (finish_small_pool): the key histogram over every wave's list, the
   // selected entries and their count, and the row's shared first bound.
   uint32_t sel_hist[kSelBins];
-  uint64_t sel[kWaveSize];
+  uint64_t sel[kSmallTake];
   int sel_count;
   uint32_t bound_key[2];  // the row's first bound and the largest key of its union
 };
@@ -2215,6 +2217,150 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
     const uint32_t idx = composite_index(v);
     L.topk_ids[(size_t)row * L.topk_cap + lane] = (int32_t)idx;
     L.topk_logits[(size_t)row * L.topk_cap + lane] = load_one(row_src + min(idx, (uint32_t)(L.vocab - 1)));
+  }
+}
+
+// reg_tail for pools of 65..64R (R registers per lane; entry i = r * 64 + lane, sorted
+// descending over i). The sums are the wave's scans of each register plus the totals of the
+// registers before it (each partial sum a tree of at most 7 + R - 1 roundings; with n <= 256
+// the running sums stay within 2^-42 of the reference's), the cut and the draw the first
+// matching entry over the registers in order, and the same 2^-36 margins decide whether the
+// result stands. Otherwise the weights are recomputed with V8's exp and summed bit for bit
+// through `scratch` (LDS, >= 64R doubles; wave_seq_sum). The caller's top-k list and the
+// result as in reg_tail.
+template <int R, typename In, class SumExp>
+__device__ __forceinline__ void reg_tail_wide(const uint64_t (&v)[R], int K, const Launch &L, int row,
+                                              const In *row_src, float M, SumExp sum_exp_of,
+                                              const tabby_row_params &P, double *scratch) {
+  const int lane = wave_lane();
+  const double T = P.temperature;
+  double d[R], e1[R], s[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool in = r * kWaveSize + lane < K;
+    d[r] = (double)value_of(composite_key(v[r])) - (double)M;
+    e1[r] = in ? exp_nonpos(d[r]) : 0.0;
+    s[r] = !(in && T > 0.0) ? 0.0 : T == 1.0 ? e1[r] : exp_nonpos(d[r] / T);
+  }
+  const double S1 = sum_exp_of();
+  // Inclusive prefix sums over i = r * 64 + lane.
+  auto scan = [&](const double(&x)[R], double(&out)[R]) {
+    double carry = 0.0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const double inc = wave_inclusive_scan(x[r]);
+      out[r] = r == 0 ? inc : carry + inc;
+      carry = r == 0 ? lane_f64(inc, kWaveSize - 1) : carry + lane_f64(inc, kWaveSize - 1);
+    }
+  };
+  // Entry i of a per-register array, on every lane (i uniform).
+  auto at = [&](const double(&x)[R], int i) {
+    double y = 0.0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if ((i >> 6) == r) y = lane_f64(x[r], i & (kWaveSize - 1));
+    return y;
+  };
+  // The first entry below n for which pred(r) holds on its lane, or n.
+  auto first = [&](int n, auto pred) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint64_t m = __ballot(r * kWaveSize + lane < n && pred(r));
+      if (m) return r * kWaveSize + __ffsll((unsigned long long)m) - 1;
+    }
+    return n;
+  };
+  double exact[R], pre[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) exact[r] = e1[r] / S1;
+  scan(exact, pre);
+  const double pool = lane_f64(pre[R - 1], kWaveSize - 1);
+  tabby_row_result res;
+  res.max_logit = M;
+  res.sum_exp = S1;
+  res.pool_mass = pool;
+  res.status = TABBY_OK;
+  res.topk_count = min(K, L.topk_cap);
+  int chosen = 0;
+  if (!(T > 0.0)) {
+    res.considered = 1;
+    res.pool_exhausted = 0;
+  } else {
+    const double top_p = P.top_p;
+    double ssum[R], w[R], running[R];
+    scan(s, ssum);
+    const double scaled = lane_f64(ssum[R - 1], kWaveSize - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[r] = r * kWaveSize + lane < K ? s[r] / scaled : 0.0;
+    scan(w, running);
+    const int cut_at = top_p < 1.0 ? first(K, [&](int r) { return running[r] >= top_p; }) : K;
+    int cut = cut_at < K ? cut_at + 1 : K;
+    double total = at(running, cut - 1);
+    double target = P.uniform * total;
+    const int hit = first(cut, [&](int r) { return target < running[r]; });
+    chosen = hit < cut ? hit : cut - 1;
+    // Margins of every comparison that fixed the cut and the draw (running sums are
+    // non-decreasing, so the neighbours of each boundary are the only ones to check).
+    constexpr double kMargin = 1.0 / 68719476736.0;  // 2^-36
+    const double r_cut = total, r_before = cut >= 2 ? at(running, cut - 2) : 0.0;
+    bool clear = true;
+    if (top_p < 1.0) {
+      const double m = kMargin * top_p;
+      clear = (cut < K || r_cut < top_p - m) && (cut == K || (r_cut >= top_p + m && (cut == 1 || r_before < top_p - m)));
+    }
+    const double r_hi = at(running, chosen), r_lo = chosen >= 1 ? at(running, chosen - 1) : 0.0;
+    const double m2 = kMargin * total;
+    clear = clear && r_hi > target + m2 && (chosen == 0 || r_lo < target - m2);
+    if (!clear) {
+      // Bit for bit: V8's exp for the weights, sequential sums (sampler.ts:170-203).
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = r * kWaveSize + lane;
+        if (i < K) scratch[i] = fdlibm_exp_inline(d[r] / T);
+      }
+      wave_lds_sync();
+      const double S = wave_seq_sum(scratch, K, nullptr, INFINITY).total;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = r * kWaveSize + lane;
+        if (i < K) scratch[i] = scratch[i] / S;
+      }
+      wave_lds_sync();
+      const SeqSum run = wave_seq_sum(scratch, K, scratch, top_p < 1.0 ? top_p : INFINITY);
+      wave_lds_sync();
+      cut = run.count;
+      total = run.total;
+      target = P.uniform * total;
+      chosen = cut - 1;
+      for (int base = 0; base < cut; base += kWaveSize) {
+        const int i = base + lane;
+        const uint64_t m = __ballot(i < cut && target < scratch[min(i, cut - 1)]);
+        if (m) {
+          chosen = base + __ffsll((unsigned long long)m) - 1;
+          break;
+        }
+      }
+    }
+    res.considered = (uint32_t)cut;
+    res.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
+  }
+  uint64_t cv = 0ull;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if ((chosen >> 6) == r)
+      cv = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v[r], chosen & (kWaveSize - 1)) |
+           ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v[r] >> 32), chosen & (kWaveSize - 1)) << 32);
+  res.id = (int32_t)composite_index(cv);
+  res.probability = at(exact, chosen);
+  if (lane == 0) L.results[row] = res;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = r * kWaveSize + lane;
+    if (i < K && i < L.topk_cap) {
+      const uint32_t idx = composite_index(v[r]);
+      L.topk_ids[(size_t)row * L.topk_cap + i] = (int32_t)idx;
+      L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(L.vocab - 1)));
+    }
   }
 }
 
@@ -2422,10 +2568,10 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   const int nw = (int)(blockDim.x / kWaveSize);  // the row's waves, >= kRowMinWaves
   const tabby_row_params P = L.params[row];  // kept in registers for the merge
   const RowPool rp = row_pool(L, P);
-  // Pools of at most 64 skip the waves' end-of-stream sorts and the list merge: the row's top
+  // Pools of at most 128 skip the waves' end-of-stream sorts and the list merge: the row's top
   // K is selected from the unsorted lists (finish_small_pool). A part of a row (parts > 1)
   // only hands its top K on, whatever its pool; a whole row must be finished here.
-  const bool small = rp.valid && rp.K > 0 && rp.K <= kWaveSize && (L.parts > 1 || rp.finite);
+  const bool small = rp.valid && rp.K > 0 && rp.K <= kSmallTake && (L.parts > 1 || rp.finite);
   if (threadIdx.x == 0) {
     sm.next_chunk = nw;  // chunk w is wave w's first
     sm.sel_count = 0;
@@ -2491,7 +2637,9 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
   const int total = __builtin_amdgcn_readlane((int)inc, kWaveSize - 1);  // every list entry
   uint32_t take_key = 0u;  // entries with key >= take_key are taken
   int taken = total;
-  if (total > kWaveSize) {
+  // Pools of at most 64 select from more than 64 entries (one register to sort), larger pools
+  // from more than 128; either way total >= K when selecting.
+  if (total > (K <= kWaveSize ? kWaveSize : kSmallTake)) {
     const int owner = __ffsll((unsigned long long)__ballot(inc >= (uint32_t)K)) - 1;  // total >= K
     int bin = 0;
     uint32_t upto = 0;
@@ -2513,8 +2661,8 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
     if (bin < kSelBins - 1) take_key = sb.lowest(bin);
     else taken = total;
   }
-  if (taken > kWaveSize) {
-    // More than 64 would be taken (ties at the boundary, or a row whose top lies far above
+  if (taken > kSmallTake) {
+    // More than 128 would be taken (ties at the boundary, or a row whose top lies far above
     // the first bound's union): sort each list in place for the general merge.
     const int keep = min(count, K);
     if (count <= kWaveSize) store_sorted_top<1>(list, count, keep, sm.wave[w].list);
@@ -2539,46 +2687,61 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
   }
   __syncthreads();
   if (w != 0) return true;
-  uint64_t v[1] = {lane < taken ? composite_of_raw(sm.sel[lane]) : 0ull};
-  wave_sort_desc<1>(v);
-  const int k = min(K, taken);
   float mx = lane < nw ? sm.stats[lane].max : -INFINITY;
   const float M = wave_max(mx);
   auto sum_exp = [&]() { return row_stats(sm.stats, nw).sum_exp; };
-  if (L.parts > 1) {
-    // One part of the row: its top k, sorted, and its statistics go where wave_merge_kernel
-    // reads a slice's (slice = part).
-    const double S1 = sum_exp();
-    uint64_t *out = W.cands + (size_t)row * W.row_cand_stride + (size_t)part * L.list_stride;
-    if (lane < k) out[lane] = v[0];
-    if (lane == 0) {
-      SliceStat st;
-      st.max = M;
-      st.count = (uint32_t)k;
-      st.sum = S1;
-      W.stats[(size_t)row * kMaxSplits + part] = st;
+  const int k = min(K, taken);
+  // The taken entries sorted in R registers (entry i = r * 64 + lane), then the part's
+  // hand-over or the row's tail.
+  auto finish = [&](auto &v, auto regs) {
+    constexpr int R = decltype(regs)::value;
+    if (L.parts > 1) {
+      // One part of the row: its top k, sorted, and its statistics go where wave_merge_kernel
+      // reads a slice's (slice = part).
+      const double S1 = sum_exp();
+      uint64_t *out = W.cands + (size_t)row * W.row_cand_stride + (size_t)part * L.list_stride;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (r * kWaveSize + lane < k) out[r * kWaveSize + lane] = v[r];
+      if (lane == 0) {
+        SliceStat st;
+        st.max = M;
+        st.count = (uint32_t)k;
+        st.sum = S1;
+        W.stats[(size_t)row * kMaxSplits + part] = st;
+      }
+      return;
     }
-    return true;
-  }
-  if (!((M > -INFINITY) && (M < INFINITY))) {
-    if (lane == 0) {
-      write_status(L, row, TABBY_EDOMAIN, M, sum_exp());
+    if (!((M > -INFINITY) && (M < INFINITY))) {
+      if (lane == 0) {
+        write_status(L, row, TABBY_EDOMAIN, M, sum_exp());
+        W.row_state[row].status = TABBY_EDOMAIN;
+      }
+      return;
+    }
+    const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * L.vocab;
+    bool in_domain = true;
+    auto S1_of = [&]() {
+      const double S1 = sum_exp();
+      in_domain = (S1 > 0.0) && (S1 < INFINITY);
+      return S1;
+    };
+    if constexpr (R == 1) reg_tail<In>(v[0], k, L, row, row_src, M, S1_of, P);
+    else reg_tail_wide<R, In>(v, k, L, row, row_src, M, S1_of, P, sm.merge.b);
+    if (!in_domain && lane == 0) {
+      write_status(L, row, TABBY_EDOMAIN, M, row_stats(sm.stats, nw).sum_exp);
       W.row_state[row].status = TABBY_EDOMAIN;
     }
-    return true;
-  }
-  const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * L.vocab;
-  bool in_domain = true;
-  reg_tail<In>(v[0], k, L, row, row_src, M,
-               [&]() {
-                 const double S1 = sum_exp();
-                 in_domain = (S1 > 0.0) && (S1 < INFINITY);
-                 return S1;
-               },
-               P);
-  if (!in_domain && lane == 0) {
-    write_status(L, row, TABBY_EDOMAIN, M, row_stats(sm.stats, nw).sum_exp);
-    W.row_state[row].status = TABBY_EDOMAIN;
+  };
+  if (taken <= kWaveSize) {
+    uint64_t v[1] = {lane < taken ? composite_of_raw(sm.sel[lane]) : 0ull};
+    wave_sort_desc<1>(v);
+    finish(v, std::integral_constant<int, 1>{});
+  } else {
+    uint64_t v[2] = {composite_of_raw(sm.sel[lane]),
+                     kWaveSize + lane < taken ? composite_of_raw(sm.sel[kWaveSize + lane]) : 0ull};
+    wave_sort_desc<2>(v);
+    finish(v, std::integral_constant<int, 2>{});
   }
   return true;
 }
