@@ -1048,7 +1048,11 @@ __device__ __forceinline__ uint32_t union_kth(const uint32_t *keys, int total, i
 // counted down from `top` (the largest key of the row's first bound's union; larger keys go
 // to bin 0) to the row's first bound, below which no list entry lies.
 constexpr int kSelBins = 256;
-constexpr int kSmallTake = 2 * kWaveSize;  // finish_small_pool: pools and takes of at most 128
+constexpr int kSmallTake = 4 * kWaveSize;  // finish_small_pool: takes of at most 256
+// Pools up to this size take finish_small_pool: a take is the pool plus the rest of the bin
+// that holds its K-th largest key, and a pool of 256 had no room left for that rest (nearly
+// every row fell back to the sorted merge: 47.5 -> 49.3 us at 256 rows with k = 256).
+constexpr int kSmallPoolMax = kSmallTake - 32;
 
 struct SelBins {
   uint32_t top;
@@ -2568,10 +2572,10 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   const int nw = (int)(blockDim.x / kWaveSize);  // the row's waves, >= kRowMinWaves
   const tabby_row_params P = L.params[row];  // kept in registers for the merge
   const RowPool rp = row_pool(L, P);
-  // Pools of at most 128 skip the waves' end-of-stream sorts and the list merge: the row's top
-  // K is selected from the unsorted lists (finish_small_pool). A part of a row (parts > 1)
-  // only hands its top K on, whatever its pool; a whole row must be finished here.
-  const bool small = rp.valid && rp.K > 0 && rp.K <= kSmallTake && (L.parts > 1 || rp.finite);
+  // Pools of at most kSmallPoolMax skip the waves' end-of-stream sorts and the list merge: the
+  // row's top K is selected from the unsorted lists (finish_small_pool). A part of a row
+  // (parts > 1) only hands its top K on, whatever its pool; a whole row must be finished here.
+  const bool small = rp.valid && rp.K > 0 && rp.K <= kSmallPoolMax && (L.parts > 1 || rp.finite);
   if (threadIdx.x == 0) {
     sm.next_chunk = nw;  // chunk w is wave w's first
     sm.sel_count = 0;
@@ -2637,9 +2641,9 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
   const int total = __builtin_amdgcn_readlane((int)inc, kWaveSize - 1);  // every list entry
   uint32_t take_key = 0u;  // entries with key >= take_key are taken
   int taken = total;
-  // Pools of at most 64 select from more than 64 entries (one register to sort), larger pools
-  // from more than 128; either way total >= K when selecting.
-  if (total > (K <= kWaveSize ? kWaveSize : kSmallTake)) {
+  // A pool selects from more entries than its register class holds (64, 128 or 256: one, two
+  // or four registers to sort); either way total >= K when selecting.
+  if (total > (K <= kWaveSize ? kWaveSize : K <= 2 * kWaveSize ? 2 * kWaveSize : kSmallTake)) {
     const int owner = __ffsll((unsigned long long)__ballot(inc >= (uint32_t)K)) - 1;  // total >= K
     int bin = 0;
     uint32_t upto = 0;
@@ -2662,7 +2666,7 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
     else taken = total;
   }
   if (taken > kSmallTake) {
-    // More than 128 would be taken (ties at the boundary, or a row whose top lies far above
+    // More than 256 would be taken (ties at the boundary, or a row whose top lies far above
     // the first bound's union): sort each list in place for the general merge.
     const int keep = min(count, K);
     if (count <= kWaveSize) store_sorted_top<1>(list, count, keep, sm.wave[w].list);
@@ -2737,11 +2741,20 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
     uint64_t v[1] = {lane < taken ? composite_of_raw(sm.sel[lane]) : 0ull};
     wave_sort_desc<1>(v);
     finish(v, std::integral_constant<int, 1>{});
-  } else {
+  } else if (taken <= 2 * kWaveSize) {
     uint64_t v[2] = {composite_of_raw(sm.sel[lane]),
                      kWaveSize + lane < taken ? composite_of_raw(sm.sel[kWaveSize + lane]) : 0ull};
     wave_sort_desc<2>(v);
     finish(v, std::integral_constant<int, 2>{});
+  } else {
+    uint64_t v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = r * kWaveSize + lane;
+      v[r] = i < taken ? composite_of_raw(sm.sel[i]) : 0ull;
+    }
+    wave_sort_desc<4>(v);
+    finish(v, std::integral_constant<int, 4>{});
   }
   return true;
 }

@@ -624,12 +624,13 @@ def test_exact_boundary_draws(oracle, rows):
     # values are equal, so every weight is 1/K and the running sums are j/K exactly. The
     # cut and the draw then sit on a boundary, where only the sequential sums decide (the
     # fast parallel sums must hand over to the exact ones). 256 rows take the per-row kernel
-    # (pools of 65..128 its two-register tail), 4 rows the parts and the merge kernel.
+    # (pools of 65..256 its two- and four-register tails), 4 rows the parts and the merge
+    # kernel.
     V = 20000
     w = synth.random_workload(rows=rows, vocab=V, seed=211 + rows, k_choices=(4,), temperatures=(1.0,),
                               top_ps=(0.5,), sigma=1.0)
     for r in range(rows):
-        K = (4, 8, 16, 64, 100, 128)[r % 6]
+        K = (4, 8, 16, 64, 100, 128, 200, 256)[r % 8]
         w.logits[r, :] = np.minimum(w.logits[r, :], 3.0)
         pos = (np.arange(K) * 997 + r * 13) % V
         w.logits[r, pos] = 7.5
@@ -638,26 +639,26 @@ def test_exact_boundary_draws(oracle, rows):
         w.top_p[r] = j / K
         w.temperature[r] = (1.0, 0.5, 2.0)[(r // 8) % 3]
         w.uniform[r] = ((r // 24) % K) / K if r % 3 else 0.5
-    res, ids, vals = run_gpu(w, k_max=128, topk_cap=64)
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=64)
     _log(f"exact boundaries, {rows} rows", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
 
 
 @pytest.mark.parametrize("rows", [256, 4])
-def test_small_pool_takes_of_65_to_128(oracle, rows):
-    # Pools of at most 128 are selected from the waves' unsorted lists through a 256-bin key
-    # histogram. Ties at the K-th largest put more entries in its bin than K: 100 or 120 equal
-    # maxima under pools of 50, 64, 100 and 128 take 65..128 entries (sorted in two registers);
-    # 200 equal maxima take more than 128 (the sorted merge); other rows have pools of 65..128
-    # over N(0, 3^2) logits with and without top-p.
+def test_small_pool_takes_of_65_to_256(oracle, rows):
+    # Pools of at most 256 are selected from the waves' unsorted lists through a 256-bin key
+    # histogram. Ties at the K-th largest put more entries in its bin than K: 100, 120, 200 or
+    # 250 equal maxima under pools of 50, 64, 100, 128, 200 and 256 take 65..256 entries
+    # (sorted in two or four registers); 300 equal maxima take more than 256 (the sorted
+    # merge); other rows have pools of 65..256 over N(0, 3^2) logits with and without top-p.
     V = 40000
-    w = synth.random_workload(rows=rows, vocab=V, seed=404 + rows, k_choices=(65, 100, 128),
+    w = synth.random_workload(rows=rows, vocab=V, seed=404 + rows, k_choices=(65, 100, 128, 129, 200, 256),
                               temperatures=(0.6, 1.0, 1.7), top_ps=(0.8, 0.95, 1.0), sigma=3.0)
     for r in range(rows):
         if r % 3 == 0:
-            ties = (100, 120, 200)[(r // 3) % 3]
-            K = (50, 64, 100, 128)[(r // 9) % 4]
+            ties = (100, 120, 200, 250, 300)[(r // 3) % 5]
+            K = (50, 64, 100, 128, 200, 256)[(r // 15) % 6]
             w.logits[r, :] = np.minimum(w.logits[r, :], 4.0)
             w.logits[r, (np.arange(ties) * 331 + r) % V] = 9.0
             w.top_k[r] = K
-    res, ids, vals = run_gpu(w, k_max=128, topk_cap=100)
-    _log(f"small-pool takes of 65..128, {rows} rows", compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=100)
+    _log(f"small-pool takes of 65..256, {rows} rows", compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100))
