@@ -1962,6 +1962,11 @@ template <typename In, class SumExp>
 __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int row, const In *row_src,
                                          float M, SumExp sum_exp_of, const tabby_row_params &P);
 
+template <int R, typename In, class SumExp>
+__device__ __forceinline__ void reg_tail_wide(const uint64_t (&v)[R], int K, const Launch &L, int row,
+                                              const In *row_src, float M, SumExp sum_exp_of,
+                                              const tabby_row_params &P, double *scratch);
+
 // The row's top K, sorted, into sm.sorted[0..K) from its sorted lists (merge_lists_4 in the
 // register class of K; m1: the first 64 entries' loads, already issued). No barrier when
 // K == 0.
@@ -2001,9 +2006,9 @@ __device__ __forceinline__ void merge_row(WaveMergeSmem &sm, const Launch &L, co
 
 // The rest of a row once its pool, sm.sorted[0..K), and its max and sum-exp are known: the
 // f64 tail of sampleFromTopK, the hand-over to the head kernels, or an error status. Wave 0
-// and wave 1 work; every wave of the workgroup must call it. REG: pools of at most 64 take
-// wave 0's reg_tail (the merge kernels; row_kernel's pools of at most 64 end in
-// finish_small_pool, and its code stays as it is).
+// and wave 1 work; every wave of the workgroup must call it. REG: finite pools take wave 0's
+// register tail (the merge kernels; row_kernel's small pools end in finish_small_pool, and
+// its general path keeps the two-wave form).
 template <typename In, bool REG>
 __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, const Workspace &W, int row,
                                             const tabby_row_params &P, const RowPool &rp, float row_max,
@@ -2014,10 +2019,21 @@ __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, 
   const In *row_src = reinterpret_cast<const In *>(L.logits) + (size_t)row * L.vocab;
   const bool in_domain = (row_max > -INFINITY) && (row_max < INFINITY) && (sum_exp > 0.0) &&
                          (sum_exp < INFINITY);
-  if (REG && valid_params && in_domain && finite && K <= kWaveSize) {
-    // Pools of at most 64: one register per lane, wave 0's reg_tail.
+  if (REG && valid_params && in_domain && finite) {
+    // Wave 0's register tail: one, two or four registers per lane.
     if (wave_id() != 0) return;
-    reg_tail<In>(lane < K ? sm.sorted[lane] : 0ull, K, L, row, row_src, row_max, [&]() { return sum_exp; }, P);
+    auto S1_of = [&]() { return sum_exp; };
+    if (K <= kWaveSize) {
+      reg_tail<In>(lane < K ? sm.sorted[lane] : 0ull, K, L, row, row_src, row_max, S1_of, P);
+    } else if (K <= 2 * kWaveSize) {
+      const uint64_t v[2] = {sm.sorted[lane], kWaveSize + lane < K ? sm.sorted[kWaveSize + lane] : 0ull};
+      reg_tail_wide<2, In>(v, K, L, row, row_src, row_max, S1_of, P, sm.b);
+    } else {
+      uint64_t v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = r * kWaveSize + lane < K ? sm.sorted[r * kWaveSize + lane] : 0ull;
+      reg_tail_wide<4, In>(v, K, L, row, row_src, row_max, S1_of, P, sm.b);
+    }
     return;
   }
   if (valid_params && in_domain && finite) {
