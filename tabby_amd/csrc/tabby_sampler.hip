@@ -3980,6 +3980,13 @@ Plan plan_launch(int rows, int vocab, int dtype, const void *logits, int k_max, 
     L.pool_rows = 1;
     L.splits = 1;
     L.slice_len = vocab;
+  } else if (L.kcap <= kWaveKcap && rows * 2 > cus && rows < cus) {
+    // Between half the CUs and all of them: one 16-wave workgroup per row all the same (the
+    // idle CUs leave the others more of the HBM bandwidth). Against the one-wave slices and
+    // their merge kernel: 130 rows 32.5 -> 22.6 us, 200 rows 39.5 -> 26.5 us, 255 rows 43.9 ->
+    // 31.2 us (151,936 f32, k = 50), 200 rows at k = 100 50.6 -> 29.4 us.
+    L.parts = 1;
+    L.row_waves = kRowWaves;
   } else if (per_row_launch(L, cus)) {
     L.parts = 1;
     L.row_waves = std::max(L.splits, kRowMinWaves);  // at least the five the merge uses

@@ -566,14 +566,25 @@ def test_config5_full_512_rows(oracle):
     _log("config5[512 rows]", compare(w, res, ids, vals, run_oracle(oracle, w, 1024), 1024))
 
 
-@pytest.mark.parametrize("rows", [192, 197])
-def test_wave_kernel_batches_between_half_and_all_cus(oracle, rows):
-    # 129-255 rows with pools up to 256 take the one-wave slice kernel and its merge kernel;
-    # 192 rows (a multiple of 8) place each row's slices on the XCD of its merge, 197 do not.
+@pytest.mark.parametrize("rows", [129, 192, 197, 255])
+def test_row_kernel_batches_between_half_and_all_cus(oracle, rows):
+    # 129-255 rows with pools up to 256: one 16-wave workgroup per row, as at 256 rows, with
+    # the other CUs idle; pools of 1 to 224 take the small-pool path, 256 the sorted merge.
     w = synth.config(3, rows=rows)
-    w.top_k[:] = np.resize(np.array([1, 20, 50, 100, 256], np.int32), rows)
+    w.top_k[:] = np.resize(np.array([1, 20, 50, 100, 200, 256], np.int32), rows)
     res, ids, vals = run_gpu(w, k_max=256, topk_cap=100)
-    _log(f"wave kernel {rows} rows", compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100))
+    _log(f"row kernel {rows} rows", compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100))
+
+
+@pytest.mark.parametrize("rows", [64, 61])
+def test_wave_kernel_short_rows(oracle, rows):
+    # Up to half as many rows as CUs whose rows are too short for two parts take the one-wave
+    # slice kernel and its merge kernel; 64 rows (a multiple of 8) place each row's slices on
+    # the XCD of its merge, 61 do not.
+    w = synth.random_workload(rows=rows, vocab=12000, seed=61 + rows, ties=True, neg_inf_frac=0.1,
+                              k_choices=(1, 20, 50, 100, 256), temperatures=(0.0, 0.7, 1.3))
+    res, ids, vals = run_gpu(w, k_max=256, topk_cap=100)
+    _log(f"wave kernel {rows} short rows", compare(w, res, ids, vals, run_oracle(oracle, w, 100), 100))
 
 
 def test_headline_workload_device_form(oracle):
