@@ -74,6 +74,35 @@ __device__ __forceinline__ double wave_inclusive_scan(double x) {
   return x + below;
 }
 
+// The DPP move of control `ctrl` applied to both halves of v; rows outside row_mask get 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROW_MASK, 0xF, false);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Two independent inclusive prefix sums over the wave's lanes, interleaved stage by stage so
+// that each one's DPP moves fill the other's latency: within rows of 16 by row shifts, then
+// row_bcast:15 (lane 15 of each row added to the next row: rows 1 and 3) and row_bcast:31
+// (lane 31 added to rows 2 and 3). Lane i's sum is a tree of at most six roundings over lanes
+// 0..i (for integer-valued terms below 2^53 it is exact).
+__device__ __forceinline__ void wave_inclusive_scan2(double &a, double &b) {
+  a += row_shift_up<1>(a);
+  b += row_shift_up<1>(b);
+  a += row_shift_up<2>(a);
+  b += row_shift_up<2>(b);
+  a += row_shift_up<4>(a);
+  b += row_shift_up<4>(b);
+  a += row_shift_up<8>(a);
+  b += row_shift_up<8>(b);
+  a += dpp_f64<0x142, 0xA>(a);  // row_bcast:15
+  b += dpp_f64<0x142, 0xA>(b);
+  a += dpp_f64<0x143, 0xC>(a);  // row_bcast:31
+  b += dpp_f64<0x143, 0xC>(b);
+}
+
 // Parity maps x -> (x & k) ^ c on {0, 1}, encoded k | c << 1; kParityId is the identity.
 constexpr uint32_t kParityId = 1u;
 

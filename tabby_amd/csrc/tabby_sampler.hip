@@ -2131,6 +2131,8 @@ struct RowSmem {
   uint32_t sel_hist[kSelBins];
   uint64_t sel[kSmallTake];
   int sel_count;
+  int done;              // waves finished streaming (the last one selects the take)
+  uint32_t sel_take[2];  // the take's smallest key and its size
   uint32_t bound_key[2];  // the row's first bound and the largest key of its union
 };
 
@@ -2158,16 +2160,20 @@ __device__ __forceinline__ Draw draw_of(double running, int K, double top_p, dou
 // sampleFromTopK (src/engine/sampler.ts:147-212) over a pool of K <= 64 candidates sorted
 // descending one per lane (lane i holds the i-th largest composite), by one wave in registers.
 // The reference's sums are sequential left-to-right f64 sums and the cut and the draw depend
-// on their last bits. Here the terms come from exp_nonpos (within 8 ulp of exp) and every sum
-// is a parallel prefix (wave_inclusive_scan: each partial sum a tree of at most seven
-// roundings). Against the reference's sequential sums of its exact terms, the weights then
-// differ by less than 82 * 2^-53 relative and their running sums by less than 2^-45.6 of
-// their value: when every comparison that decides the cut and the draw clears its threshold
-// by more than 2^-36 relative, the reference decides the same way. Otherwise the weights are
-// recomputed with V8's exp (fdlibm) and summed bit for bit (reg_seq_sum), and decided again.
-// poolMass and the probability (compared within 1e-5) keep the fast terms. T <= 0 is greedy
-// (sampler.ts:159-167). S1 is the row's sum-exp, obtained after the terms (its loads overlap
-// them).
+// on their last bits. Here the terms s_i come from exp_nonpos (within 8 ulp of exp), their
+// prefix sums P_i from one parallel scan (wave_inclusive_scan2: a tree of at most six
+// roundings, interleaved with the scan of the exact terms for poolMass), and the running sum
+// of the weights is P_i / P_(K-1), within 29 * 2^-53 of the exact ratio. The reference's
+// running sums of its weights (V8's exp within an ulp, then K sequential roundings for the
+// total, one for each weight, i for the running sum) are within 130 * 2^-53 of the same
+// ratio, so the two differ by less than 2^-45.6 of their value: when every comparison that
+// decides the cut and the draw clears its threshold by more than 2^-36 relative, the
+// reference decides the same way. Each lane checks its own running sum against the
+// comparisons it takes part in (the cut's and the chosen entry's, and those just below them)
+// and one ballot collects the failures. Otherwise the weights are recomputed with V8's exp
+// (fdlibm) and summed bit for bit (reg_seq_sum), and decided again. poolMass and the
+// probability (compared within 1e-5) keep the fast terms. T <= 0 is greedy
+// (sampler.ts:159-167). S1 is the row's sum-exp (the caller may have computed it already).
 template <typename In, class SumExp>
 __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int row, const In *row_src,
                                          float M, SumExp sum_exp_of, const tabby_row_params &P) {
@@ -2179,7 +2185,9 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
   const double s = !(in && T > 0.0) ? 0.0 : T == 1.0 ? e1 : exp_nonpos(d / T);
   const double S1 = sum_exp_of();
   const double exact = e1 / S1;
-  const double pool = lane_f64(wave_inclusive_scan(exact), K - 1);
+  double pe = exact, ps = s;
+  wave_inclusive_scan2(pe, ps);  // lanes >= K add zeros
+  const double pool = lane_f64(pe, K - 1);
   tabby_row_result res;
   res.max_logit = M;
   res.sum_exp = S1;
@@ -2192,25 +2200,23 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
     res.pool_exhausted = 0;
   } else {
     const double top_p = P.top_p;
-    const double scaled = lane_f64(wave_inclusive_scan(s), K - 1);
-    const double running = wave_inclusive_scan(in ? s / scaled : 0.0);
+    const double scaled = lane_f64(ps, K - 1);
+    const double running = in ? ps / scaled : 0.0;
     Draw dr = draw_of(running, K, top_p, P.uniform);
     // Margins of every comparison that fixed the cut and the draw (running sums are
-    // non-decreasing, so the neighbours of each boundary are the only ones to check).
+    // non-decreasing, so the neighbours of each boundary are the only ones to check), each
+    // lane testing the ones its own running sum decides.
     constexpr double kMargin = 1.0 / 68719476736.0;  // 2^-36
-    const double r_cut = lane_f64(running, dr.cut - 1);
-    const double r_before = dr.cut >= 2 ? lane_f64(running, dr.cut - 2) : 0.0;
-    bool clear = true;
+    bool fail = false;
     if (top_p < 1.0) {
       const double m = kMargin * top_p;
-      clear = (dr.cut < K || r_cut < top_p - m) &&
-              (dr.cut == K || (r_cut >= top_p + m && (dr.cut == 1 || r_before < top_p - m)));
+      if (dr.cut == K) fail = lane == K - 1 && !(running < top_p - m);
+      else fail = (lane == dr.cut - 1 && !(running >= top_p + m)) || (lane == dr.cut - 2 && !(running < top_p - m));
     }
-    const double r_hi = lane_f64(running, dr.chosen);
-    const double r_lo = dr.chosen >= 1 ? lane_f64(running, dr.chosen - 1) : 0.0;
     const double m2 = kMargin * dr.total;
-    clear = clear && r_hi > dr.target + m2 && (dr.chosen == 0 || r_lo < dr.target - m2);
-    if (!__builtin_amdgcn_readfirstlane((int)clear)) {
+    fail = fail || (lane == dr.chosen && !(running > dr.target + m2)) ||
+           (lane == dr.chosen - 1 && !(running < dr.target - m2));
+    if (__ballot(fail)) {
       // Bit for bit: V8's exp for the weights, sequential sums (sampler.ts:170-203).
       const double se = in ? fdlibm_exp_inline(d / T) : 0.0;
       double partial;
@@ -2578,6 +2584,7 @@ __global__ __launch_bounds__(kBlock) void lmhead_merge_kernel(Launch L, Workspac
 template <typename In>
 __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, const Workspace &W, int row, int part,
                                   const tabby_row_params &P, const RowPool &rp, int nw);
+__device__ __forceinline__ void small_pool_select(RowSmem &sm, int K);
 
 template <typename In, int VEC>
 __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Workspace W) {
@@ -2595,11 +2602,19 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   if (threadIdx.x == 0) {
     sm.next_chunk = nw;  // chunk w is wave w's first
     sm.sel_count = 0;
+    sm.done = 0;
   }
   for (int i = (int)threadIdx.x; i < kSelBins; i += (int)blockDim.x) sm.sel_hist[i] = 0u;
   __syncthreads();
   wave_slice<In, VEC, true>(sm.wave[w], L, P, row, w, part, sm.wave[w].list, &sm.stats[w], &sm.next_chunk,
                             sm.bound_keys, nw, !small, sm.bound_key, small ? sm.sel_hist : nullptr);
+  if (small) {
+    // The last wave to finish selects the take. Each wave's histogram adds precede its
+    // increment of sm.done in the LDS's order, so the last increment sees every add.
+    int last = 0;
+    if (wave_lane() == 0) last = atomicAdd(&sm.done, 1) == nw - 1 ? 1 : 0;
+    if (__builtin_amdgcn_readfirstlane(last)) small_pool_select(sm, rp.K);
+  }
   __syncthreads();
   if (small && finish_small_pool<In>(sm, L, W, row, part, P, rp, nw)) return;
   constexpr int stride = (int)(sizeof(WaveSmem) / sizeof(uint64_t));
@@ -2637,15 +2652,14 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   finish_pool<In>(sm.merge, L, W, row, P, rp, sm.merge.row_max, sm.merge.row_sum);
 }
 
-template <typename In>
-__device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, const Workspace &W, int row, int part,
-                                                  const tabby_row_params &P, const RowPool &rp, int nw) {
-  const int w = wave_id(), lane = wave_lane();
-  const int K = rp.K;
-  const uint64_t *list = sm.wave[w].list;  // raw entries: value bits << 32 | ~index
-  const int count = (int)sm.stats[w].count;
-  // The bin holding the K-th largest key, from the top of the histogram the waves filled as
-  // they finished (four bins per lane; every wave computes the same).
+// The take of a row whose pool is at most kSmallPoolMax (finish_small_pool): the bin holding
+// the K-th largest key, from the top of the histogram the waves filled as they finished (four
+// bins per lane), gives the smallest key taken and the number of entries at or above it
+// (every list entry when the union is small enough to take whole). One wave computes it --
+// the row's last to finish streaming, while the others wait at the barrier -- and leaves
+// both in sm.sel_take.
+__device__ __forceinline__ void small_pool_select(RowSmem &sm, int K) {
+  const int lane = wave_lane();
   const SelBins sb = sel_bins(sm.bound_key[1], sm.bound_key[0]);
   uint32_t h[4], sum = 0;
 #pragma unroll
@@ -2681,6 +2695,22 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
     if (bin < kSelBins - 1) take_key = sb.lowest(bin);
     else taken = total;
   }
+  if (lane == 0) {
+    sm.sel_take[0] = take_key;
+    sm.sel_take[1] = (uint32_t)taken;
+  }
+}
+
+template <typename In>
+__device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, const Workspace &W, int row, int part,
+                                                  const tabby_row_params &P, const RowPool &rp, int nw) {
+  const int w = wave_id(), lane = wave_lane();
+  const int K = rp.K;
+  const uint64_t *list = sm.wave[w].list;  // raw entries: value bits << 32 | ~index
+  const int count = (int)sm.stats[w].count;
+  // The take, selected by the row's last wave to finish streaming (small_pool_select).
+  const uint32_t take_key = (uint32_t)__builtin_amdgcn_readfirstlane((int)sm.sel_take[0]);
+  const int taken = __builtin_amdgcn_readfirstlane((int)sm.sel_take[1]);
   if (taken > kSmallTake) {
     // More than 256 would be taken (ties at the boundary, or a row whose top lies far above
     // the first bound's union): sort each list in place for the general merge.
@@ -2707,9 +2737,11 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
   }
   __syncthreads();
   if (w != 0) return true;
-  float mx = lane < nw ? sm.stats[lane].max : -INFINITY;
-  const float M = wave_max(mx);
-  auto sum_exp = [&]() { return row_stats(sm.stats, nw).sum_exp; };
+  // The row's statistics: independent of the sort below, which they share a block with.
+  const RowStats rs = row_stats(sm.stats, nw);
+  const float M = rs.max;
+  const double S1 = rs.sum_exp;
+  auto sum_exp = [&]() { return S1; };
   const int k = min(K, taken);
   // The taken entries sorted in R registers (entry i = r * 64 + lane), then the part's
   // hand-over or the row's tail.
@@ -2749,7 +2781,7 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
     if constexpr (R == 1) reg_tail<In>(v[0], k, L, row, row_src, M, S1_of, P);
     else reg_tail_wide<R, In>(v, k, L, row, row_src, M, S1_of, P, sm.merge.b);
     if (!in_domain && lane == 0) {
-      write_status(L, row, TABBY_EDOMAIN, M, row_stats(sm.stats, nw).sum_exp);
+      write_status(L, row, TABBY_EDOMAIN, M, S1);
       W.row_state[row].status = TABBY_EDOMAIN;
     }
   };
