@@ -2131,8 +2131,11 @@ struct RowSmem {
   uint32_t sel_hist[kSelBins];
   uint64_t sel[kSmallTake];
   int sel_count;
-  int done;              // waves finished streaming (the last one selects the take)
+  uint32_t fin_mask;     // the waves finished streaming (the last one selects the take)
   uint32_t sel_take[2];  // the take's smallest key and its size
+  uint32_t part_mask;    // the waves whose statistics the second-to-last one combined ...
+  float part_max;        // ... their max
+  double part_sum;       // ... and sum-exp against it
   uint32_t bound_key[2];  // the row's first bound and the largest key of its union
 };
 
@@ -2602,18 +2605,37 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   if (threadIdx.x == 0) {
     sm.next_chunk = nw;  // chunk w is wave w's first
     sm.sel_count = 0;
-    sm.done = 0;
+    sm.fin_mask = 0u;
   }
   for (int i = (int)threadIdx.x; i < kSelBins; i += (int)blockDim.x) sm.sel_hist[i] = 0u;
   __syncthreads();
   wave_slice<In, VEC, true>(sm.wave[w], L, P, row, w, part, sm.wave[w].list, &sm.stats[w], &sm.next_chunk,
                             sm.bound_keys, nw, !small, sm.bound_key, small ? sm.sel_hist : nullptr);
   if (small) {
-    // The last wave to finish selects the take. Each wave's histogram adds precede its
-    // increment of sm.done in the LDS's order, so the last increment sees every add.
-    int last = 0;
-    if (wave_lane() == 0) last = atomicAdd(&sm.done, 1) == nw - 1 ? 1 : 0;
-    if (__builtin_amdgcn_readfirstlane(last)) small_pool_select(sm, rp.K);
+    // Each wave marks itself finished; the waves marked before it are in the returned mask.
+    // Its histogram adds and statistics precede the mark in the LDS's order, so the last
+    // wave sees every add, and the second-to-last every other wave's statistics: it combines
+    // them while the last one streams and selects the take.
+    uint32_t before = 0;
+    if (wave_lane() == 0) before = atomicOr(&sm.fin_mask, 1u << w);
+    before = (uint32_t)__builtin_amdgcn_readfirstlane((int)before);
+    const int rank = __popc(before);
+    if (rank == nw - 1) {
+      small_pool_select(sm, rp.K);
+    } else if (rank == nw - 2) {
+      const uint32_t mask = before | (1u << w);
+      const int lane = wave_lane();
+      const bool mine = lane < nw && ((mask >> lane) & 1u);
+      const SliceStat st = mine ? sm.stats[lane] : SliceStat{-INFINITY, 0u, 0.0};
+      const float mx = wave_max(st.max);
+      const double part = st.max == -INFINITY ? 0.0 : st.sum * (double)__builtin_amdgcn_exp2f((st.max - mx) * kLog2e);
+      const double sum = wave_sum(part);
+      if (lane == 0) {
+        sm.part_mask = mask;
+        sm.part_max = mx;
+        sm.part_sum = sum;
+      }
+    }
   }
   __syncthreads();
   if (small && finish_small_pool<In>(sm, L, W, row, part, P, rp, nw)) return;
@@ -2737,10 +2759,17 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
   }
   __syncthreads();
   if (w != 0) return true;
-  // The row's statistics: independent of the sort below, which they share a block with.
-  const RowStats rs = row_stats(sm.stats, nw);
-  const float M = rs.max;
-  const double S1 = rs.sum_exp;
+  // The row's statistics: the second-to-last wave's combination and the one wave it missed.
+  float M = sm.part_max;
+  double S1 = sm.part_sum;
+  const uint32_t missed = ((1u << nw) - 1u) & ~sm.part_mask;
+  if (missed) {
+    const SliceStat st = sm.stats[__ffs(missed) - 1];
+    const float mx = fmaxf(M, st.max);
+    S1 = (M == -INFINITY ? 0.0 : S1 * (double)__builtin_amdgcn_exp2f((M - mx) * kLog2e)) +
+         (st.max == -INFINITY ? 0.0 : st.sum * (double)__builtin_amdgcn_exp2f((st.max - mx) * kLog2e));
+    M = mx;
+  }
   auto sum_exp = [&]() { return S1; };
   const int k = min(K, taken);
   // The taken entries sorted in R registers (entry i = r * 64 + lane), then the part's

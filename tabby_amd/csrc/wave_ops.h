@@ -96,17 +96,16 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 
 // Inclusive prefix sum over the wave's lanes in lane order: DPP row shifts (0 shifted in)
-// within each 16-lane row, then the totals of the rows below from three readlanes.
+// within each 16-lane row, then row_bcast:15 (lane 15 of each row added to the next row: rows
+// 1 and 3) and row_bcast:31 (lane 31 added to rows 2 and 3).
 __device__ __forceinline__ uint32_t wave_inclusive_scan_u32(uint32_t x) {
   x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, true);  // row_shr:1
   x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, true);  // row_shr:2
   x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, true);  // row_shr:4
   x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, true);  // row_shr:8
-  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
-  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 31);
-  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 47);
-  const int row = wave_lane() >> 4;
-  return x + (row == 0 ? 0u : row == 1 ? r0 : row == 2 ? r0 + r1 : r0 + r1 + r2);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return x;
 }
 
 // Makes this wave's LDS writes visible to its other lanes (LDS operations of one wave
