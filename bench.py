@@ -10,6 +10,8 @@ host in the same run.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
        python bench.py --config N | --host-params | --read-ceiling | --greedy | --softmax
                        (secondary measurements, one JSON line each)
+       python bench.py --timeline  (the headline row kernel's phase times, from the timeline
+                       build of the library: tabby_amd/lib/libtabby_sampler_timeline.so)
 """
 from __future__ import annotations
 
@@ -63,6 +65,10 @@ def parse_args():
                          "against the unfused pair (tabby_lmhead_q4_device, then the sampler) on "
                          "Qwen2.5-0.5B's lm_head shape (151,936 x 896 int4, block 32), one decode "
                          "row (--rows up to 8); a secondary measurement")
+    ap.add_argument("--timeline", action="store_true",
+                    help="run the headline workload on the timeline build of the library (the "
+                         "row kernel with phase timestamps compiled in) and print the phases' "
+                         "percentiles over the rows of the last call, in us; a diagnostic")
     ap.add_argument("--softmax", action="store_true",
                     help="time the attention row softmax (tabby_softmax_rows_device) on a "
                          "prefill shape: 14 heads x 512 queries over 512 positions, causal; a "
@@ -289,10 +295,87 @@ def cpu_baseline(w, seconds: float) -> dict | None:
     }
 
 
+def timeline(args) -> int:
+    """--timeline: the headline's row_kernel phases, from the timeline library's stamps."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from tabby_amd import build as B
+    from tabby_amd import sampler as S
+    from tabby_amd import synth
+
+    lib = S.load_library(B.TIMELINE_LIB_PATH)  # before anything loads the plain library
+    lib.tabby_debug_timeline.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.tabby_debug_timeline.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = synth.config(3, rows=args.rows, vocab=args.vocab)
+    w.top_k[:] = args.top_k
+    w.top_p[:] = args.top_p
+    base = torch.from_numpy(w.logits).to(dev)
+    params = np.zeros(w.rows, dtype=S.PARAMS_DTYPE)
+    params["temperature"], params["top_p"] = w.temperature, w.top_p
+    params["uniform"], params["top_k"] = w.uniform, w.top_k
+    buffers, pbufs = [], []
+    for b in range(ROTATE):
+        shift = (b * 61) % w.rows
+        buffers.append(torch.roll(base, shifts=shift, dims=0).contiguous())
+        pbufs.append(torch.from_numpy(np.roll(params, shift).view(np.uint8).copy()).to(dev))
+    results = torch.zeros(w.rows * S.RESULT_DTYPE.itemsize, dtype=torch.uint8, device=dev)
+    sampler = S.GpuSampler(vocab_max=w.vocab, rows_max=w.rows, k_max=max(64, int(w.top_k.max())))
+    stream = torch.cuda.current_stream()
+    for i in range(args.warmup + args.steps):
+        sampler.sample_device(buffers[i % ROTATE], pbufs[i % ROTATE], results, stream=stream)
+    torch.cuda.synchronize()
+    slots, groups = 32, 1024
+    tl = np.zeros(groups * slots, dtype=np.uint64)
+    if lib.tabby_debug_timeline(tl.ctypes.data, tl.nbytes) != 0:
+        print("bench: tabby_debug_timeline failed", file=sys.stderr)
+        return 1
+    tl = tl.reshape(groups, slots)[: w.rows].astype(np.int64)
+    start, rt0, rt1 = tl[:, 16], tl[:, 24], tl[:, 25]
+    # Shader-clock ticks per us, from each row's start-to-end in both clocks (real time: 100 MHz).
+    rate = float(np.median((tl[:, 21] - start) / ((rt1 - rt0) * 1e-2)))
+    waves = (tl[:, :16] - start[:, None]) / rate
+    last = waves.max(1)
+
+    def pct(a):
+        return {p: round(float(np.percentile(a, q)), 2) for p, q in (("p0", 0), ("p50", 50), ("max", 100))}
+
+    phases = {
+        "first_bound_ready": pct((tl[:, 22] - start) / rate),
+        "first_wave_stream_end": pct(waves.min(1)),
+        "last_wave_stream_end": pct(last),
+        "selection_by_last_wave": pct((tl[:, 29] - start) / rate - last),
+        "first_tail_barrier_passed": pct((tl[:, 17] - start) / rate - last),
+        "take": pct((tl[:, 18] - tl[:, 17]) / rate),
+        "second_tail_barrier": pct((tl[:, 19] - tl[:, 18]) / rate),
+        "stats_fold_and_sort": pct((tl[:, 20] - tl[:, 19]) / rate),
+        "register_tail": pct((tl[:, 21] - tl[:, 20]) / rate),
+        "tail_after_last_wave": pct((tl[:, 21] - start) / rate - last),
+        "row_end": pct((rt1 - rt0.min()) * 1e-2),
+    }
+    print(json.dumps({
+        "metric": "row_kernel phase times (us from each row's start; tail phases as durations), "
+                  f"headline workload, last of {args.warmup + args.steps} calls",
+        "unit": "us", "rows": w.rows, "vocab": w.vocab, "shader_clock_mhz": round(rate, 1),
+        "phases": phases,
+        "library": os.path.relpath(B.TIMELINE_LIB_PATH, ROOT),
+    }))
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.copy_calibration:
         return copy_calibration()
+    if args.timeline:
+        if args.gpus != 1:
+            print("bench.py measures one GPU only", file=sys.stderr)
+            return 2
+        return timeline(args)
     if args.read_ceiling or args.greedy or args.softmax or args.lmhead:
         if args.gpus != 1:
             print("bench.py measures one GPU only", file=sys.stderr)

@@ -3,10 +3,12 @@
 * ``tabby_amd/lib/libtabby_sampler.so`` -- the HIP kernels and the C ABI of
   ``include/tabby_sampler.h``, compiled for gfx950 with hipcc (every ``csrc/*.hip``, one
   object each under ``tabby_amd/_build/``, then linked).
+* ``tabby_amd/lib/libtabby_sampler_timeline.so`` -- the same, with the row kernel's phase
+  timestamps compiled in (``-DTABBY_TIMELINE``), read by ``bench.py --timeline`` only.
 * ``tabby_amd/node/build/tabby_sampler.node`` -- the N-API addon that exposes the C ABI to
   Node (g++ against ``/usr/include/node``), when the Node headers are present.
 
-Run ``python -m tabby_amd.build``. Both outputs are rebuilt on every call.
+Run ``python -m tabby_amd.build``. All outputs are rebuilt on every call.
 """
 from __future__ import annotations
 
@@ -21,6 +23,9 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libtabby_sampler.so")
+# The same library with the row kernel's phase timestamps compiled in (TABBY_TIMELINE), for
+# `bench.py --timeline`; nothing else loads it.
+TIMELINE_LIB_PATH = os.path.join(LIB_DIR, "libtabby_sampler_timeline.so")
 OBJ_DIR = os.path.join(PKG, "_build")
 NODE_DIR = os.path.join(PKG, "node")
 NODE_ADDON = os.path.join(NODE_DIR, "build", "tabby_sampler.node")
@@ -55,34 +60,46 @@ def sources() -> list:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compiles each csrc/*.hip to an object in parallel, then links the shared library."""
-    os.makedirs(OBJ_DIR, exist_ok=True)
-    hipcc = _hipcc()
-    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
-    jobs = []
-    for src in sources():
-        obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + ".o")
-        cmd = [hipcc, *compile_flags, "-c", "-o", obj, src]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        jobs.append((cmd, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
-                                                text=True)))
-    objs = []
-    for cmd, obj, proc in jobs:
-        _, err = proc.communicate()
-        if proc.returncode != 0:
-            raise RuntimeError(f"hipcc failed ({proc.returncode}) on {cmd[-1]}:\n{err[-6000:]}")
-        objs.append(obj)
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
+def _link(hipcc: str, objs: list, path: str, verbose: bool) -> None:
+    tmp = path + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc (link) failed ({r.returncode}):\n{r.stderr[-6000:]}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compiles each csrc/*.hip to an object in parallel, then links the shared library, and
+    the timeline variant (tabby_sampler.hip again with TABBY_TIMELINE, the other objects
+    shared)."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    hipcc = _hipcc()
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = []
+    for src in sources():
+        obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + ".o")
+        jobs.append(([hipcc, *compile_flags, "-c", "-o", obj, src], obj))
+    main_src = os.path.join(CSRC, "tabby_sampler.hip")
+    timeline_obj = os.path.join(OBJ_DIR, "tabby_sampler_timeline.o")
+    jobs.append(([hipcc, *compile_flags, "-DTABBY_TIMELINE", "-c", "-o", timeline_obj, main_src], timeline_obj))
+    procs = []
+    for cmd, obj in jobs:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    objs = []
+    for cmd, obj, proc in procs:
+        _, err = proc.communicate()
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({proc.returncode}) on {cmd[-1]}:\n{err[-6000:]}")
+        objs.append(obj)
+    os.makedirs(LIB_DIR, exist_ok=True)
+    main_obj = os.path.join(OBJ_DIR, "tabby_sampler.o")
+    _link(hipcc, [o for o in objs if o != timeline_obj], LIB_PATH, verbose)
+    _link(hipcc, [o for o in objs if o != main_obj], TIMELINE_LIB_PATH, verbose)
     return LIB_PATH
 
 

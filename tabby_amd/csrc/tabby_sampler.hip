@@ -49,6 +49,38 @@
 #include "tabby_sampler.h"
 #include "abi_internal.h"
 
+// Phase timestamps of row_kernel, compiled in only for the timeline library (TABBY_TIMELINE,
+// read by tabby_debug_timeline): per workgroup, kTimelineSlots 64-bit stamps, s_memtime
+// (shader clock) or s_memrealtime (100 MHz). Slots 0-15: each wave's stream end; 16/24: the
+// workgroup's start (shader clock / real time); 22: the first bound ready (wave 0); 29: the
+// last wave's take selection done; 30: the second-to-last wave's statistics done; 17: past
+// the first tail barrier, 18: the take done, 19: past the second barrier (wave 0); 20: the
+// sort done; 21/25: the row finished (shader clock / real time).
+#ifdef TABBY_TIMELINE
+namespace tabby {
+constexpr int kTimelineSlots = 32;
+constexpr int kTimelineGroups = 1024;
+__device__ unsigned long long g_timeline[kTimelineGroups * kTimelineSlots];
+}  // namespace tabby
+#define TABBY_STAMP(slot)                                                                        \
+  do {                                                                                           \
+    if (wave_lane() == 0 && blockIdx.x < kTimelineGroups)                                        \
+      g_timeline[(size_t)blockIdx.x * kTimelineSlots + (slot)] = __builtin_amdgcn_s_memtime();   \
+  } while (0)
+#define TABBY_STAMP_REAL(slot)                                                                   \
+  do {                                                                                           \
+    if (wave_lane() == 0 && blockIdx.x < kTimelineGroups)                                        \
+      g_timeline[(size_t)blockIdx.x * kTimelineSlots + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define TABBY_STAMP(slot) \
+  do {                    \
+  } while (0)
+#define TABBY_STAMP_REAL(slot) \
+  do {                         \
+  } while (0)
+#endif
+
 namespace tabby {
 
 constexpr float kLog2e = 1.44269504088896340736f;
@@ -1240,6 +1272,7 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
       theta_key = max(theta_key, t);
       theta = value_of(theta_key);
       union_top = max(union_top, theta_key);
+      if (slice == 0) TABBY_STAMP(22);
       if (bound_out && slice == 0 && wave_lane() == 0) {
         bound_out[0] = theta_key;
         bound_out[1] = union_top;
@@ -2602,6 +2635,10 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   // row's top K is selected from the unsorted lists (finish_small_pool). A part of a row
   // (parts > 1) only hands its top K on, whatever its pool; a whole row must be finished here.
   const bool small = rp.valid && rp.K > 0 && rp.K <= kSmallPoolMax && (L.parts > 1 || rp.finite);
+  if (w == 0) {
+    TABBY_STAMP(16);
+    TABBY_STAMP_REAL(24);
+  }
   if (threadIdx.x == 0) {
     sm.next_chunk = nw;  // chunk w is wave w's first
     sm.sel_count = 0;
@@ -2611,6 +2648,7 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   __syncthreads();
   wave_slice<In, VEC, true>(sm.wave[w], L, P, row, w, part, sm.wave[w].list, &sm.stats[w], &sm.next_chunk,
                             sm.bound_keys, nw, !small, sm.bound_key, small ? sm.sel_hist : nullptr);
+  TABBY_STAMP(w);
   if (small) {
     // Each wave marks itself finished; the waves marked before it are in the returned mask.
     // Its histogram adds and statistics precede the mark in the LDS's order, so the last
@@ -2622,6 +2660,7 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
     const int rank = __popc(before);
     if (rank == nw - 1) {
       small_pool_select(sm, rp.K);
+      TABBY_STAMP(29);
     } else if (rank == nw - 2) {
       const uint32_t mask = before | (1u << w);
       const int lane = wave_lane();
@@ -2635,9 +2674,11 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
         sm.part_max = mx;
         sm.part_sum = sum;
       }
+      TABBY_STAMP(30);
     }
   }
   __syncthreads();
+  if (w == 0) TABBY_STAMP(17);
   if (small && finish_small_pool<In>(sm, L, W, row, part, P, rp, nw)) return;
   constexpr int stride = (int)(sizeof(WaveSmem) / sizeof(uint64_t));
   const RowLists lists{sm.wave[0].list, nw, stride, (int64_t)nw * stride};
@@ -2757,8 +2798,10 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
       if (take) sm.sel[at + (int)lanes_below(mask)] = e;
     }
   }
+  if (w == 0) TABBY_STAMP(18);
   __syncthreads();
   if (w != 0) return true;
+  TABBY_STAMP(19);
   // The row's statistics: the second-to-last wave's combination and the one wave it missed.
   float M = sm.part_max;
   double S1 = sm.part_sum;
@@ -2817,7 +2860,10 @@ __device__ __forceinline__ bool finish_small_pool(RowSmem &sm, const Launch &L, 
   if (taken <= kWaveSize) {
     uint64_t v[1] = {lane < taken ? composite_of_raw(sm.sel[lane]) : 0ull};
     wave_sort_desc<1>(v);
+    TABBY_STAMP(20);
     finish(v, std::integral_constant<int, 1>{});
+    TABBY_STAMP(21);
+    TABBY_STAMP_REAL(25);
   } else if (taken <= 2 * kWaveSize) {
     uint64_t v[2] = {composite_of_raw(sm.sel[lane]),
                      kWaveSize + lane < taken ? composite_of_raw(sm.sel[kWaveSize + lane]) : 0ull};
@@ -4115,6 +4161,17 @@ int check_common(tabby_sampler *h, const void *logits, int32_t dtype, int32_t ro
 }  // namespace
 
 extern "C" {
+
+#ifdef TABBY_TIMELINE
+// The timeline library only (not part of the drop-in boundary): copies the row kernel's phase
+// stamps (kTimelineGroups x kTimelineSlots uint64, see TABBY_STAMP) to host memory.
+TABBY_API int tabby_debug_timeline(void *host, size_t bytes) {
+  if (bytes > sizeof(unsigned long long) * tabby::kTimelineGroups * tabby::kTimelineSlots) return TABBY_EINVAL;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(tabby::g_timeline), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess
+             ? TABBY_OK
+             : TABBY_EHIP;
+}
+#endif
 
 const char *tabby_last_error(void) { return g_last_error.c_str(); }
 

@@ -52,6 +52,17 @@ def test_library_exports_every_declared_symbol():
     assert tabby == set(declared_symbols()), tabby ^ set(declared_symbols())
 
 
+def test_timeline_library_adds_only_its_reader():
+    # The timeline build (row kernel phase stamps for bench.py --timeline) exports the same
+    # boundary plus tabby_debug_timeline; the plain library does not export the reader.
+    assert os.path.exists(B.TIMELINE_LIB_PATH), "build the library first (python -m tabby_amd.build)"
+    out = subprocess.run(["nm", "-D", "--defined-only", B.TIMELINE_LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    tabby = {s for s in exported if s.startswith("tabby_")}
+    assert tabby == set(declared_symbols()) | {"tabby_debug_timeline"}
+
+
 def test_version_and_last_error_are_callable_without_a_device():
     lib = S.load_library()
     assert lib.tabby_version().decode().startswith("tabby")
