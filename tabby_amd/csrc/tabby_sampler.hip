@@ -2283,11 +2283,12 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
 }
 
 // reg_tail for pools of 65..64R (R registers per lane; entry i = r * 64 + lane, sorted
-// descending over i). The sums are the wave's scans of each register plus the totals of the
-// registers before it (each partial sum a tree of at most 7 + R - 1 roundings; with n <= 256
-// the running sums stay within 2^-42 of the reference's), the cut and the draw the first
-// matching entry over the registers in order, and the same 2^-36 margins decide whether the
-// result stands. Otherwise the weights are recomputed with V8's exp and summed bit for bit
+// descending over i). The prefix sums are the wave's scans of each register (the exact and
+// the scaled terms' interleaved) plus the totals of the registers before it (each a tree of
+// at most 6 + R - 1 roundings), the running sums of the weights P_i / P_(K-1); with n <= 256
+// they stay within 2^-42 of the reference's. The cut and the draw are the first matching
+// entry over the registers in order, and the same 2^-36 margins, checked by each lane for its
+// own entries and collected by one ballot, decide whether the result stands. Otherwise the weights are recomputed with V8's exp and summed bit for bit
 // through `scratch` (LDS, >= 64R doubles; wave_seq_sum). The caller's top-k list and the
 // result as in reg_tail.
 template <int R, typename In, class SumExp>
@@ -2296,6 +2297,7 @@ __device__ __forceinline__ void reg_tail_wide(const uint64_t (&v)[R], int K, con
                                               const tabby_row_params &P, double *scratch) {
   const int lane = wave_lane();
   const double T = P.temperature;
+  const double S1 = sum_exp_of();  // first: its loads and chain overlap the exps below
   double d[R], e1[R], s[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -2304,17 +2306,6 @@ __device__ __forceinline__ void reg_tail_wide(const uint64_t (&v)[R], int K, con
     e1[r] = in ? exp_nonpos(d[r]) : 0.0;
     s[r] = !(in && T > 0.0) ? 0.0 : T == 1.0 ? e1[r] : exp_nonpos(d[r] / T);
   }
-  const double S1 = sum_exp_of();
-  // Inclusive prefix sums over i = r * 64 + lane.
-  auto scan = [&](const double(&x)[R], double(&out)[R]) {
-    double carry = 0.0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const double inc = wave_inclusive_scan(x[r]);
-      out[r] = r == 0 ? inc : carry + inc;
-      carry = r == 0 ? lane_f64(inc, kWaveSize - 1) : carry + lane_f64(inc, kWaveSize - 1);
-    }
-  };
   // Entry i of a per-register array, on every lane (i uniform).
   auto at = [&](const double(&x)[R], int i) {
     double y = 0.0;
@@ -2332,11 +2323,22 @@ __device__ __forceinline__ void reg_tail_wide(const uint64_t (&v)[R], int K, con
     }
     return n;
   };
-  double exact[R], pre[R];
+  // Inclusive prefix sums over i = r * 64 + lane of the exact terms (pe) and of the scaled
+  // ones (ps), the two scans of each register interleaved, the registers chained by their
+  // totals.
+  double exact[R], pe[R], ps[R];
+  double carry_e = 0.0, carry_s = 0.0;
 #pragma unroll
-  for (int r = 0; r < R; ++r) exact[r] = e1[r] / S1;
-  scan(exact, pre);
-  const double pool = lane_f64(pre[R - 1], kWaveSize - 1);
+  for (int r = 0; r < R; ++r) {
+    exact[r] = e1[r] / S1;
+    double a = exact[r], b = s[r];
+    wave_inclusive_scan2(a, b);
+    pe[r] = r == 0 ? a : carry_e + a;
+    ps[r] = r == 0 ? b : carry_s + b;
+    carry_e = r == 0 ? lane_f64(a, kWaveSize - 1) : carry_e + lane_f64(a, kWaveSize - 1);
+    carry_s = r == 0 ? lane_f64(b, kWaveSize - 1) : carry_s + lane_f64(b, kWaveSize - 1);
+  }
+  const double pool = carry_e;
   tabby_row_result res;
   res.max_logit = M;
   res.sum_exp = S1;
@@ -2349,12 +2351,10 @@ __device__ __forceinline__ void reg_tail_wide(const uint64_t (&v)[R], int K, con
     res.pool_exhausted = 0;
   } else {
     const double top_p = P.top_p;
-    double ssum[R], w[R], running[R];
-    scan(s, ssum);
-    const double scaled = lane_f64(ssum[R - 1], kWaveSize - 1);
+    const double scaled = carry_s;
+    double running[R];  // P_i / P_(K-1)
 #pragma unroll
-    for (int r = 0; r < R; ++r) w[r] = r * kWaveSize + lane < K ? s[r] / scaled : 0.0;
-    scan(w, running);
+    for (int r = 0; r < R; ++r) running[r] = r * kWaveSize + lane < K ? ps[r] / scaled : 0.0;
     const int cut_at = top_p < 1.0 ? first(K, [&](int r) { return running[r] >= top_p; }) : K;
     int cut = cut_at < K ? cut_at + 1 : K;
     double total = at(running, cut - 1);
@@ -2362,18 +2362,21 @@ __device__ __forceinline__ void reg_tail_wide(const uint64_t (&v)[R], int K, con
     const int hit = first(cut, [&](int r) { return target < running[r]; });
     chosen = hit < cut ? hit : cut - 1;
     // Margins of every comparison that fixed the cut and the draw (running sums are
-    // non-decreasing, so the neighbours of each boundary are the only ones to check).
+    // non-decreasing, so the neighbours of each boundary are the only ones to check), each
+    // lane testing the ones its own entries decide; one ballot collects the failures.
     constexpr double kMargin = 1.0 / 68719476736.0;  // 2^-36
-    const double r_cut = total, r_before = cut >= 2 ? at(running, cut - 2) : 0.0;
-    bool clear = true;
-    if (top_p < 1.0) {
-      const double m = kMargin * top_p;
-      clear = (cut < K || r_cut < top_p - m) && (cut == K || (r_cut >= top_p + m && (cut == 1 || r_before < top_p - m)));
+    const double m = kMargin * top_p, m2 = kMargin * total;
+    bool fail = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = r * kWaveSize + lane;
+      if (top_p < 1.0) {
+        if (cut == K) fail = fail || (i == K - 1 && !(running[r] < top_p - m));
+        else fail = fail || (i == cut - 1 && !(running[r] >= top_p + m)) || (i == cut - 2 && !(running[r] < top_p - m));
+      }
+      fail = fail || (i == chosen && !(running[r] > target + m2)) || (i == chosen - 1 && !(running[r] < target - m2));
     }
-    const double r_hi = at(running, chosen), r_lo = chosen >= 1 ? at(running, chosen - 1) : 0.0;
-    const double m2 = kMargin * total;
-    clear = clear && r_hi > target + m2 && (chosen == 0 || r_lo < target - m2);
-    if (!clear) {
+    if (__ballot(fail)) {
       // Bit for bit: V8's exp for the weights, sequential sums (sampler.ts:170-203).
 #pragma unroll
       for (int r = 0; r < R; ++r) {
