@@ -60,20 +60,6 @@ __device__ __forceinline__ double lane_f64(double v, int lane) {
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-// Inclusive prefix sum over the wave's lanes of non-negative integer-valued v (see above:
-// exact below 2^53, >= 2^53 otherwise): within rows of 16 by DPP shifts, then the totals of
-// the rows below.
-__device__ __forceinline__ double wave_inclusive_scan(double x) {
-  x += row_shift_up<1>(x);
-  x += row_shift_up<2>(x);
-  x += row_shift_up<4>(x);
-  x += row_shift_up<8>(x);
-  const double r0 = lane_f64(x, 15), r1 = lane_f64(x, 31), r2 = lane_f64(x, 47);
-  const int row = wave_lane() >> 4;
-  const double below = row == 0 ? 0.0 : row == 1 ? r0 : row == 2 ? r0 + r1 : (r0 + r1) + r2;
-  return x + below;
-}
-
 // The DPP move of control `ctrl` applied to both halves of v; rows outside row_mask get 0.
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ double dpp_f64(double v) {
@@ -81,6 +67,21 @@ __device__ __forceinline__ double dpp_f64(double v) {
   const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROW_MASK, 0xF, false);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROW_MASK, 0xF, false);
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Inclusive prefix sum over the wave's lanes of non-negative integer-valued v (see above:
+// exact below 2^53, >= 2^53 otherwise; for other terms lane i's sum is a tree of at most six
+// roundings over lanes 0..i): within rows of 16 by DPP shifts, then row_bcast:15 (lane 15 of
+// each row added to the next row: rows 1 and 3) and row_bcast:31 (lane 31 added to rows 2
+// and 3).
+__device__ __forceinline__ double wave_inclusive_scan(double x) {
+  x += row_shift_up<1>(x);
+  x += row_shift_up<2>(x);
+  x += row_shift_up<4>(x);
+  x += row_shift_up<8>(x);
+  x += dpp_f64<0x142, 0xA>(x);  // row_bcast:15
+  x += dpp_f64<0x143, 0xC>(x);  // row_bcast:31
+  return x;
 }
 
 // Two independent inclusive prefix sums over the wave's lanes, interleaved stage by stage so
