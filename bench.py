@@ -362,6 +362,10 @@ def timeline(args) -> int:
                   f"headline workload, last of {args.warmup + args.steps} calls",
         "unit": "us", "rows": w.rows, "vocab": w.vocab, "shader_clock_mhz": round(rate, 1),
         "phases": phases,
+        # Mean stream end by wave index (waves w, w + 4, w + 8, w + 12 share a SIMD, oldest
+        # first), and by XCD (workgroup i runs on XCD i mod 8).
+        "stream_end_by_wave": [round(float(x), 2) for x in waves.mean(0)],
+        "last_wave_end_by_xcd": [round(float(last[np.arange(w.rows) % 8 == x].mean()), 2) for x in range(8)],
         "library": os.path.relpath(B.TIMELINE_LIB_PATH, ROOT),
     }))
     return 0
