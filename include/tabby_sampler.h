@@ -47,8 +47,10 @@ typedef enum { TABBY_F32 = 0, TABBY_F16 = 1 } tabby_dtype;
  * SeededRandom.next() (sampler.ts:112-118) would return for this row. All f64, as JS
  * numbers are: 0.9 as f32 is not 0.9, and a mulberry32 draw has 32 significant bits. */
 typedef struct {
-  double temperature; /* <= 0: greedy, the uniform is not used (sampler.ts:159-167) */
-  double top_p;       /* >= 1: no nucleus cut (sampler.ts:177) */
+  double temperature; /* <= 0 (-0, -inf included): greedy, the uniform is not used
+                         (sampler.ts:159-167); NaN and +inf are refused (TABBY_EINVAL) */
+  double top_p;       /* any value, as sampler.ts:177-186 takes it: >= 1 or NaN, no nucleus
+                         cut; <= 0 keeps the first candidate */
   double uniform;     /* in [0, 1) */
   int32_t top_k;      /* 1..k_max candidates; 0 = the whole vocabulary */
   int32_t reserved;   /* must be 0 */
@@ -115,7 +117,8 @@ TABBY_API int tabby_sampler_sample(tabby_sampler *sampler, const void *logits_de
  * capture, tight serving loops, harnesses that forbid hipMalloc). It takes no handle and
  * calls no hipMalloc, hipFree or allocating routine; its scratch is a fixed 16 MiB array in
  * the library's device image, one per GPU, kept until the process ends (the first call on a
- * device looks up its address). The caller passes inputs and outputs as for
+ * device looks up its address). The 16 MiB are taken on every device the library's code is
+ * loaded on, whether or not this entry is ever called. The caller passes inputs and outputs as for
  * tabby_sampler_sample_device, with flags = 0, on the current device. Limits: k_max <= 256,
  * and rows whose pool is the whole vocabulary (top_k = 0 or >= vocab, vocab > 256) get
  * status TABBY_EINVAL; a batch whose scratch would exceed 16 MiB returns TABBY_ECAPACITY

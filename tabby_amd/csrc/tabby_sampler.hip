@@ -185,10 +185,22 @@ __device__ __forceinline__ int32_t effective_k(const tabby_row_params &p, int vo
   return (p.top_k <= 0 || p.top_k >= vocab) ? vocab : p.top_k;
 }
 
+// A row's parameters as the sampler accepts them: top_k in [0, k_max], the uniform in [0, 1),
+// and a temperature below +inf that is not NaN. sampler.ts would sample a NaN temperature
+// (`NaN <= 0` is false: every weight NaN, the draw falling to the pool's last entry) and turn
+// +inf into a uniform draw whose -inf entries poison the sums; here both are TABBY_EINVAL on
+// every path (the hosts throw before drawing a uniform). top_p is taken as sampler.ts takes
+// it, any value: below 1 cuts at the first running sum reaching it (the first, for top_p <= 0),
+// NaN or >= 1 never cuts.
 __device__ __forceinline__ bool params_valid(const tabby_row_params &p, int k_max) {
   return p.top_k >= 0 && p.top_k <= k_max && p.reserved == 0 && !(p.uniform < 0.0) &&
-         !(p.uniform >= 1.0) && p.uniform == p.uniform;
+         !(p.uniform >= 1.0) && p.uniform == p.uniform && p.temperature < INFINITY;
 }
+
+// sampleFromTopK's greedy branch (src/engine/sampler.ts:159): T <= 0 (-0 and -inf included)
+// takes the pool's first entry and leaves the uniform unused. Every tail tests this one
+// predicate; params_valid has already rejected NaN, so it is the complement of T > 0.
+__device__ __forceinline__ bool greedy_temp(double T) { return T <= 0.0; }
 
 // How many of its largest elements a slice keeps as candidates: the row's pool for a row
 // whose pool fits the kernels (keff <= kcap); for a whole-vocabulary row, the top-k list the
@@ -218,7 +230,7 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
                                 float max_logit, double sum_exp, const tabby_row_params &P) {
   constexpr int PER = KCAP / kBlock;
   const double T = P.temperature, top_p = P.top_p;
-  if (!(T > 0.0)) return false;
+  if (greedy_temp(T)) return false;
   const int lane = lane_id(), wave = wave_id();
   double *run = sm.u.tail.w;  // running sums, by index
   double c[PER], e_sum = 0.0, acc = 0.0;
@@ -337,7 +349,7 @@ __device__ __forceinline__ void finish_row(Smem &sm, const Launch &L, int row, c
     const float l = value_of(composite_key(sm.sorted[i]));
     const double d = (double)l - (double)max_logit;
     exact[i] = fdlibm_exp(d) / sum_exp;
-    w[i] = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
+    w[i] = !greedy_temp(T) ? fdlibm_exp(d / T) : 0.0;
   }
   __syncthreads();
   // Sequential sums (bit-exact; see seqsum.h): poolMass on wave 0 and the scaled total on
@@ -347,13 +359,13 @@ __device__ __forceinline__ void finish_row(Smem &sm, const Launch &L, int row, c
     const double pool = wave_seq_sum(exact, count, nullptr, INFINITY).total;
     if (lane_id() == 0) sm.pool_mass = pool;
   } else if (wave_id() == 1) {
-    const double scaled = T > 0.0 ? wave_seq_sum(w, count, nullptr, INFINITY).total : 0.0;
+    const double scaled = !greedy_temp(T) ? wave_seq_sum(w, count, nullptr, INFINITY).total : 0.0;
     if (lane_id() == 0) sm.scaled_total = scaled;
   }
   __syncthreads();
   const double pool_mass = sm.pool_mass;
   const double scaled_total = sm.scaled_total;
-  if (T > 0.0) {
+  if (!greedy_temp(T)) {
     for (int i = threadIdx.x; i < count; i += kBlock) w[i] = w[i] / scaled_total;
     __syncthreads();
   }
@@ -365,7 +377,7 @@ __device__ __forceinline__ void finish_row(Smem &sm, const Launch &L, int row, c
     r.status = TABBY_OK;
     r.topk_count = min(count, L.topk_cap);
     int chosen = 0;
-    if (T <= 0.0) {
+    if (greedy_temp(T)) {
       r.considered = 1;
       r.pool_exhausted = 0;
     } else {
@@ -444,7 +456,7 @@ __device__ __forceinline__ void wave_finish(const uint64_t *pool_in, int count, 
     if (r * kWaveSize + lane < count) {
       const double d = (double)value_of(composite_key(v[r])) - (double)max_logit;
       exact[r] = fdlibm_exp(d) / sum_exp;
-      if (T > 0.0) w[r] = fdlibm_exp(d / T);
+      if (!greedy_temp(T)) w[r] = fdlibm_exp(d / T);
     }
   }
   double pool = 0.0, scaled = 0.0;
@@ -463,7 +475,7 @@ __device__ __forceinline__ void wave_finish(const uint64_t *pool_in, int count, 
   res.status = TABBY_OK;
   res.topk_count = min(count, L.topk_cap);
   int chosen = 0;
-  if (T <= 0.0) {
+  if (greedy_temp(T)) {
     res.considered = 1;
     res.pool_exhausted = 0;
   } else {
@@ -1376,7 +1388,7 @@ __global__ __launch_bounds__(kWaveSize) void wave_kernel(Launch L, Workspace W) 
 // keys); a bisection of (kNegInfKey, top] stays as the fallback past 64 steps.
 __device__ __forceinline__ uint32_t head_threshold(float row_max, double T) {
   const uint32_t top = key_of(row_max);
-  if (!(T > 0.0)) return top;
+  if (greedy_temp(T)) return top;
   auto in_head = [&](uint32_t k) { return ((double)value_of(k) - (double)row_max) / T >= -37.5; };
   uint32_t c = min(max(key_of((float)((double)row_max - 37.5 * T)), kNegInfKey + 1u), top);
   int steps = 0;
@@ -1584,7 +1596,7 @@ __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
     if (wave_id() != 0) return;
     const double T = P.temperature;
     double list_sum = 0.0;
-    if (handed > 0 && T > 0.0) {
+    if (handed > 0 && !greedy_temp(T)) {
       double *terms = sm.u.tail.w;  // the histogram is no longer needed
       for (int i = lane_id(); i < handed; i += kWaveSize)
         terms[i] = fdlibm_exp(((double)value_of(composite_key(sm.sorted[i])) - (double)row_max) / T);
@@ -1892,7 +1904,7 @@ __device__ __forceinline__ void wave_tail(WaveMergeSmem &sm, int K, const Launch
   res.status = TABBY_OK;
   res.topk_count = min(K, L.topk_cap);
   int chosen = 0;
-  if (!(T > 0.0)) {  // greedy, the uniform unused
+  if (greedy_temp(T)) {  // greedy, the uniform unused
     res.considered = 1;
     res.pool_exhausted = 0;
   } else {
@@ -2083,9 +2095,9 @@ __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, 
       if (lane == 0) sm.pool = pool;
     } else if (w == 1) {
       for (int i = lane; i < K; i += kWaveSize)
-        sm.b[i] = T > 0.0 ? fdlibm_exp_inline(((double)value_of(composite_key(sm.sorted[i])) - M) / T) : 0.0;
+        sm.b[i] = !greedy_temp(T) ? fdlibm_exp_inline(((double)value_of(composite_key(sm.sorted[i])) - M) / T) : 0.0;
       wave_lds_sync();
-      if (T > 0.0) wave_draw(sm, K, P, wave_seq_sum(sm.b, K, nullptr, INFINITY).total);
+      if (!greedy_temp(T)) wave_draw(sm, K, P, wave_seq_sum(sm.b, K, nullptr, INFINITY).total);
     }
     __syncthreads();
   }
@@ -2106,10 +2118,10 @@ __device__ __forceinline__ void finish_pool(WaveMergeSmem &sm, const Launch &L, 
     const double T = P.temperature;
     for (int i = lane; i < K; i += kWaveSize) {
       list[i] = sm.sorted[i];
-      if (T > 0.0) sm.b[i] = fdlibm_exp_inline(((double)value_of(composite_key(sm.sorted[i])) - (double)row_max) / T);
+      if (!greedy_temp(T)) sm.b[i] = fdlibm_exp_inline(((double)value_of(composite_key(sm.sorted[i])) - (double)row_max) / T);
     }
     wave_lds_sync();
-    const double list_sum = T > 0.0 && K > 0 ? wave_seq_sum(sm.b, K, nullptr, INFINITY).total : 0.0;
+    const double list_sum = !greedy_temp(T) && K > 0 ? wave_seq_sum(sm.b, K, nullptr, INFINITY).total : 0.0;
     if (lane == 0) {
       RowState st;
       st.max = row_max;
@@ -2218,7 +2230,7 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
   const double T = P.temperature;
   const double d = (double)value_of(composite_key(v)) - (double)M;
   const double e1 = in ? exp_nonpos(d) : 0.0;
-  const double s = !(in && T > 0.0) ? 0.0 : T == 1.0 ? e1 : exp_nonpos(d / T);
+  const double s = (!in || greedy_temp(T)) ? 0.0 : T == 1.0 ? e1 : exp_nonpos(d / T);
   const double S1 = sum_exp_of();
   const double exact = e1 / S1;
   double pe = exact, ps = s;
@@ -2231,7 +2243,7 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
   res.status = TABBY_OK;
   res.topk_count = min(K, L.topk_cap);
   int chosen = 0;
-  if (!(T > 0.0)) {
+  if (greedy_temp(T)) {
     res.considered = 1;
     res.pool_exhausted = 0;
   } else {
@@ -2304,7 +2316,7 @@ __device__ __forceinline__ void reg_tail_wide(const uint64_t (&v)[R], int K, con
     const bool in = r * kWaveSize + lane < K;
     d[r] = (double)value_of(composite_key(v[r])) - (double)M;
     e1[r] = in ? exp_nonpos(d[r]) : 0.0;
-    s[r] = !(in && T > 0.0) ? 0.0 : T == 1.0 ? e1[r] : exp_nonpos(d[r] / T);
+    s[r] = (!in || greedy_temp(T)) ? 0.0 : T == 1.0 ? e1[r] : exp_nonpos(d[r] / T);
   }
   // Entry i of a per-register array, on every lane (i uniform).
   auto at = [&](const double(&x)[R], int i) {
@@ -2346,7 +2358,7 @@ __device__ __forceinline__ void reg_tail_wide(const uint64_t (&v)[R], int K, con
   res.status = TABBY_OK;
   res.topk_count = min(K, L.topk_cap);
   int chosen = 0;
-  if (!(T > 0.0)) {
+  if (greedy_temp(T)) {
     res.considered = 1;
     res.pool_exhausted = 0;
   } else {
@@ -2654,11 +2666,18 @@ __global__ __launch_bounds__(kRowWaves * kWaveSize) void row_kernel(Launch L, Wo
   TABBY_STAMP(w);
   if (small) {
     // Each wave marks itself finished; the waves marked before it are in the returned mask.
-    // Its histogram adds and statistics precede the mark in the LDS's order, so the last
-    // wave sees every add, and the second-to-last every other wave's statistics: it combines
-    // them while the last one streams and selects the take.
+    // The mark sits between workgroup-scope fences that every lane executes: the wave's
+    // histogram adds and its statistics happen before it (release), and what the wave reads
+    // after it -- the other waves' statistics, the whole histogram -- after every earlier
+    // mark (acquire). So the last wave sees every add, and the second-to-last every other
+    // wave's statistics: it combines them while the last one streams and selects the take.
+    // (At workgroup scope a fence is a wait for the wave's own outstanding memory
+    // operations, none once its stream has ended; no cache is written back.)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     uint32_t before = 0;
-    if (wave_lane() == 0) before = atomicOr(&sm.fin_mask, 1u << w);
+    if (wave_lane() == 0)
+      before = __hip_atomic_fetch_or(&sm.fin_mask, 1u << w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     before = (uint32_t)__builtin_amdgcn_readfirstlane((int)before);
     const int rank = __popc(before);
     if (rank == nw - 1) {
@@ -2972,7 +2991,7 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
   // The ulp of P_N (the sequential sum of the top N's terms, from the merge).
   const int N = (int)(rs.handoff >> 16);
   const double T = P.temperature, M = (double)rs.max;
-  const bool count_ulps = T > 0.0 && N > 0 && N <= kWaveKcap;
+  const bool count_ulps = !greedy_temp(T) && N > 0 && N <= kWaveKcap;
   const double scale = ulp_scale(rs.list_sum);
   const uint64_t last = count_ulps ? W.head_sorted[(size_t)row * W.head_stride + N - 1] : 0ull;
   double r = 0.0, ties = 0.0, outside = 0.0;
@@ -3174,7 +3193,7 @@ __device__ __forceinline__ void sort_segment(SortSmem &sm, const Launch &L, cons
       const double e = (double)__builtin_amdgcn_exp2f((float)(d * 1.4426950408889634));
       pool_part += e / rs.sum_exp;
       e_part += e;
-      sg[i] = T > 0.0 ? fdlibm_exp(d / T) : 0.0;
+      sg[i] = !greedy_temp(T) ? fdlibm_exp(d / T) : 0.0;
     }
     const double ps = block_sum(pool_part, sm.bs);
     const double es = block_sum(e_part, sm.bs);
@@ -3349,7 +3368,7 @@ __global__ __launch_bounds__(kFinishThreads) void head_finish_kernel(Launch L, W
   res.status = TABBY_OK;
   res.topk_count = min(H, L.topk_cap);
   int chosen = 0;
-  if (T <= 0.0) {
+  if (greedy_temp(T)) {
     res.considered = 1;
     res.pool_exhausted = 0;
   } else {
@@ -3435,7 +3454,7 @@ __device__ __forceinline__ bool head_fast_finish(HeadFastSmem &sm, const Launch 
   const int V = L.vocab, lane = wave_lane();
   const double M = (double)rs.max, S1 = rs.sum_exp, T = P.temperature, top_p = P.top_p;
   int chosen = 0, cut = 1;
-  if (T > 0.0) {
+  if (!greedy_temp(T)) {
     for (int i = lane; i < N; i += kWaveSize)
       sm.s[i] = fdlibm_exp(((double)value_of(composite_key(sm.top[i])) - M) / T);
     const double PN = rs.list_sum;
@@ -3511,7 +3530,7 @@ __global__ __launch_bounds__(kPlanThreads) void head_fast_kernel(Launch L, Works
   if (wave_id() == 0 && N > 0 && N <= kWaveKcap) {
     const uint64_t *list = W.head_sorted + (size_t)row * W.head_stride;
     for (int i = wave_lane(); i < N; i += kWaveSize) sm.top[i] = list[i];
-    if (P.temperature > 0.0) {
+    if (!greedy_temp(P.temperature)) {
       const double *acc = W.head_acc + (size_t)row * W.acc_stride * 3;
       for (int i = wave_lane(); i < L.h_splits; i += kWaveSize) {
         r += acc[3 * i];
@@ -4327,6 +4346,11 @@ int tabby_sampler_sample_lmhead_q4_device(tabby_sampler *h, const uint32_t *pack
                                   ", got " + std::to_string(rows));
   if (vocab > h->vocab_max)
     return fail(TABBY_EINVAL, "vocab must be at most " + std::to_string(h->vocab_max) + ", got " + std::to_string(vocab));
+  // At most kMaxSplits slices of at most kLhMaxWaves waves of rows (lmhead_slice_kernel's
+  // launch bound): 262,144 rows.
+  if (vocab > kMaxSplits * kLhMaxWaves * kWaveSize)
+    return fail(TABBY_ECAPACITY, "the fused lm_head takes at most " + std::to_string(kMaxSplits * kLhMaxWaves * kWaveSize) +
+                                     " vocabulary rows, got " + std::to_string(vocab));
   // Slices of 64 * waves rows: one slice for vocabularies up to 1,024; otherwise enough
   // waves per slice (at least four) that at most 256 slices cover the vocabulary -- about one
   // per CU (238 slices of 640 rows for 151,936).
@@ -4387,6 +4411,8 @@ int tabby_sampler_sample(tabby_sampler *h, const void *logits_dev, int32_t dtype
     if (p.reserved != 0) return fail(TABBY_EINVAL, "tabby_row_params.reserved must be 0");
     if (!(p.uniform >= 0.0 && p.uniform < 1.0))
       return fail(TABBY_EINVAL, "uniform must be in [0, 1), row " + std::to_string(r));
+    if (!(p.temperature < INFINITY))
+      return fail(TABBY_EINVAL, "temperature must not be NaN or +Infinity, row " + std::to_string(r));
     if (p.top_k == 0 || p.top_k >= vocab) {
       if (vocab > (h->k_max <= kKcapSmall ? kKcapSmall : kKcapLarge)) flags |= TABBY_FLAG_FULL_VOCAB;
     }

@@ -21,6 +21,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <string>
@@ -63,6 +64,16 @@ bool get_i64(napi_env env, napi_value v, int64_t *out) {
   return napi_get_value_int64(env, v, out) == napi_ok;
 }
 
+// An argument the C ABI takes as int32_t: in [lo, INT32_MAX].
+bool in_i32(int64_t v, int64_t lo) { return v >= lo && v <= INT32_MAX; }
+
+// rows x cols entries of `elem` bytes fit in `cap` bytes, with both counts in [1, INT32_MAX]
+// (the C ABI's int32_t); checked by division, so no product can overflow.
+bool dims_fit(int64_t rows, int64_t cols, size_t elem, size_t cap) {
+  if (!in_i32(rows, 1) || !in_i32(cols, 1)) return false;
+  return (uint64_t)rows <= cap / elem / (uint64_t)cols;
+}
+
 void release_handle(Handle *h) {
   if (h->sampler) tabby_sampler_destroy(h->sampler);
   h->sampler = nullptr;
@@ -102,7 +113,8 @@ napi_value Create(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, 4, argv)) return fail(env, "create(device, vocabMax, rowsMax, kMax)");
   int64_t a[4];
   for (int i = 0; i < 4; ++i)
-    if (!get_i64(env, argv[i], &a[i])) return fail(env, "create: integer arguments expected");
+    if (!get_i64(env, argv[i], &a[i]) || !in_i32(a[i], INT32_MIN))
+      return fail(env, "create: 32-bit integer arguments expected");
   tabby_sampler *s = nullptr;
   const int rc = tabby_sampler_create((int)a[0], (int32_t)a[1], (int32_t)a[2], (int32_t)a[3], &s);
   if (rc) return fail(env, tabby_last_error());
@@ -226,10 +238,11 @@ napi_value Sample(napi_env env, napi_callback_info info) {
   if (!get_i64(env, argv[2], &dtype) || !get_i64(env, argv[3], &rows) ||
       !get_i64(env, argv[4], &vocab) || !get_i64(env, argv[6], &cap))
     return fail(env, "sample: integer dtype, rows, vocab and topkCap expected");
-  if (rows <= 0 || vocab <= 0 || cap < 0) return fail(env, "sample: rows and vocab must be positive");
+  if (!in_i32(rows, 1) || !in_i32(vocab, 1) || !in_i32(cap, 0))
+    return fail(env, "sample: rows and vocab must be in [1, 2^31 - 1], topkCap in [0, 2^31 - 1]");
   const size_t elem = dtype == TABBY_F16 ? 2 : 4;
-  if ((size_t)rows * (size_t)vocab * elem > b->bytes)
-    return fail(env, "sample: rows x vocab exceeds the device buffer");
+  if (!dims_fit(rows, vocab, elem, b->bytes)) return fail(env, "sample: rows x vocab exceeds the device buffer");
+  if (cap > 0 && !dims_fit(rows, cap, 4, SIZE_MAX / 2)) return fail(env, "sample: rows x topkCap is too large");
   void *pdata;
   size_t plen;
   if (napi_get_arraybuffer_info(env, argv[5], &pdata, &plen) != napi_ok ||
@@ -274,9 +287,9 @@ napi_value Argmax(napi_env env, napi_callback_info info) {
   int64_t dtype, rows, vocab;
   if (!get_i64(env, argv[2], &dtype) || !get_i64(env, argv[3], &rows) || !get_i64(env, argv[4], &vocab))
     return fail(env, "argmax: integer dtype, rows and vocab expected");
-  if (rows <= 0 || vocab <= 0) return fail(env, "argmax: rows and vocab must be positive");
+  if (!in_i32(rows, 1) || !in_i32(vocab, 1)) return fail(env, "argmax: rows and vocab must be in [1, 2^31 - 1]");
   const size_t elem = dtype == TABBY_F16 ? 2 : 4;
-  if ((size_t)rows * (size_t)vocab * elem > b->bytes) return fail(env, "argmax: rows x vocab exceeds the device buffer");
+  if (!dims_fit(rows, vocab, elem, b->bytes)) return fail(env, "argmax: rows x vocab exceeds the device buffer");
   if ((size_t)rows > h->ids_cap) {
     (void)hipSetDevice(h->device);
     if (h->ids_dev) (void)hipFree(h->ids_dev);
@@ -310,9 +323,11 @@ napi_value SoftmaxRows(napi_env env, napi_callback_info info) {
   int64_t a[4];
   for (int i = 0; i < 4; ++i)
     if (!get_i64(env, argv[2 + i], &a[i])) return fail(env, "softmaxRows: integer arguments expected");
-  if (a[0] <= 0 || a[1] <= 0) return fail(env, "softmaxRows: nRows and rowLen must be positive");
-  const size_t bytes = (size_t)a[0] * (size_t)a[1] * 4;
-  if (bytes > in->bytes || bytes > out->bytes) return fail(env, "softmaxRows: nRows x rowLen exceeds a buffer");
+  if (!in_i32(a[0], 1) || !in_i32(a[1], 1)) return fail(env, "softmaxRows: nRows and rowLen must be in [1, 2^31 - 1]");
+  if (!in_i32(a[2], INT32_MIN) || !in_i32(a[3], INT32_MIN))
+    return fail(env, "softmaxRows: causalPeriod and causalOffset must be 32-bit integers");
+  if (!dims_fit(a[0], a[1], 4, std::min(in->bytes, out->bytes)))
+    return fail(env, "softmaxRows: nRows x rowLen exceeds a buffer");
   (void)hipSetDevice(in->device);
   const int rc = tabby_softmax_rows_device(static_cast<const float *>(in->ptr), static_cast<float *>(out->ptr),
                                            (int32_t)a[0], (int32_t)a[1], (int32_t)a[2], (int32_t)a[3], nullptr);

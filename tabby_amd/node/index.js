@@ -205,6 +205,11 @@ class Sampler {
         // forward.ts:348-351 rejects before any GPU work
         throw new Error(`topK must be between 0 and ${this.kMax}, got ${p.topK}`);
       }
+      // A NaN or +Infinity temperature is refused on every path (sampler.ts would sample
+      // NaN weights), before any uniform is drawn.
+      if (!(p.temperature < Infinity)) {
+        throw new Error(`temperature must not be NaN or +Infinity, got ${p.temperature}`);
+      }
     }
     const cap = opts && opts.topK ? opts.topK : 0;
     const packed = packParams(list, uniformsFor(list, rng));

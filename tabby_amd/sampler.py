@@ -19,6 +19,7 @@ the binding raises.
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 from dataclasses import dataclass, field
 from typing import List, Optional, Sequence, Union
@@ -203,6 +204,11 @@ def make_params(params: Union[SamplingParams, Sequence[SamplingParams]], rows: i
         params = [params] * rows
     if len(params) != rows:
         raise ValueError(f"expected {rows} SamplingParams, got {len(params)}")
+    for p in params:
+        # A NaN or +inf temperature is refused on every path (sampler.ts would sample NaN
+        # weights), before any uniform is drawn.
+        if not p.temperature < math.inf:
+            raise ValueError(f"temperature must not be NaN or +Infinity, got {p.temperature}")
     out = np.zeros(rows, dtype=PARAMS_DTYPE)
     explicit = None
     if rng is not None and not isinstance(rng, SeededRandom):

@@ -214,6 +214,18 @@ function main() {
       report.topKError = e.message;
     }
     report.stateAfterError = rng.state;
+    // A NaN or +Infinity temperature is refused before a uniform is drawn; -0 is greedy.
+    report.temperatureErrors = [NaN, Infinity].map((t) => {
+      try {
+        s.sample(row, { temperature: t, topK: 40, topP: 0.9 }, rng);
+        return null;
+      } catch (e) {
+        return e.message;
+      }
+    });
+    report.stateAfterTemperatureErrors = rng.state;
+    report.negZero = s.sample(row, { temperature: -0, topK: 40, topP: 0.9 }, rng);
+    report.stateAfterNegZero = rng.state;
     s.destroy();
     console.log(JSON.stringify(report));
   } else {

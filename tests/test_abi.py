@@ -111,3 +111,16 @@ def test_rng_is_advanced_only_for_non_greedy_rows():
     ref = S.SeededRandom(9)
     a, b = ref.next(), ref.next()
     assert p["uniform"].tolist() == [a, 0.0, b]
+
+
+def test_nan_and_inf_temperature_refused_before_any_uniform():
+    # A NaN or +inf temperature is refused (the device form gives TABBY_EINVAL for the row);
+    # the host raises before advancing the RNG. -0 and -inf are greedy (T <= 0) and draw none.
+    for t in (float("nan"), float("inf")):
+        rng = S.SeededRandom(9)
+        with pytest.raises(ValueError, match="temperature must not be NaN or \\+Infinity"):
+            S.make_params([S.SamplingParams(0.7, 40, 0.9), S.SamplingParams(t, 40, 0.9)], 2, rng)
+        assert rng.state == 9
+    p = S.make_params([S.SamplingParams(-0.0, 40, 0.9), S.SamplingParams(float("-inf"), 40, 0.9)], 2,
+                      S.SeededRandom(9))
+    assert p["uniform"].tolist() == [0.0, 0.0]

@@ -94,6 +94,12 @@ def test_node_sample_api_rng_and_errors(oracle):
     # forward.ts:348-351: topK out of range is rejected before any GPU work or RNG use.
     assert "topK must be between 0 and 64, got 65" in rep["topKError"]
     assert rep["stateAfterError"] == rep["stateAfterSample"]
+    # A NaN or +inf temperature throws before any uniform is drawn; -0 is greedy (T <= 0).
+    assert rep["temperatureErrors"] == ["temperature must not be NaN or +Infinity, got NaN",
+                                        "temperature must not be NaN or +Infinity, got Infinity"]
+    assert rep["stateAfterTemperatureErrors"] == rep["stateAfterSample"]
+    assert rep["negZero"]["id"] == oracle.argmax(row) and rep["negZero"]["consideredCount"] == 1
+    assert rep["stateAfterNegZero"] == rep["stateAfterSample"]
 
 
 @needs_node
