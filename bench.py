@@ -198,7 +198,11 @@ def lmhead_bench(args, dev, stream) -> int:
     vocab, hidden, block = 151936, 896, 32
     rows = min(args.rows, 8) if args.rows != 256 else 1
     words, f16, f32 = synth.lm_head_q4(vocab, hidden, block)
-    head = S.LmHeadQ4(words, f16, vocab, hidden, block)
+    # Four packed copies of the weights and scales (4 x 76.6 MB > the 256 MB MALL), rotated
+    # with the hidden states, so that every call reads its weights from HBM as a decode step
+    # does (one lm_head pass per token, the weights evicted by the rest of the model between).
+    heads = [S.LmHeadQ4(words, f16, vocab, hidden, block) for _ in range(ROTATE)]
+    head = heads[0]
     xs = [torch.from_numpy(synth.hidden_states(rows, hidden, seed=11 + b)).to(dev) for b in range(ROTATE)]
     params = np.zeros(rows, dtype=S.PARAMS_DTYPE)
     params["temperature"], params["top_k"], params["top_p"] = 0.7, 40, 0.9
@@ -207,14 +211,15 @@ def lmhead_bench(args, dev, stream) -> int:
     res = torch.zeros(rows * S.RESULT_DTYPE.itemsize, dtype=torch.uint8, device=dev)
     logits = torch.empty((rows, vocab), dtype=torch.float32, device=dev)
     g = S.GpuSampler(vocab_max=vocab, rows_max=max(rows, 1), k_max=64)
-    fused_us = _timed(lambda i: g.sample_lmhead_q4_device(head, xs[i % ROTATE], pdev, res, stream=stream),
+    fused_us = _timed(lambda i: g.sample_lmhead_q4_device(heads[i % ROTATE], xs[i % ROTATE], pdev, res,
+                                                          stream=stream),
                       args.steps, args.warmup, stream)
 
     def unfused(i):
-        head.logits(xs[i % ROTATE], out=logits, stream=stream)
+        heads[i % ROTATE].logits(xs[i % ROTATE], out=logits, stream=stream)
         g.sample_device(logits, pdev, res, stream=stream)
     unfused_us = _timed(unfused, args.steps, args.warmup, stream)
-    gemv_us = _timed(lambda i: head.logits(xs[i % ROTATE], out=logits, stream=stream),
+    gemv_us = _timed(lambda i: heads[i % ROTATE].logits(xs[i % ROTATE], out=logits, stream=stream),
                      args.steps, args.warmup, stream)
     # The answer of the fused call against the oracle (matmulQuantized, then the sampler).
     fused = g.sample_lmhead_q4(head, xs[0], params)
@@ -233,7 +238,8 @@ def lmhead_bench(args, dev, stream) -> int:
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(weight_bytes / (fused_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)},
         "dtype": "int4 weights, f32 arithmetic",
-        "data": "random-init int4 weights (synth.lm_head_q4), randomF32 hidden states, 4 rotated",
+        "data": "random-init int4 weights (synth.lm_head_q4) in 4 rotated device copies (306 MB, read "
+                "from HBM), randomF32 hidden states, 4 rotated",
         "parity": {"rows_checked": rows, "mismatched_rows": bad}}), flush=True)
     return 1 if bad else 0
 
@@ -279,7 +285,9 @@ def cpu_baseline(w, seconds: float) -> dict | None:
     args = (w.logits_f32()[:sample_rows], w.top_k[:sample_rows], w.temperature[:sample_rows],
             w.top_p[:sample_rows], w.uniform[:sample_rows])
     single = oracle.node_bench(*args, seconds=seconds, threads=1)
-    cores = min(os.cpu_count() or 1, 16)
+    # One worker per host core (Node's os.cpus().length), as the baseline plan states; the CPUs
+    # this process may actually run on (affinity and any cgroup quota) are reported beside.
+    cores = os.cpu_count() or 1
     multi = oracle.node_bench(*args, seconds=seconds, threads=cores)
     return {
         "value": round(multi["rowsPerSec"], 2),
@@ -292,7 +300,25 @@ def cpu_baseline(w, seconds: float) -> dict | None:
                    f"{multi['threads']} worker_threads ({multi['cpu']})"),
         "single_thread": {"value": round(single["rowsPerSec"], 2), "unit": "rows/s", "cores": 1,
                           "rows": single["rows"], "seconds": round(single["seconds"], 2)},
+        "usable_cpus": _usable_cpus(),
     }
+
+
+def _usable_cpus() -> dict:
+    """The host's logical CPUs, those this process may run on, and the cgroup CPU quota (if
+    any): the worker count above is the first; the rate is whatever the others allow."""
+    out = {"host": os.cpu_count()}
+    try:
+        out["affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            out["cgroup_quota"] = round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        pass
+    return out
 
 
 def timeline(args) -> int:
