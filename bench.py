@@ -380,6 +380,12 @@ def timeline(args) -> int:
         "second_tail_barrier": pct((tl[:, 19] - tl[:, 18]) / rate),
         "stats_fold_and_sort": pct((tl[:, 20] - tl[:, 19]) / rate),
         "register_tail": pct((tl[:, 21] - tl[:, 20]) / rate),
+        # Inside the register tail (rows that sample; greedy rows skip the draw's stamps).
+        "reg_tail_terms": pct((tl[:, 23] - tl[:, 20]) / rate),
+        "reg_tail_scans": pct((tl[:, 26] - tl[:, 23]) / rate),
+        "reg_tail_cut_and_draw": pct((tl[:, 27] - tl[:, 26]) / rate),
+        "reg_tail_margins": pct((tl[:, 28] - tl[:, 27]) / rate),
+        "reg_tail_result": pct((tl[:, 21] - tl[:, 28]) / rate),
         "tail_after_last_wave": pct((tl[:, 21] - start) / rate - last),
         "row_end": pct((rt1 - rt0.min()) * 1e-2),
     }

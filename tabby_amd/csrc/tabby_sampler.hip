@@ -55,7 +55,9 @@
 // workgroup's start (shader clock / real time); 22: the first bound ready (wave 0); 29: the
 // last wave's take selection done; 30: the second-to-last wave's statistics done; 17: past
 // the first tail barrier, 18: the take done, 19: past the second barrier (wave 0); 20: the
-// sort done; 21/25: the row finished (shader clock / real time).
+// sort done; in the register tail (reg_tail), 23: the terms computed, 26: their scans, 27:
+// the cut and the draw, 28: the margins checked; 21/25: the row finished (shader clock / real
+// time).
 #ifdef TABBY_TIMELINE
 namespace tabby {
 constexpr int kTimelineSlots = 32;
@@ -922,6 +924,39 @@ __device__ __forceinline__ int wave_local(int chunk, int e) {
   return chunk * kWChunk + ((e / VEC) * kWaveSize + wave_lane()) * VEC + e % VEC;
 }
 
+// The chunks of one slice (n elements from src) as the one-wave streaming loops read them,
+// element e of a lane's 16 being wave_local(chunk, e): 16-byte vectors (VEC > 1) or single
+// elements (VEC = 1: an odd length or an unaligned row), through a buffer resource over the
+// slice (RowBuffer). Elements past the slice's end, and every element of a chunk index past
+// the last, read as zero without touching memory; callers mask them by index. Loads are
+// issued unconditionally, so that the wait before a chunk's use leaves the next chunk in
+// flight.
+template <typename In, int VEC>
+struct ChunkReader {
+  RowBuffer buf;
+  __device__ __forceinline__ ChunkReader(const In *src, int n) : buf(src, (uint32_t)n * (uint32_t)sizeof(In)) {}
+  __device__ __forceinline__ void load(int chunk, float (&x)[kWChunkPerLane]) const {
+    const uint32_t base = (uint32_t)__builtin_amdgcn_readfirstlane(chunk * (int)(kWChunk * sizeof(In)));
+    if constexpr (VEC == 1) {
+      const uint32_t lane_off = (uint32_t)wave_lane() * (uint32_t)sizeof(In);
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e)
+        x[e] = buf.load_elem((const In *)nullptr, lane_off, base + (uint32_t)(e * kWaveSize * sizeof(In)));
+    } else {
+      static_assert(VEC * sizeof(In) == 16, "16-byte vectors");
+      constexpr int ITEMS = kWChunkPerLane / VEC;
+      const uint32_t lane_off = (uint32_t)wave_lane() * 16u;
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) {
+        float v[VEC];
+        Widen<In, VEC>::from(buf.load16(lane_off, base + (uint32_t)(j * kWaveSize * 16)), v);
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) x[j * VEC + c] = v[c];
+      }
+    }
+  }
+};
+
 // The wave kernel's LDS list holds raw entries, (value bits << 32) | ~index, so that an
 // append needs no key transform; a prune or the final sort turns them into composites
 // (key_of(value) << 32 | ~index) as it reads them. key_of maps -0 to the key of +0.
@@ -1143,6 +1178,7 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
   const int keff = effective_k(P, V);
   const int kk = slice_keep(valid_params, keff, n, L.kcap, L.head_pass, L.topk_cap);
   const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
+  const ChunkReader<In, VEC> rd(src, n);
   const int prune_at = kWListCap - kWaveSize;
 
   float lane_max = -INFINITY;
@@ -1239,9 +1275,9 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
       return __builtin_amdgcn_readfirstlane(c);
     };
     const int a = slice;
-    wave_load_any<In, VEC>(src, n, a, nchunks, x);
+    rd.load(a, x);
     int b = next();
-    wave_load_any<In, VEC>(src, n, b, nchunks, y);
+    rd.load(b, y);
     // The row's first bound, shared by its waves. A wave's 64 lane maxima over its first two
     // chunks are 64 distinct elements of the row; each wave publishes its m largest, and the
     // kk-th largest of the union (waves * m >= kk keys) has kk distinct elements at or above
@@ -1300,30 +1336,30 @@ __device__ __forceinline__ void wave_slice(WaveSmem &sm, const Launch &L, const 
         step(b, false, y);
         break;
       }
-      wave_load_any<In, VEC>(src, n, c, nchunks, x);
+      rd.load(c, x);
       step(b, false, y);
       b = next();
       if (b >= nchunks) {
         step(c, false, x);
         break;
       }
-      wave_load_any<In, VEC>(src, n, b, nchunks, y);
+      rd.load(b, y);
       step(c, false, x);
     }
   } else {
-    wave_load_any<In, VEC>(src, n, 0, nchunks, x);
+    rd.load(0, x);
     for (int c = 0; c < nchunks; c += 2) {
       if (c + 1 >= nchunks) {
         step(c, c == 0, x);
         break;
       }
-      wave_load_any<In, VEC>(src, n, c + 1, nchunks, y);
+      rd.load(c + 1, y);
       step(c, c == 0, x);
       if (c + 2 >= nchunks) {
         step(c + 1, false, y);
         break;
       }
-      wave_load_any<In, VEC>(src, n, c + 2, nchunks, x);
+      rd.load(c + 2, x);
       step(c + 1, false, y);
     }
   }
@@ -2233,9 +2269,11 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
   const double s = (!in || greedy_temp(T)) ? 0.0 : T == 1.0 ? e1 : exp_nonpos(d / T);
   const double S1 = sum_exp_of();
   const double exact = e1 / S1;
+  TABBY_STAMP(23);
   double pe = exact, ps = s;
   wave_inclusive_scan2(pe, ps);  // lanes >= K add zeros
   const double pool = lane_f64(pe, K - 1);
+  TABBY_STAMP(26);
   tabby_row_result res;
   res.max_logit = M;
   res.sum_exp = S1;
@@ -2251,6 +2289,7 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
     const double scaled = lane_f64(ps, K - 1);
     const double running = in ? ps / scaled : 0.0;
     Draw dr = draw_of(running, K, top_p, P.uniform);
+    TABBY_STAMP(27);
     // Margins of every comparison that fixed the cut and the draw (running sums are
     // non-decreasing, so the neighbours of each boundary are the only ones to check), each
     // lane testing the ones its own running sum decides.
@@ -2281,6 +2320,7 @@ __device__ __forceinline__ void reg_tail(uint64_t v, int K, const Launch &L, int
     chosen = dr.chosen;
     res.considered = (uint32_t)dr.cut;
     res.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
+    TABBY_STAMP(28);
   }
   const uint64_t cv = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, chosen) |
                       ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), chosen) << 32);
@@ -2984,10 +3024,11 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
   uint64_t *head = W.head + (size_t)row * W.head_stride + begin;
   int stored = 0;
 
-  // Both chunks' loads at once (a slice's second chunk past the row's end loads a dummy line).
+  // Both chunks' loads at once (a slice's second chunk past the row's end reads zeros).
   float x[kWChunkPerLane], y[kWChunkPerLane];
-  wave_load_any<In, VEC>(src, n, 0, nchunks, x);
-  wave_load_any<In, VEC>(src, n, 1, nchunks, y);
+  const ChunkReader<In, VEC> rd(src, n);
+  rd.load(0, x);
+  rd.load(1, y);
   // The ulp of P_N (the sequential sum of the top N's terms, from the merge).
   const int N = (int)(rs.handoff >> 16);
   const double T = P.temperature, M = (double)rs.max;
@@ -3751,10 +3792,8 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     sm.count = 0u;
   }
   __syncthreads();
-  auto load = [&](int c, float(&v)[kWChunkPerLane]) {
-    if (c < full_chunks) wave_load_full<In, VEC>(src, c, v);
-    else if (c < nchunks) wave_load<In, VEC>(src, n, c, v);
-  };
+  const ChunkReader<In, VEC> rd(src, n);
+  auto load = [&](int c, float(&v)[kWChunkPerLane]) { rd.load(c, v); };
   auto claim = [&]() {
     int c = 0;
     if (lane == 0) c = atomicAdd(&sm.next_chunk, 1);
@@ -3842,8 +3881,6 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     }
   };
   if (a < nchunks) step(a, x);  // chunk b is already in flight
-  // (Unlike row_kernel, the loads stay conditional here: the unconditional form needs more
-  // than the 64 VGPRs that two workgroups per CU leave, and spilled.)
   while (b < nchunks) {
     const int c = claim();
     load(c, x);
