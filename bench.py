@@ -337,9 +337,13 @@ def timeline(args) -> int:
     lib.tabby_debug_timeline.restype = ctypes.c_int
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    w = synth.config(3, rows=args.rows, vocab=args.vocab)
-    w.top_k[:] = args.top_k
-    w.top_p[:] = args.top_p
+    pool = args.config == 5  # config 5: pool_row_kernel's phases instead of row_kernel's
+    if pool:
+        w = synth.config(5)
+    else:
+        w = synth.config(3, rows=args.rows, vocab=args.vocab)
+        w.top_k[:] = args.top_k
+        w.top_p[:] = args.top_p
     base = torch.from_numpy(w.logits).to(dev)
     params = np.zeros(w.rows, dtype=S.PARAMS_DTYPE)
     params["temperature"], params["top_p"] = w.temperature, w.top_p
@@ -370,6 +374,26 @@ def timeline(args) -> int:
     def pct(a):
         return {p: round(float(np.percentile(a, q)), 2) for p, q in (("p0", 0), ("p50", 50), ("max", 100))}
 
+    if pool:
+        phases = {
+            "first_bound_ready": pct((tl[:, 22] - start) / rate),
+            "first_wave_stream_end": pct(waves.min(1)),
+            "last_wave_stream_end": pct(last),
+            "barrier_after_stream": pct((tl[:, 17] - start) / rate - last),
+            "selection": pct((tl[:, 18] - tl[:, 17]) / rate),
+            "gather_and_statistics": pct((tl[:, 21] - tl[:, 18]) / rate),
+            "row_end": pct((rt1 - rt0.min()) * 1e-2),
+        }
+        print(json.dumps({
+            "metric": "pool_row_kernel phase times (us from each row's start; later phases as "
+                      f"durations), config 5, last of {args.warmup + args.steps} calls",
+            "unit": "us", "rows": w.rows, "vocab": w.vocab, "shader_clock_mhz": round(rate, 1),
+            "phases": phases,
+            "candidates_per_row": {p: int(v) for p, v in pct(tl[:, 31]).items()},
+            "stream_end_by_wave": [round(float(x), 2) for x in waves.mean(0)],
+            "library": os.path.relpath(B.TIMELINE_LIB_PATH, ROOT),
+        }))
+        return 0
     phases = {
         "first_bound_ready": pct((tl[:, 22] - start) / rate),
         "first_wave_stream_end": pct(waves.min(1)),

@@ -57,7 +57,9 @@
 // the first tail barrier, 18: the take done, 19: past the second barrier (wave 0); 20: the
 // sort done; in the register tail (reg_tail), 23: the terms computed, 26: their scans, 27:
 // the cut and the draw, 28: the margins checked; 21/25: the row finished (shader clock / real
-// time).
+// time). pool_row_kernel (pools above 256) uses slots 0-15, 16/24, 22 and 21/25 the same way,
+// 17 for the barrier after the stream, 18 for the selection done, and records its candidate
+// count in slot 31 (TABBY_RECORD).
 #ifdef TABBY_TIMELINE
 namespace tabby {
 constexpr int kTimelineSlots = 32;
@@ -74,7 +76,15 @@ __device__ unsigned long long g_timeline[kTimelineGroups * kTimelineSlots];
     if (wave_lane() == 0 && blockIdx.x < kTimelineGroups)                                        \
       g_timeline[(size_t)blockIdx.x * kTimelineSlots + (slot)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
+#define TABBY_RECORD(slot, value)                                                                \
+  do {                                                                                           \
+    if (wave_lane() == 0 && blockIdx.x < kTimelineGroups)                                        \
+      g_timeline[(size_t)blockIdx.x * kTimelineSlots + (slot)] = (unsigned long long)(value);    \
+  } while (0)
 #else
+#define TABBY_RECORD(slot, value) \
+  do {                            \
+  } while (0)
 #define TABBY_STAMP(slot) \
   do {                    \
   } while (0)
@@ -3787,6 +3797,10 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
   const int kk = slice_keep(valid_params, keff, n, L.kcap, L.head_pass, L.topk_cap);
   const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * n;
   uint64_t *region = W.cands + (size_t)row * W.row_cand_stride;
+  if (w == 0) {
+    TABBY_STAMP(16);
+    TABBY_STAMP_REAL(24);
+  }
   if (threadIdx.x == 0) {
     sm.next_chunk = kPoolWaves;
     sm.count = 0u;
@@ -3829,6 +3843,7 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     };
     theta = theta_of(radix_select(keys, (uint32_t)kk, sm.hist, sm.bs, 2).prefix);
     __syncthreads();  // the keys are read before the list overwrites them
+    if (w == 0) TABBY_STAMP(22);
   }
 
   float lane_max = -INFINITY;
@@ -3890,6 +3905,7 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     load(b, y);
     step(c, x);
   }
+  TABBY_STAMP(w);
   const float ms = wave_max(lane_max);
   const double ss = wave_sum(rebase_sum(lane_sum, lane_max, lane_ml, ms));
   if (lane == 0) {
@@ -3902,6 +3918,10 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
   __syncthreads();
   // The row's exact top kk of the candidates, unsorted, to region[0 .. kept).
   const uint32_t C = sm.count;
+  if (w == 0) {
+    TABBY_STAMP(17);
+    TABBY_RECORD(31, C);
+  }
   uint32_t kept = 0u;
   if (kk > 0 && C > (uint32_t)kk) {
     auto each = [&](auto &&f) {
@@ -3914,6 +3934,7 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     if (threadIdx.x == 0) sm.bs.slot = 0u;
     __syncthreads();
     // region[0 .. kk) lies below the overflow entries (kk <= 1,024 < kPoolListCap).
+    if (w == 0) TABBY_STAMP(18);
     each([&](uint64_t v) {
       const bool take = v >= thr;
       const uint32_t at = wave_slot(take, &sm.bs.slot);
@@ -3933,6 +3954,8 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       st.sum = rs.sum_exp;
       W.stats[(size_t)row * kMaxSplits] = st;
     }
+    TABBY_STAMP(21);
+    TABBY_STAMP_REAL(25);
   }
 }
 
