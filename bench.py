@@ -381,6 +381,8 @@ def timeline(args) -> int:
             "last_wave_stream_end": pct(last),
             "barrier_after_stream": pct((tl[:, 17] - start) / rate - last),
             "selection": pct((tl[:, 18] - tl[:, 17]) / rate),
+            "selection_key_passes": pct((tl[:, 23] - tl[:, 17]) / rate),
+            "selection_index_passes": pct((tl[:, 18] - tl[:, 23]) / rate),
             "gather_and_statistics": pct((tl[:, 21] - tl[:, 18]) / rate),
             "row_end": pct((rt1 - rt0.min()) * 1e-2),
         }
@@ -390,6 +392,7 @@ def timeline(args) -> int:
             "unit": "us", "rows": w.rows, "vocab": w.vocab, "shader_clock_mhz": round(rate, 1),
             "phases": phases,
             "candidates_per_row": {p: int(v) for p, v in pct(tl[:, 31]).items()},
+            "key_passes_per_row": {p: int(v) for p, v in pct(tl[:, 26]).items()},
             "stream_end_by_wave": [round(float(x), 2) for x in waves.mean(0)],
             "library": os.path.relpath(B.TIMELINE_LIB_PATH, ROOT),
         }))

@@ -58,8 +58,9 @@
 // sort done; in the register tail (reg_tail), 23: the terms computed, 26: their scans, 27:
 // the cut and the draw, 28: the margins checked; 21/25: the row finished (shader clock / real
 // time). pool_row_kernel (pools above 256) uses slots 0-15, 16/24, 22 and 21/25 the same way,
-// 17 for the barrier after the stream, 18 for the selection done, and records its candidate
-// count in slot 31 (TABBY_RECORD).
+// 17 for the barrier after the stream, 23 for the selection's key passes done, 18 for the
+// selection done, and records its candidate count in slot 31 and its key passes in slot 26
+// (TABBY_RECORD).
 #ifdef TABBY_TIMELINE
 namespace tabby {
 constexpr int kTimelineSlots = 32;
@@ -3700,36 +3701,51 @@ __device__ __forceinline__ int pool_hist_at(int b) { return b + (b >> 5); }
 
 template <class Each, class BinOf>
 __device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Each each, BinOf bin_of, uint32_t need) {
-  for (int i = threadIdx.x; i < kPoolHistPad; i += kPoolThreads) sm.hist[i] = 0u;
+  static_assert(kPoolHistPad % 4 == 0 && kPoolHistPad <= 4 * kPoolThreads, "one 16-byte store per thread");
+  if ((int)threadIdx.x < kPoolHistPad / 4) reinterpret_cast<u32x4 *>(sm.hist)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
   each([&](uint64_t v) {
     const int b = bin_of(v);
-    if (b >= 0) atomicAdd(&sm.hist[pool_hist_at(b)], 1u);
+    // Lanes whose entries all fall in one bin (a tied key's entries do) add their count
+    // with one atomic: 64 atomics on one LDS address serialise.
+    // (Both masks are ballots of real predicates over the active lanes: a ballot of `true`
+    // may be folded to the whole wave, which the loop's last, partial step is not.)
+    const int b0 = __builtin_amdgcn_readfirstlane(b);
+    const uint64_t same = __ballot(b == b0);
+    if (!__ballot(b != b0)) {
+      if (b0 >= 0 && wave_lane() == __ffsll((unsigned long long)same) - 1)
+        atomicAdd(&sm.hist[pool_hist_at(b0)], (uint32_t)__popcll(same));
+    } else if (b >= 0) {
+      atomicAdd(&sm.hist[pool_hist_at(b)], 1u);
+    }
   });
   __syncthreads();
   if (wave_id() == 0) {
-    // Lane sums, their scan, then the owning lane walks its bins again (keeping 32 counts
-    // per lane in registers spilled under the kernel's 64-VGPR budget).
+    // Lane sums and their scan find the lane that owns the bin; then lanes 0..31 take one of
+    // that lane's 32 bins each and a second scan finds the bin (a walk of the owner's bins by
+    // the owner alone was a chain of up to 31 dependent LDS reads).
     constexpr int PER = kBins / kWaveSize;
     const int lane = wave_lane();
     uint32_t sum = 0u;
     static_assert(PER == 32, "pool_hist_at pads one word per 32 bins: a lane's bins are lane * 33 + q");
     const uint32_t *mine = sm.hist + lane * (PER + 1);
-#pragma unroll 4
+#pragma unroll 8
     for (int q = 0; q < PER; ++q) sum += mine[q];
     const uint32_t inc = wave_inclusive_scan_u32(sum);
-    const uint32_t before = inc - sum;
-    if (before < need && need <= inc) {
-      uint32_t acc = before;
-      int q = 0;
-      for (; q < PER - 1; ++q) {  // the lane's last bin holds it if none before does
-        const uint32_t c = mine[q];
-        if (need <= acc + c) break;
-        acc += c;
-      }
-      sm.bs.bin = (uint32_t)(lane * PER + q);
-      sm.bs.above = acc;
-      sm.bs.count = mine[q];
+    // need <= the total: some lane's running sum reaches it (else the last lane, whose
+    // reads stay inside the histogram).
+    const uint64_t got = __ballot(inc >= need);
+    const int owner = got ? __ffsll((unsigned long long)got) - 1 : kWaveSize - 1;
+    const uint32_t before = (uint32_t)__builtin_amdgcn_readlane((int)(inc - sum), owner);
+    const uint32_t c = lane < PER ? sm.hist[owner * (PER + 1) + lane] : 0u;
+    const uint32_t cum = before + wave_inclusive_scan_u32(c);
+    // The owner's last bin holds it if none before does.
+    const uint64_t reach = __ballot(lane < PER - 1 && cum >= need);
+    const int q = reach ? __ffsll((unsigned long long)reach) - 1 : PER - 1;
+    if (lane == q) {
+      sm.bs.bin = (uint32_t)(owner * PER + q);
+      sm.bs.above = cum - c;
+      sm.bs.count = c;
     }
   }
   __syncthreads();
@@ -3743,11 +3759,15 @@ __device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Each each, BinOf bin_
 // key remains (a quantized row resolves in one), then the ~index digits of that key's
 // entries (bits 20..10, 9..0; bits 31..21 of ~index are ones below 2^21 indices). A pass
 // that leaves its bin exactly taken ends early.
+// The rest of pool_select from a key range [lo, hi] that holds the `need`-th entry: narrower
+// key passes until one key remains, then that key's ties by their indices' digits.
 template <class Each>
-__device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Each each, uint32_t need, uint32_t lo, uint32_t hi) {
-  for (;;) {
+__device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Each each, uint32_t need, uint32_t lo,
+                                                     uint32_t hi, int key_passes) {
+  while (lo != hi) {
+    ++key_passes;
     const uint32_t range = hi - lo;
-    const int bits = range == 0u ? 0 : 32 - __builtin_clz(range);
+    const int bits = 32 - __builtin_clz(range);
     const int shift = bits > 11 ? bits - 11 : 0;
     const uint32_t top_key = hi, low_key = lo;
     const PoolBin r = pool_pass(sm, each, [&](uint64_t v) {
@@ -3757,10 +3777,20 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Each each, uint32_
     need -= r.above;
     const uint32_t bin_top = hi - (r.bin << shift);
     const uint32_t bin_low = bin_top - min((1u << shift) - 1u, bin_top - lo);
-    if (r.count == need) return (uint64_t)bin_low << 32;  // the whole bin is taken
+    if (r.count == need) {  // the whole bin is taken
+      if (wave_id() == 0) {
+        TABBY_RECORD(26, key_passes);
+        TABBY_STAMP(23);
+      }
+      return (uint64_t)bin_low << 32;
+    }
     hi = bin_top;
     lo = bin_low;
     if (shift == 0) break;
+  }
+  if (wave_id() == 0) {
+    TABBY_RECORD(26, key_passes);
+    TABBY_STAMP(23);
   }
   uint64_t prefix = ((uint64_t)lo << 32) | 0xffe00000ull;
   int done = 21;
@@ -3779,6 +3809,71 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Each each, uint32_
     if (r.count == need) return prefix;
   }
   return prefix;
+}
+
+// The row's kk-th largest candidate composite (need = kk entries at or above it), among the
+// candidates that `each` visits -- entries [sel_begin, sel_end) of the list (list[i] in LDS
+// for i < kPoolListCap, else region[i]), at first the C candidates -- all with keys in
+// [lo, hi]: histogram passes over the keys (2,048 bins of the candidates' own range, narrowed
+// until one key remains -- a quantized row resolves in one), then over the tied key's index
+// digits. After the first pass only the chosen bin's entries matter: they are copied behind
+// the candidates (B entries at list[C ..), when C + B fits the LDS list) and `each` is moved
+// onto them, so the later passes visit those B alone instead of all C (config 5: ~6,300
+// candidates, a tied bin of a few hundred; the later passes had re-read every candidate).
+template <class Each>
+__device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Each each, uint32_t need, uint32_t lo, uint32_t hi,
+                                                uint32_t C, uint32_t &sel_begin, uint32_t &sel_end) {
+  if (lo == hi) return pool_select_from(sm, each, need, lo, hi, 0);
+  const uint32_t range = hi - lo;
+  const int bits = 32 - __builtin_clz(range);
+  const int shift = bits > 11 ? bits - 11 : 0;
+  const PoolBin r = pool_pass(sm, each, [&](uint64_t v) {
+    const uint32_t k = composite_key(v);
+    return (k >= lo && k <= hi) ? (int)((hi - k) >> shift) : -1;
+  }, need);
+  need -= r.above;
+  const uint32_t bin_top = hi - (r.bin << shift);
+  const uint32_t bin_low = bin_top - min((1u << shift) - 1u, bin_top - lo);
+  if (r.count == need) {  // the whole bin is taken
+    if (wave_id() == 0) {
+      TABBY_RECORD(26, 1);
+      TABBY_STAMP(23);
+    }
+    return (uint64_t)bin_low << 32;
+  }
+  if (shift == 0 || C + r.count > (uint32_t)kPoolListCap) return pool_select_from(sm, each, need, bin_low, bin_top, 1);
+  // The chosen bin's entries, copied to list[C, C + B), and their smallest and largest key
+  // (the later passes bin [smallest, largest]; one key -- a tie -- goes straight to the index
+  // digits).
+  if (threadIdx.x == 0) {
+    sm.bs.slot2 = 0u;
+    sm.bs.u[0] = ~0u;
+    sm.bs.u[1] = 0u;
+  }
+  __syncthreads();
+  uint32_t kmin = ~0u, kmax = 0u;
+  each([&](uint64_t v) {
+    const uint32_t k = composite_key(v);
+    const bool in = k >= bin_low && k <= bin_top;
+    const uint32_t at = wave_slot(in, &sm.bs.slot2);
+    if (in) {
+      sm.u.list[C + at] = v;
+      kmin = min(kmin, k);
+      kmax = max(kmax, k);
+    }
+  });
+  kmin = ~wave_max_u32(~kmin);
+  kmax = wave_max_u32(kmax);
+  if (wave_lane() == 0) {
+    atomicMin(&sm.bs.u[0], kmin);
+    atomicMax(&sm.bs.u[1], kmax);
+  }
+  __syncthreads();
+  sel_begin = C;
+  sel_end = C + sm.bs.slot2;  // the bin's r.count entries
+  const uint32_t lo2 = sm.bs.u[0], hi2 = sm.bs.u[1];
+  __syncthreads();  // sm.bs is reused
+  return pool_select_from(sm, each, need, lo2, hi2, 1);
 }
 
 // Two workgroups per CU (74 KB of LDS and at most 64 VGPRs each): one's bound and selection
@@ -3924,13 +4019,17 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
   }
   uint32_t kept = 0u;
   if (kk > 0 && C > (uint32_t)kk) {
+    uint32_t sel_begin = 0u, sel_end = C;  // the entries `each` visits (pool_select narrows them)
     auto each = [&](auto &&f) {
-      for (uint32_t i = threadIdx.x; i < C; i += kPoolThreads) f(i < (uint32_t)kPoolListCap ? sm.u.list[i] : region[i]);
+      for (uint32_t i = sel_begin + threadIdx.x; i < sel_end; i += kPoolThreads)
+        f(i < (uint32_t)kPoolListCap ? sm.u.list[i] : region[i]);
     };
     // Every candidate's key lies between theta's and the row max's.
     float mx = lane < kPoolWaves ? sm.stats[lane].max : -INFINITY;
     mx = wave_max(mx);
-    const uint64_t thr = pool_select(sm, each, (uint32_t)kk, key_of(theta), key_of(mx));
+    const uint64_t thr = pool_select(sm, each, (uint32_t)kk, key_of(theta), key_of(mx), C, sel_begin, sel_end);
+    sel_begin = 0u;  // the gather below visits every candidate
+    sel_end = C;
     if (threadIdx.x == 0) sm.bs.slot = 0u;
     __syncthreads();
     // region[0 .. kk) lies below the overflow entries (kk <= 1,024 < kPoolListCap).
