@@ -69,6 +69,9 @@ def parse_args():
                     help="run the headline workload on the timeline build of the library (the "
                          "row kernel with phase timestamps compiled in) and print the phases' "
                          "percentiles over the rows of the last call, in us; a diagnostic")
+    ap.add_argument("--timeline-raw", metavar="PATH", default=None,
+                    help="with --timeline: also save the last call's raw stamps (rows x 32 "
+                         "slots, int64) to PATH as .npy")
     ap.add_argument("--softmax", action="store_true",
                     help="time the attention row softmax (tabby_softmax_rows_device) on a "
                          "prefill shape: 14 heads x 512 queries over 512 positions, causal; a "
@@ -365,6 +368,8 @@ def timeline(args) -> int:
         print("bench: tabby_debug_timeline failed", file=sys.stderr)
         return 1
     tl = tl.reshape(groups, slots)[: w.rows].astype(np.int64)
+    if args.timeline_raw:
+        np.save(args.timeline_raw, tl)
     start, rt0, rt1 = tl[:, 16], tl[:, 24], tl[:, 25]
     # Shader-clock ticks per us, from each row's start-to-end in both clocks (real time: 100 MHz).
     rate = float(np.median((tl[:, 21] - start) / ((rt1 - rt0) * 1e-2)))
@@ -383,7 +388,9 @@ def timeline(args) -> int:
             "selection": pct((tl[:, 18] - tl[:, 17]) / rate),
             "selection_key_passes": pct((tl[:, 23] - tl[:, 17]) / rate),
             "selection_index_passes": pct((tl[:, 18] - tl[:, 23]) / rate),
-            "gather_and_statistics": pct((tl[:, 21] - tl[:, 18]) / rate),
+            "gather": pct((tl[:, 19] - tl[:, 18]) / rate),
+            "sort": pct((tl[:, 20] - tl[:, 19]) / rate),
+            "sample_from_pool": pct((tl[:, 21] - tl[:, 20]) / rate),
             "row_end": pct((rt1 - rt0.min()) * 1e-2),
         }
         print(json.dumps({

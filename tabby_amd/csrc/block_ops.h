@@ -180,11 +180,13 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t *a, int n) {
 }
 
 // In-place descending sort of a[0..n) in LDS, n a power of two, by the whole workgroup:
-// each wave sorts 256-entry chunks in registers (the network's stages below 256 need no
-// barrier), and only the strides of 256 and above go through LDS with a barrier each.
-template <int NW = kWaves>
+// each wave sorts chunks of 64 * R entries in registers (the network's stages below the
+// chunk need no barrier), and only the strides of a chunk and above go through LDS with a
+// barrier each. R = 4 (256-entry chunks) suits four waves; with sixteen, R = 1 keeps every
+// wave busy in the register stages at the cost of two more LDS strides per merge level.
+template <int NW = kWaves, int R = 4>
 __device__ __forceinline__ void block_sort_desc(uint64_t *a, int n) {
-  constexpr int R = 4, kChunkN = kWaveSize * R;  // 256 entries per wave pass
+  constexpr int kChunkN = kWaveSize * R;  // entries per wave pass
   if (n < kChunkN) {
     bitonic_sort_desc<NW>(a, n);
     return;

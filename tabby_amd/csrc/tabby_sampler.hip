@@ -59,8 +59,8 @@
 // the cut and the draw, 28: the margins checked; 21/25: the row finished (shader clock / real
 // time). pool_row_kernel (pools above 256) uses slots 0-15, 16/24, 22 and 21/25 the same way,
 // 17 for the barrier after the stream, 23 for the selection's key passes done, 18 for the
-// selection done, and records its candidate count in slot 31 and its key passes in slot 26
-// (TABBY_RECORD).
+// selection done, 19 for the pool gathered, 20 for the pool sorted, and records its candidate
+// count in slot 31 and its key passes in slot 26 (TABBY_RECORD).
 #ifdef TABBY_TIMELINE
 namespace tabby {
 constexpr int kTimelineSlots = 32;
@@ -116,6 +116,8 @@ struct SliceStat {
   uint32_t count; // candidates written
   double sum;     // sum over the slice of exp(x - max)
 };
+// SliceStat.count of a row that pool_row_kernel sampled itself: merge_kernel skips the row.
+constexpr uint32_t kPoolRowDone = 0xffffffffu;
 
 // Per-row hand-over from the sampling kernel to the head kernel (whole-vocabulary rows).
 struct RowState {
@@ -227,6 +229,21 @@ __device__ __forceinline__ int slice_keep(bool valid, int keff, int n, int kcap,
   return head_pass ? min(max(topk_cap, kHeadList), n) : 0;
 }
 
+// The first active lane's f64, bit for bit (the readfirstlane builtin takes 32-bit ints).
+__device__ __forceinline__ double readfirstlane_f64(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const long long b = __double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(b >> 32), lane);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
 // The fast form of finish_row for pools of 257..KCAP (as reg_tail for pools up to 64): terms
 // from exp_nonpos (within 8 ulp of exp), the running sums of the scaled terms a workgroup scan
 // divided by their total (each partial sum a tree of at most 12 roundings, then one
@@ -238,10 +255,12 @@ __device__ __forceinline__ int slice_keep(bool valid, int keff, int n, int kcap,
 // row bit for bit. poolMass and the probability (compared within 1e-5) take the fast terms.
 // Three barriers: one exchange of the waves' totals, then one per first-index search (one LDS
 // atomic per wave: the first lane that holds a match).
-template <int KCAP, typename In, class Smem>
+template <int KCAP, typename In, class Smem, int NW = kWaves>
 __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int row, const In *row_src, int count,
                                 float max_logit, double sum_exp, const tabby_row_params &P) {
-  constexpr int PER = KCAP / kBlock;
+  constexpr int kThreads = NW * kWaveSize;
+  static_assert(KCAP % kThreads == 0, "whole entries per thread");
+  constexpr int PER = KCAP / kThreads;
   const double T = P.temperature, top_p = P.top_p;
   if (greedy_temp(T)) return false;
   const int lane = lane_id(), wave = wave_id();
@@ -267,11 +286,20 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
   }
   __syncthreads();
   double scaled = 0.0, e_total = 0.0, base = incl - acc;
+  if constexpr (NW <= kWaves) {
 #pragma unroll
-  for (int k = 0; k < kWaves; ++k) {
-    scaled += sm.bs.d[k];
-    e_total += sm.bs.d2[k];
-    if (k < wave) base += sm.bs.d[k];
+    for (int k = 0; k < NW; ++k) {
+      scaled += sm.bs.d[k];
+      e_total += sm.bs.d2[k];
+      if (k < wave) base += sm.bs.d[k];
+    }
+  } else {
+    // Many waves: lane k takes wave k's totals, and a wave scan gives every prefix (the
+    // unrolled loop above held too many of them in registers).
+    const double waves_incl = wave_inclusive_scan(lane < NW ? sm.bs.d[lane] : 0.0);
+    scaled = readlane_f64(waves_incl, NW - 1);
+    e_total = wave_sum(lane < NW ? sm.bs.d2[lane] : 0.0);
+    if (wave > 0) base += readlane_f64(waves_incl, wave - 1);
   }
   const double pool = e_total / sum_exp;
   double r[PER];
@@ -335,7 +363,7 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
   }
   if (L.topk_cap > 0) {
     const int m = min(count, L.topk_cap);
-    for (int i = threadIdx.x; i < m; i += kBlock) {
+    for (int i = threadIdx.x; i < m; i += kThreads) {
       const uint32_t idx = composite_index(sm.sorted[i]);
       L.topk_ids[(size_t)row * L.topk_cap + i] = (int32_t)idx;
       L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(L.vocab - 1)));
@@ -350,15 +378,16 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
 // evaluated bit for bit by a wave (seqsum.h). The running sums of the draw (sampler.ts:195-203)
 // are the top-p cumulative sums (sampler.ts:178-185), and `total` (:191-192) is the last of
 // them. The fast form above is tried first.
-template <int KCAP, typename In, class Smem>
+template <int KCAP, typename In, class Smem, int NW = kWaves>
 __device__ __forceinline__ void finish_row(Smem &sm, const Launch &L, int row, const In *row_src,
                            int count, float max_logit, double sum_exp,
                            const tabby_row_params &P) {
-  if (finish_row_fast<KCAP, In>(sm, L, row, row_src, count, max_logit, sum_exp, P)) return;
+  constexpr int kThreads = NW * kWaveSize;
+  if (finish_row_fast<KCAP, In, Smem, NW>(sm, L, row, row_src, count, max_logit, sum_exp, P)) return;
   const double T = P.temperature;
   double *exact = sm.u.tail.exact;
   double *w = sm.u.tail.w;
-  for (int i = threadIdx.x; i < count; i += kBlock) {
+  for (int i = threadIdx.x; i < count; i += kThreads) {
     const float l = value_of(composite_key(sm.sorted[i]));
     const double d = (double)l - (double)max_logit;
     exact[i] = fdlibm_exp(d) / sum_exp;
@@ -379,7 +408,7 @@ __device__ __forceinline__ void finish_row(Smem &sm, const Launch &L, int row, c
   const double pool_mass = sm.pool_mass;
   const double scaled_total = sm.scaled_total;
   if (!greedy_temp(T)) {
-    for (int i = threadIdx.x; i < count; i += kBlock) w[i] = w[i] / scaled_total;
+    for (int i = threadIdx.x; i < count; i += kThreads) w[i] = w[i] / scaled_total;
     __syncthreads();
   }
   if (wave_id() == 0) {
@@ -418,27 +447,12 @@ __device__ __forceinline__ void finish_row(Smem &sm, const Launch &L, int row, c
   }
   if (L.topk_cap > 0) {
     const int m = min(count, L.topk_cap);
-    for (int i = threadIdx.x; i < m; i += kBlock) {
+    for (int i = threadIdx.x; i < m; i += kThreads) {
       const uint32_t idx = composite_index(sm.sorted[i]);
       L.topk_ids[(size_t)row * L.topk_cap + i] = (int32_t)idx;
       L.topk_logits[(size_t)row * L.topk_cap + i] = load_one(row_src + min(idx, (uint32_t)(L.vocab - 1)));
     }
   }
-}
-
-// The first active lane's f64, bit for bit (the readfirstlane builtin takes 32-bit ints).
-__device__ __forceinline__ double readfirstlane_f64(double v) {
-  const uint64_t b = (uint64_t)__double_as_longlong(v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
-  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-}
-
-__device__ __forceinline__ double readlane_f64(double v, int lane) {
-  const long long b = __double_as_longlong(v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)b, lane);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(b >> 32), lane);
-  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
 // sampleFromTopK (src/engine/sampler.ts:147-212) for a pool of at most 64*R candidates, by
@@ -1487,6 +1501,7 @@ template <int KCAP, typename In>
 __global__ __launch_bounds__(kBlock) void merge_kernel(Launch L, Workspace W) {
   __shared__ MergeSmem<KCAP> sm;
   const int row = (int)blockIdx.x;
+  if (L.pool_rows && W.stats[(size_t)row * kMaxSplits].count == kPoolRowDone) return;
   const int splits = L.splits;
   const int V = L.vocab;
   const tabby_row_params P = L.params[row];
@@ -3680,13 +3695,23 @@ struct PoolSmem {
   union {
     uint64_t list[kPoolListCap];
     uint32_t keys[kPoolBoundKeys];  // the first bound's keys, before anything is appended
+    struct {
+      double exact[kKcapLarge];
+      double w[kKcapLarge];
+    } tail;  // finish_row's terms, once the pool is in `sorted`
   } u;
-  uint32_t hist[kPoolHistPad];
+  union {
+    uint32_t hist[kPoolHistPad];
+    uint64_t sorted[kKcapLarge];  // the row's pool, gathered after the last selection pass
+  };
   SliceStat stats[kPoolWaves];
   BlockScratchT<kPoolWaves> bs;
+  double pool_mass;
+  double scaled_total;
   uint32_t count;
   int next_chunk;
 };
+static_assert(sizeof(uint64_t) * kKcapLarge <= sizeof(uint32_t) * kPoolHistPad, "the pool fits the histogram's words");
 
 // One histogram pass of the pool kernel's selections, by the whole workgroup: the entries
 // that bin_of admits (bin >= 0; bin 0 holds the largest) are counted, and wave 0 finds the
@@ -3895,6 +3920,9 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
   if (w == 0) {
     TABBY_STAMP(16);
     TABBY_STAMP_REAL(24);
+    // Where the workgroup runs: XCC_ID, and HW_ID's CU, shader-array and engine fields.
+    TABBY_RECORD(30, ((__builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xfu) << 16) |
+                         ((__builtin_amdgcn_s_getreg((31 << 11) | 4) >> 8) & 0xffu));
   }
   if (threadIdx.x == 0) {
     sm.next_chunk = kPoolWaves;
@@ -3966,28 +3994,39 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       lane_ml = ml;
     }
     if (kk == 0 || !__ballot(cm >= theta)) return;
+    // Past the row's end the elements become NaN, which fails x >= theta for every theta
+    // (-inf included), so that one compare decides each element below.
+    if (c >= full_chunks) {
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e)
+        if (wave_local<VEC>(c, e) >= n) cur[e] = __builtin_nanf("");
+    }
     // The chunk's candidates: counted first, then one reservation for the wave, then the
     // same ballots again for the appends (keeping sixteen 64-bit masks live spilled registers).
-    const bool partial = c >= full_chunks;
-    auto takes = [&](int e) { return cur[e] >= theta && (!partial || wave_local<VEC>(c, e) < n); };
     uint32_t total = 0;
 #pragma unroll
-    for (int e = 0; e < kWChunkPerLane; ++e) total += (uint32_t)__popcll(__ballot(takes(e)));
+    for (int e = 0; e < kWChunkPerLane; ++e) total += (uint32_t)__popcll(__ballot(cur[e] >= theta));
     if (total == 0u) return;
     uint32_t at = 0u;
     if (lane == 0) at = atomicAdd(&sm.count, total);
     at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
+    auto append = [&](auto &&store) {
 #pragma unroll
-    for (int e = 0; e < kWChunkPerLane; ++e) {
-      const uint64_t mask = __ballot(takes(e));
-      if (mask) {
-        if ((mask >> lane) & 1ull) {
-          const uint32_t pos = at + lanes_below(mask);
-          const uint64_t v = composite(key_of(cur[e]), (uint32_t)wave_local<VEC>(c, e));
-          if (pos < (uint32_t)kPoolListCap) sm.u.list[pos] = v; else region[pos] = v;
-        }
+      for (int e = 0; e < kWChunkPerLane; ++e) {
+        const bool take = cur[e] >= theta;
+        const uint64_t mask = __ballot(take);
+        if (take) store(at + lanes_below(mask), composite(key_of(cur[e]), (uint32_t)wave_local<VEC>(c, e)));
         at += (uint32_t)__popcll(mask);
       }
+    };
+    // A reservation inside the LDS list (all but the rarest) stores with no per-element test
+    // of where the entry goes.
+    if (at + total <= (uint32_t)kPoolListCap) {
+      append([&](uint32_t pos, uint64_t v) { sm.u.list[pos] = v; });
+    } else {
+      append([&](uint32_t pos, uint64_t v) {
+        if (pos < (uint32_t)kPoolListCap) sm.u.list[pos] = v; else region[pos] = v;
+      });
     }
   };
   if (a < nchunks) step(a, x);  // chunk b is already in flight
@@ -4011,12 +4050,21 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     sm.stats[w] = st;
   }
   __syncthreads();
-  // The row's exact top kk of the candidates, unsorted, to region[0 .. kept).
+  // The row's exact top kk of the candidates, unsorted: to `sorted` in LDS for a row this
+  // workgroup samples itself (valid parameters, a pool of at most kcap, finite statistics:
+  // every row that merge_kernel would sample from the pool), else to region[0 .. kept) for
+  // merge_kernel (statuses and whole-vocabulary rows).
   const uint32_t C = sm.count;
   if (w == 0) {
     TABBY_STAMP(17);
     TABBY_RECORD(31, C);
   }
+  const RowStats rs = row_stats(sm.stats, kPoolWaves);
+  const bool here = valid_params && keff <= L.kcap && rs.max > -INFINITY && rs.max < INFINITY &&
+                    rs.sum_exp > 0.0 && rs.sum_exp < INFINITY && kk > 0 && C > 0u;
+  auto put = [&](uint32_t at, uint64_t v) {
+    if (here) sm.sorted[at] = v; else region[at] = v;
+  };
   uint32_t kept = 0u;
   if (kk > 0 && C > (uint32_t)kk) {
     uint32_t sel_begin = 0u, sel_end = C;  // the entries `each` visits (pool_select narrows them)
@@ -4025,31 +4073,40 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
         f(i < (uint32_t)kPoolListCap ? sm.u.list[i] : region[i]);
     };
     // Every candidate's key lies between theta's and the row max's.
-    float mx = lane < kPoolWaves ? sm.stats[lane].max : -INFINITY;
-    mx = wave_max(mx);
-    const uint64_t thr = pool_select(sm, each, (uint32_t)kk, key_of(theta), key_of(mx), C, sel_begin, sel_end);
+    const uint64_t thr = pool_select(sm, each, (uint32_t)kk, key_of(theta), key_of(rs.max), C, sel_begin, sel_end);
     sel_begin = 0u;  // the gather below visits every candidate
     sel_end = C;
     if (threadIdx.x == 0) sm.bs.slot = 0u;
-    __syncthreads();
+    __syncthreads();  // (also: the selection's last histogram reads are done, `sorted` is free)
     // region[0 .. kk) lies below the overflow entries (kk <= 1,024 < kPoolListCap).
     if (w == 0) TABBY_STAMP(18);
     each([&](uint64_t v) {
       const bool take = v >= thr;
       const uint32_t at = wave_slot(take, &sm.bs.slot);
-      if (take && at < (uint32_t)kk) region[at] = v;
+      if (take && at < (uint32_t)kk) put(at, v);
     });
     kept = (uint32_t)kk;
   } else if (kk > 0) {
-    for (uint32_t i = threadIdx.x; i < C; i += kPoolThreads) region[i] = sm.u.list[i];  // C <= kk: in LDS
+    for (uint32_t i = threadIdx.x; i < C; i += kPoolThreads) put(i, sm.u.list[i]);  // C <= kk: in LDS
     kept = C;
   }
+  if (here) {
+    // sampleFromTopK over the pool, as merge_kernel would: the statistics are this row's one
+    // slice's (the merge's sum in slice order is that slice's sum), the pool sorted descending.
+    const int count = (int)kept;
+    const int npow = next_pow2(count);
+    for (int i = count + (int)threadIdx.x; i < npow; i += kPoolThreads) sm.sorted[i] = 0ull;
+    __syncthreads();  // the gather's reads of the list are done: finish_row reuses it
+    if (w == 0) TABBY_STAMP(19);
+    block_sort_desc<kPoolWaves, 1>(sm.sorted, npow);
+    if (w == 0) TABBY_STAMP(20);
+    finish_row<kKcapLarge, In, PoolSmem, kPoolWaves>(sm, L, row, src, count, rs.max, rs.sum_exp, P);
+  }
   if (w == 0) {
-    const RowStats rs = row_stats(sm.stats, kPoolWaves);
     if (lane == 0) {
       SliceStat st;
       st.max = rs.max;
-      st.count = kept;
+      st.count = here ? kPoolRowDone : kept;
       st.sum = rs.sum_exp;
       W.stats[(size_t)row * kMaxSplits] = st;
     }
