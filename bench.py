@@ -324,6 +324,20 @@ def _usable_cpus() -> dict:
     return out
 
 
+def cu_pairs(where, end, pct):
+    """Percentiles of the earlier and the later stream end among workgroups that shared a CU."""
+    import numpy as np
+    first, second = [], []
+    for cu in np.unique(where):
+        e = np.sort(end[where == cu])
+        if len(e) >= 2:
+            first.append(e[0])
+            second.append(e[-1])
+    if not first:
+        return None
+    return {"cus": len(first), "earlier": pct(np.array(first)), "later": pct(np.array(second))}
+
+
 def timeline(args) -> int:
     """--timeline: the headline's row_kernel phases, from the timeline library's stamps."""
     import ctypes
@@ -401,6 +415,9 @@ def timeline(args) -> int:
             "candidates_per_row": {p: int(v) for p, v in pct(tl[:, 31]).items()},
             "key_passes_per_row": {p: int(v) for p, v in pct(tl[:, 26]).items()},
             "stream_end_by_wave": [round(float(x), 2) for x in waves.mean(0)],
+            # The two workgroups on each CU (slot 30: XCC and CU): the earlier and the later
+            # to end its stream (us from the first row's start, real time).
+            "stream_end_on_cu": cu_pairs(tl[:, 30], last + (rt0 - rt0.min()) * 1e-2, pct),
             "library": os.path.relpath(B.TIMELINE_LIB_PATH, ROOT),
         }))
         return 0

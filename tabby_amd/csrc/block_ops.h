@@ -226,6 +226,57 @@ __device__ __forceinline__ void block_sort_desc(uint64_t *a, int n) {
   }
 }
 
+// In-place descending sort of a[0..n), n a power of two and at most NW * 64, by the whole
+// workgroup of NW waves, through tmp[0..n) in LDS: each wave sorts 64 entries in registers,
+// then log2(n / 64) merge rounds, each a barrier: an entry's place in the merged pair of runs
+// is its place in its own run plus the entries of the other run ahead of it, found by binary
+// search (an equal entry of the left run counts as ahead of the right run's, so that equal
+// entries -- the zero padding -- still take distinct places). Against the bitonic network
+// above that is one barrier per doubling instead of one per stride, and a dependent LDS read
+// per halving instead of a compare-exchange stage.
+template <int NW>
+__device__ __forceinline__ void block_merge_sort_desc(uint64_t *a, uint64_t *tmp, int n) {
+  const int t = (int)threadIdx.x, lane = t & 63;
+  if (n <= 64) {
+    if (t < 64) {
+      uint64_t v[1] = {lane < n ? a[lane] : 0ull};
+      wave_sort_desc<1>(v);
+      if (lane < n) a[lane] = v[0];
+    }
+    __syncthreads();
+    return;
+  }
+  if (t < n) {
+    uint64_t v[1] = {a[t]};
+    wave_sort_desc<1>(v);
+    a[t] = v[0];
+  }
+  __syncthreads();
+  uint64_t *src = a, *dst = tmp;
+  for (int len = 64; len < n; len <<= 1) {
+    if (t < n) {
+      const uint64_t x = src[t];
+      const int run = t / len, i = t - run * len;
+      const bool left = (run & 1) == 0;
+      const uint64_t *other = src + (run ^ 1) * len;
+      auto ahead = [&](uint64_t y) { return left ? y > x : y >= x; };
+      int pos = 0;  // entries of `other` ahead of x: a prefix of it
+      for (int step = len >> 1; step > 0; step >>= 1)
+        if (ahead(other[pos + step - 1])) pos += step;
+      pos += ahead(other[pos]) ? 1 : 0;  // only at pos == len - 1 can other[pos] be ahead
+      dst[(run & ~1) * len + i + pos] = x;
+    }
+    __syncthreads();
+    uint64_t *const s2 = src;
+    src = dst;
+    dst = s2;
+  }
+  if (src != a) {
+    if (t < n) a[t] = src[t];
+    __syncthreads();
+  }
+}
+
 __host__ __device__ __forceinline__ int next_pow2(int v) {
   int p = 1;
   while (p < v) p <<= 1;

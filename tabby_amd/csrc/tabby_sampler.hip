@@ -60,7 +60,7 @@
 // time). pool_row_kernel (pools above 256) uses slots 0-15, 16/24, 22 and 21/25 the same way,
 // 17 for the barrier after the stream, 23 for the selection's key passes done, 18 for the
 // selection done, 19 for the pool gathered, 20 for the pool sorted, and records its candidate
-// count in slot 31 and its key passes in slot 26 (TABBY_RECORD).
+// count in slot 31, its key passes in slot 26 and where it ran in slot 30 (TABBY_RECORD).
 #ifdef TABBY_TIMELINE
 namespace tabby {
 constexpr int kTimelineSlots = 32;
@@ -3699,6 +3699,7 @@ struct PoolSmem {
       double exact[kKcapLarge];
       double w[kKcapLarge];
     } tail;  // finish_row's terms, once the pool is in `sorted`
+    uint64_t merge[kKcapLarge];  // the sort's second buffer, before those
   } u;
   union {
     uint32_t hist[kPoolHistPad];
@@ -3712,6 +3713,7 @@ struct PoolSmem {
   int next_chunk;
 };
 static_assert(sizeof(uint64_t) * kKcapLarge <= sizeof(uint32_t) * kPoolHistPad, "the pool fits the histogram's words");
+static_assert(kKcapLarge <= kPoolThreads, "block_merge_sort_desc sorts one entry per thread");
 
 // One histogram pass of the pool kernel's selections, by the whole workgroup: the entries
 // that bin_of admits (bin >= 0; bin 0 holds the largest) are counted, and wave 0 finds the
@@ -3972,7 +3974,7 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
   float lane_max = -INFINITY;
   float lane_ml = 0.0f;   // the reference of lane_sum's terms (as in wave_slice)
   double lane_sum = 0.0;
-  auto step = [&](int c, float(&cur)[kWChunkPerLane]) {
+  auto step = [&](int c, float(&cur)[kWChunkPerLane]) __attribute__((always_inline)) {
     mask_tail(c, cur);
     float cm = cur[0];
 #pragma unroll
@@ -4098,7 +4100,7 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     for (int i = count + (int)threadIdx.x; i < npow; i += kPoolThreads) sm.sorted[i] = 0ull;
     __syncthreads();  // the gather's reads of the list are done: finish_row reuses it
     if (w == 0) TABBY_STAMP(19);
-    block_sort_desc<kPoolWaves, 1>(sm.sorted, npow);
+    block_merge_sort_desc<kPoolWaves>(sm.sorted, sm.u.merge, npow);
     if (w == 0) TABBY_STAMP(20);
     finish_row<kKcapLarge, In, PoolSmem, kPoolWaves>(sm, L, row, src, count, rs.max, rs.sum_exp, P);
   }
