@@ -116,7 +116,8 @@ struct SliceStat {
   uint32_t count; // candidates written
   double sum;     // sum over the slice of exp(x - max)
 };
-// SliceStat.count of a row that pool_row_kernel sampled itself: merge_kernel skips the row.
+// SliceStat.count of a row that pool_row_kernel ended itself (sampled, or its status written):
+// merge_kernel skips the row.
 constexpr uint32_t kPoolRowDone = 0xffffffffu;
 
 // Per-row hand-over from the sampling kernel to the head kernel (whole-vocabulary rows).
@@ -4062,13 +4063,23 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     TABBY_RECORD(31, C);
   }
   const RowStats rs = row_stats(sm.stats, kPoolWaves);
-  const bool here = valid_params && keff <= L.kcap && rs.max > -INFINITY && rs.max < INFINITY &&
-                    rs.sum_exp > 0.0 && rs.sum_exp < INFINITY && kk > 0 && C > 0u;
+  // The row's outcome, as merge_kernel decides it: a status (parameters outside the contract,
+  // statistics outside the domain, a whole-vocabulary row with no head pass), a pool this
+  // workgroup samples (`here`), or a whole-vocabulary row for merge_kernel and the head
+  // kernels. (C >= kk >= 1 for a pool in the domain: theta has kk elements at or above it.)
+  const bool in_domain = rs.max > -INFINITY && rs.max < INFINITY && rs.sum_exp > 0.0 && rs.sum_exp < INFINITY;
+  const bool pool = keff <= L.kcap;
+  int32_t status = TABBY_OK;
+  if (!valid_params || !in_domain) status = !valid_params ? TABBY_EINVAL : TABBY_EDOMAIN;
+  else if (!pool && !L.head_pass) status = TABBY_EINVAL;
+  else if (pool && C == 0u) status = TABBY_EDOMAIN;
+  const bool here = status == TABBY_OK && pool;
   auto put = [&](uint32_t at, uint64_t v) {
     if (here) sm.sorted[at] = v; else region[at] = v;
   };
   uint32_t kept = 0u;
-  if (kk > 0 && C > (uint32_t)kk) {
+  const bool selects = status == TABBY_OK && kk > 0;
+  if (selects && C > (uint32_t)kk) {
     uint32_t sel_begin = 0u, sel_end = C;  // the entries `each` visits (pool_select narrows them)
     auto each = [&](auto &&f) {
       for (uint32_t i = sel_begin + threadIdx.x; i < sel_end; i += kPoolThreads)
@@ -4088,7 +4099,7 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       if (take && at < (uint32_t)kk) put(at, v);
     });
     kept = (uint32_t)kk;
-  } else if (kk > 0) {
+  } else if (selects) {
     for (uint32_t i = threadIdx.x; i < C; i += kPoolThreads) put(i, sm.u.list[i]);  // C <= kk: in LDS
     kept = C;
   }
@@ -4108,9 +4119,13 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     if (lane == 0) {
       SliceStat st;
       st.max = rs.max;
-      st.count = here ? kPoolRowDone : kept;
+      st.count = here || status != TABBY_OK ? kPoolRowDone : kept;
       st.sum = rs.sum_exp;
       W.stats[(size_t)row * kMaxSplits] = st;
+      if (status != TABBY_OK) {
+        write_status(L, row, status, rs.max, rs.sum_exp);
+        W.row_state[row].status = status;
+      }
     }
     TABBY_STAMP(21);
     TABBY_STAMP_REAL(25);
@@ -4269,8 +4284,11 @@ hipError_t launch_pair(const Launch &L, const Workspace &W, int cus, hipStream_t
     hipLaunchKernelGGL((wave_kernel<In, VEC>), slices, dim3(kWaveSize), 0, stream, L, W);
     hipLaunchKernelGGL((wave_merge_kernel<In>), rows, dim3(kBlock), 0, stream, L, W);
   } else if (L.pool_rows) {
+    // pool_row_kernel ends every row but a head pass's whole-vocabulary ones, which
+    // merge_kernel hands to the head kernels.
     hipLaunchKernelGGL((pool_row_kernel<In, VEC>), rows, dim3(kPoolThreads), 0, stream, L, W);
-    hipLaunchKernelGGL((merge_kernel<kKcapLarge, In>), rows, dim3(kBlock), 0, stream, L, W);
+    if (L.head_pass)
+      hipLaunchKernelGGL((merge_kernel<kKcapLarge, In>), rows, dim3(kBlock), 0, stream, L, W);
   } else {
     hipLaunchKernelGGL((slice_kernel<In, VEC>), slices, dim3(kBlock), 0, stream, L, W);
     hipLaunchKernelGGL((merge_kernel<kKcapLarge, In>), rows, dim3(kBlock), 0, stream, L, W);
