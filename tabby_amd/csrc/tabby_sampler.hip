@@ -3727,12 +3727,49 @@ struct PoolBin {
 
 __device__ __forceinline__ int pool_hist_at(int b) { return b + (b >> 5); }
 
-template <class Each, class BinOf>
-__device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Each each, BinOf bin_of, uint32_t need) {
+// The selection visits the candidate list in batches: `batches(g)` loads kPoolBatch entries
+// per lane (all in flight before the first is used) and calls g(v, ok) with them; each_of
+// hands the valid ones to f one by one.
+constexpr int kPoolBatch = 4;
+template <class Batches, class F>
+__device__ __forceinline__ void each_of(Batches &batches, F &&f) {
+  batches([&](const uint64_t (&v)[kPoolBatch], const bool (&ok)[kPoolBatch]) {
+#pragma unroll
+    for (int u = 0; u < kPoolBatch; ++u)
+      if (ok[u]) f(v[u]);
+  });
+}
+
+// wave_slot for a batch: slots for every taken entry of the lanes' B entries, with one LDS
+// atomic for the wave (pos[u] is set where take[u]).
+template <int B>
+__device__ __forceinline__ void wave_slots(const bool (&take)[B], uint32_t *slot, uint32_t (&pos)[B]) {
+  uint64_t m[B], any = 0ull;
+  uint32_t total = 0u;
+#pragma unroll
+  for (int u = 0; u < B; ++u) {
+    m[u] = __ballot(take[u]);
+    any |= m[u];
+    total += (uint32_t)__popcll(m[u]);
+  }
+  if (!any) return;
+  const int leader = __ffsll((unsigned long long)any) - 1;  // a lane that takes: active
+  uint32_t base = 0u;
+  if ((int)lane_id() == leader) base = atomicAdd(slot, total);
+  base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
+#pragma unroll
+  for (int u = 0; u < B; ++u) {
+    pos[u] = base + lanes_below(m[u]);
+    base += (uint32_t)__popcll(m[u]);
+  }
+}
+
+template <class Batches, class BinOf>
+__device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Batches &batches, BinOf bin_of, uint32_t need) {
   static_assert(kPoolHistPad % 4 == 0 && kPoolHistPad <= 4 * kPoolThreads, "one 16-byte store per thread");
   if ((int)threadIdx.x < kPoolHistPad / 4) reinterpret_cast<u32x4 *>(sm.hist)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
-  each([&](uint64_t v) {
+  each_of(batches, [&](uint64_t v) {
     const int b = bin_of(v);
     // Lanes whose entries all fall in one bin (a tied key's entries do) add their count
     // with one atomic: 64 atomics on one LDS address serialise.
@@ -3789,8 +3826,8 @@ __device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Each each, BinOf bin_
 // that leaves its bin exactly taken ends early.
 // The rest of pool_select from a key range [lo, hi] that holds the `need`-th entry: narrower
 // key passes until one key remains, then that key's ties by their indices' digits.
-template <class Each>
-__device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Each each, uint32_t need, uint32_t lo,
+template <class Batches>
+__device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Batches &batches, uint32_t need, uint32_t lo,
                                                      uint32_t hi, int key_passes) {
   while (lo != hi) {
     ++key_passes;
@@ -3798,7 +3835,7 @@ __device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Each each, ui
     const int bits = 32 - __builtin_clz(range);
     const int shift = bits > 11 ? bits - 11 : 0;
     const uint32_t top_key = hi, low_key = lo;
-    const PoolBin r = pool_pass(sm, each, [&](uint64_t v) {
+    const PoolBin r = pool_pass(sm, batches, [&](uint64_t v) {
       const uint32_t k = composite_key(v);
       return (k >= low_key && k <= top_key) ? (int)((top_key - k) >> shift) : -1;
     }, need);
@@ -3828,7 +3865,7 @@ __device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Each each, ui
     const uint32_t mask = p == 0 ? 0x7ffu : 0x3ffu;
     const uint64_t want = prefix >> done;
     const int d = done;
-    const PoolBin r = pool_pass(sm, each, [&](uint64_t v) {
+    const PoolBin r = pool_pass(sm, batches, [&](uint64_t v) {
       return (v >> d) == want ? (int)(mask - ((uint32_t)(v >> sh) & mask)) : -1;
     }, need);
     need -= r.above;
@@ -3840,22 +3877,22 @@ __device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Each each, ui
 }
 
 // The row's kk-th largest candidate composite (need = kk entries at or above it), among the
-// candidates that `each` visits -- entries [sel_begin, sel_end) of the list (list[i] in LDS
+// candidates that `batches` visits -- entries [sel_begin, sel_end) of the list (list[i] in LDS
 // for i < kPoolListCap, else region[i]), at first the C candidates -- all with keys in
 // [lo, hi]: histogram passes over the keys (2,048 bins of the candidates' own range, narrowed
 // until one key remains -- a quantized row resolves in one), then over the tied key's index
 // digits. After the first pass only the chosen bin's entries matter: they are copied behind
-// the candidates (B entries at list[C ..), when C + B fits the LDS list) and `each` is moved
+// the candidates (B entries at list[C ..), when C + B fits the LDS list) and `batches` is moved
 // onto them, so the later passes visit those B alone instead of all C (config 5: ~6,300
 // candidates, a tied bin of a few hundred; the later passes had re-read every candidate).
-template <class Each>
-__device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Each each, uint32_t need, uint32_t lo, uint32_t hi,
+template <class Batches>
+__device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Batches &batches, uint32_t need, uint32_t lo, uint32_t hi,
                                                 uint32_t C, uint32_t &sel_begin, uint32_t &sel_end) {
-  if (lo == hi) return pool_select_from(sm, each, need, lo, hi, 0);
+  if (lo == hi) return pool_select_from(sm, batches, need, lo, hi, 0);
   const uint32_t range = hi - lo;
   const int bits = 32 - __builtin_clz(range);
   const int shift = bits > 11 ? bits - 11 : 0;
-  const PoolBin r = pool_pass(sm, each, [&](uint64_t v) {
+  const PoolBin r = pool_pass(sm, batches, [&](uint64_t v) {
     const uint32_t k = composite_key(v);
     return (k >= lo && k <= hi) ? (int)((hi - k) >> shift) : -1;
   }, need);
@@ -3869,7 +3906,7 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Each each, uint32_
     }
     return (uint64_t)bin_low << 32;
   }
-  if (shift == 0 || C + r.count > (uint32_t)kPoolListCap) return pool_select_from(sm, each, need, bin_low, bin_top, 1);
+  if (shift == 0 || C + r.count > (uint32_t)kPoolListCap) return pool_select_from(sm, batches, need, bin_low, bin_top, 1);
   // The chosen bin's entries, copied to list[C, C + B), and their smallest and largest key
   // (the later passes bin [smallest, largest]; one key -- a tie -- goes straight to the index
   // digits).
@@ -3880,14 +3917,23 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Each each, uint32_
   }
   __syncthreads();
   uint32_t kmin = ~0u, kmax = 0u;
-  each([&](uint64_t v) {
-    const uint32_t k = composite_key(v);
-    const bool in = k >= bin_low && k <= bin_top;
-    const uint32_t at = wave_slot(in, &sm.bs.slot2);
-    if (in) {
-      sm.u.list[C + at] = v;
-      kmin = min(kmin, k);
-      kmax = max(kmax, k);
+  batches([&](const uint64_t (&v)[kPoolBatch], const bool (&ok)[kPoolBatch]) {
+    bool in[kPoolBatch];
+    uint32_t at[kPoolBatch];
+#pragma unroll
+    for (int u = 0; u < kPoolBatch; ++u) {
+      const uint32_t k = composite_key(v[u]);
+      in[u] = ok[u] && k >= bin_low && k <= bin_top;
+    }
+    wave_slots(in, &sm.bs.slot2, at);
+#pragma unroll
+    for (int u = 0; u < kPoolBatch; ++u) {
+      if (in[u]) {
+        const uint32_t k = composite_key(v[u]);
+        sm.u.list[C + at[u]] = v[u];
+        kmin = min(kmin, k);
+        kmax = max(kmax, k);
+      }
     }
   });
   kmin = ~wave_max_u32(~kmin);
@@ -3901,7 +3947,7 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Each each, uint32_
   sel_end = C + sm.bs.slot2;  // the bin's r.count entries
   const uint32_t lo2 = sm.bs.u[0], hi2 = sm.bs.u[1];
   __syncthreads();  // sm.bs is reused
-  return pool_select_from(sm, each, need, lo2, hi2, 1);
+  return pool_select_from(sm, batches, need, lo2, hi2, 1);
 }
 
 // Two workgroups per CU (74 KB of LDS and at most 64 VGPRs each): one's bound and selection
@@ -4080,23 +4126,37 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
   uint32_t kept = 0u;
   const bool selects = status == TABBY_OK && kk > 0;
   if (selects && C > (uint32_t)kk) {
-    uint32_t sel_begin = 0u, sel_end = C;  // the entries `each` visits (pool_select narrows them)
-    auto each = [&](auto &&f) {
-      for (uint32_t i = sel_begin + threadIdx.x; i < sel_end; i += kPoolThreads)
-        f(i < (uint32_t)kPoolListCap ? sm.u.list[i] : region[i]);
+    uint32_t sel_begin = 0u, sel_end = C;  // the entries `batches` visits (pool_select narrows them)
+    auto batches = [&](auto &&g) {
+      for (uint32_t base = sel_begin; base < sel_end; base += kPoolBatch * kPoolThreads) {
+        uint64_t v[kPoolBatch];
+        bool ok[kPoolBatch];
+#pragma unroll
+        for (int u = 0; u < kPoolBatch; ++u) {
+          const uint32_t i = base + u * kPoolThreads + threadIdx.x;
+          ok[u] = i < sel_end;
+          v[u] = !ok[u] ? 0ull : i < (uint32_t)kPoolListCap ? sm.u.list[i] : region[i];
+        }
+        g(v, ok);
+      }
     };
     // Every candidate's key lies between theta's and the row max's.
-    const uint64_t thr = pool_select(sm, each, (uint32_t)kk, key_of(theta), key_of(rs.max), C, sel_begin, sel_end);
+    const uint64_t thr = pool_select(sm, batches, (uint32_t)kk, key_of(theta), key_of(rs.max), C, sel_begin, sel_end);
     sel_begin = 0u;  // the gather below visits every candidate
     sel_end = C;
     if (threadIdx.x == 0) sm.bs.slot = 0u;
     __syncthreads();  // (also: the selection's last histogram reads are done, `sorted` is free)
     // region[0 .. kk) lies below the overflow entries (kk <= 1,024 < kPoolListCap).
     if (w == 0) TABBY_STAMP(18);
-    each([&](uint64_t v) {
-      const bool take = v >= thr;
-      const uint32_t at = wave_slot(take, &sm.bs.slot);
-      if (take && at < (uint32_t)kk) put(at, v);
+    batches([&](const uint64_t (&v)[kPoolBatch], const bool (&ok)[kPoolBatch]) {
+      bool take[kPoolBatch];
+      uint32_t at[kPoolBatch];
+#pragma unroll
+      for (int u = 0; u < kPoolBatch; ++u) take[u] = ok[u] && v[u] >= thr;
+      wave_slots(take, &sm.bs.slot, at);
+#pragma unroll
+      for (int u = 0; u < kPoolBatch; ++u)
+        if (take[u] && at[u] < (uint32_t)kk) put(at[u], v[u]);
     });
     kept = (uint32_t)kk;
   } else if (selects) {
