@@ -324,6 +324,22 @@ def _usable_cpus() -> dict:
     return out
 
 
+# The kernels one call of each workload launches (the roofline's "kernel" field).
+CALL_KERNELS = {
+    None: "row_kernel, one workgroup per row (streaming: max, sum-exp, candidates; then in LDS "
+          "the exact top-k, top-p and draw)",
+    1: "row_kernel, one workgroup streaming the row and sampling it",
+    2: "row_kernel on parts of the row, then wave_merge_kernel merging their lists and sampling",
+    3: "row_kernel, one workgroup per row (streaming: max, sum-exp, candidates; then in LDS "
+       "the exact top-k, top-p and draw)",
+    4: "row_kernel on parts of each row, wave_merge_kernel (statistics, head key, top list), "
+       "then the head kernels (head_kernel re-reads the row for its head, head_fast_kernel "
+       "finishes it; head_sort_kernel and head_finish_kernel for rows it cannot)",
+    5: "pool_row_kernel, one workgroup per row (streaming with candidate appends; then in LDS "
+       "the exact top-1024 selection, its sort, top-p and the draw)",
+}
+
+
 def cu_pairs(where, end, pct):
     """Percentiles of the earlier and the later stream end among workgroups that shared a CU."""
     import numpy as np
@@ -642,10 +658,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": ("one tabby_sampler_sample_device call = row_kernel, one workgroup per "
-                       "row (streaming: max, sum-exp, candidates; then in LDS the exact top-k, "
-                       "top-p and draw); duration = HIP-event time of the back-to-back timed "
-                       "calls / steps") if not args.host_params else
+            "kernel": (f"one tabby_sampler_sample_device call = {CALL_KERNELS.get(args.config, CALL_KERNELS[None])}; "
+                       "duration = HIP-event time of the back-to-back timed calls / steps")
+                      if not args.host_params else
                       ("one synchronous tabby_sampler_sample call (parameter upload, the "
                        "sampling kernels, result read-back); duration = HIP-event time / steps"),
             "bytes_per_launch": bytes_per_launch,
