@@ -3682,8 +3682,10 @@ __global__ void exp_kernel(const double *x, double *y, int64_t n) {
 // it, so it never exceeds the row's kk-th largest. (The 4-wave slice kernel started from
 // the first chunk's kk-th largest -- a quarter of that chunk at kk = 1,024 -- and pruned its
 // list with two workgroup barriers per chunk: config 5 took 135 us there.) At the end the
-// workgroup selects the row's exact top kk from the list (radix select over composites) and
-// writes it, unsorted, with the row's statistics, as slice 0 for merge_kernel.
+// workgroup selects the row's exact top kk from the list (pool_select), gathers it into LDS,
+// sorts it and samples it (finish_row over its 16 waves), as merge_kernel would have; a row
+// outside the contract gets its status here too. Only a head pass's whole-vocabulary rows
+// leave their top list, unsorted, with the row's statistics, as slice 0 for merge_kernel.
 // ---------------------------------------------------------------------------------------
 constexpr int kPoolWaves = 16;
 constexpr int kPoolThreads = kPoolWaves * kWaveSize;
@@ -3950,8 +3952,10 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Batches &batches, 
   return pool_select_from(sm, batches, need, lo2, hi2, 1);
 }
 
-// Two workgroups per CU (74 KB of LDS and at most 64 VGPRs each): one's bound and selection
-// overlap the other's streaming, and 512 rows run in one round.
+// Two workgroups per CU (74 KB of LDS and at most 64 VGPRs each): 512 rows run in one round,
+// and one row's bound and tail overlap the other's streaming (the SIMDs issue the older
+// workgroup's waves first, so the first-dispatched row ends its stream well before the
+// other, whose tail alone then runs with nothing streaming beside it).
 template <typename In, int VEC>
 __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Workspace W) {
   __shared__ PoolSmem sm;
@@ -4401,7 +4405,8 @@ Plan plan_launch(int rows, int vocab, int dtype, const void *logits, int k_max, 
   L.row_waves = 0;
   L.pool_rows = 0;
   if (kcap > kWaveKcap && rows >= cus) {
-    // One pool_row_kernel workgroup per row; merge_kernel reads its list as slice 0.
+    // One pool_row_kernel workgroup per row (merge_kernel, for a head pass, reads a
+    // whole-vocabulary row's list as slice 0).
     L.pool_rows = 1;
     L.splits = 1;
     L.slice_len = vocab;
