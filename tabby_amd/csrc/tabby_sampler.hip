@@ -3036,26 +3036,27 @@ __global__ __launch_bounds__(kWaveSize) void head_kernel(Launch L, Workspace W) 
   __shared__ uint64_t list[kWListCap];
   int row, slice;
   row_slice_of((int)blockIdx.x, L.rows, L.h_splits, row, slice);
-  const tabby_row_params P = L.params[row];
-  const RowState rs = W.row_state[row];  // requested with the parameters: one round trip
-  if (!is_head_row(P, L) || rs.status != TABBY_OK) return;
   const int V = L.vocab, lane = wave_lane();
   const int begin = slice * L.h_slice_len;
   const int n = min(L.h_slice_len, V - begin);
   const int nchunks = (n + kWChunk - 1) / kWChunk;
   const int full_chunks = n / kWChunk;
   const In *src = reinterpret_cast<const In *>(L.logits) + (size_t)row * V + begin;
+  // Both chunks' loads at once (a slice's second chunk past the row's end reads zeros),
+  // issued with the row's parameters and state rather than after them: one round trip for
+  // all three (a row that turns out to need no head pass has read its slice for nothing).
+  float x[kWChunkPerLane], y[kWChunkPerLane];
+  const ChunkReader<In, VEC> rd(src, n);
+  rd.load(0, x);
+  rd.load(1, y);
+  const tabby_row_params P = L.params[row];
+  const RowState rs = W.row_state[row];
+  if (!is_head_row(P, L) || rs.status != TABBY_OK) return;
   const float hv = value_of(rs.head_key);
   // This slice's part of the head goes to its own range of the row's head buffer (no
   // atomics: a row's slices appending to one counter serialised on it).
   uint64_t *head = W.head + (size_t)row * W.head_stride + begin;
   int stored = 0;
-
-  // Both chunks' loads at once (a slice's second chunk past the row's end reads zeros).
-  float x[kWChunkPerLane], y[kWChunkPerLane];
-  const ChunkReader<In, VEC> rd(src, n);
-  rd.load(0, x);
-  rd.load(1, y);
   // The ulp of P_N (the sequential sum of the top N's terms, from the merge).
   const int N = (int)(rs.handoff >> 16);
   const double T = P.temperature, M = (double)rs.max;
