@@ -3585,28 +3585,43 @@ __global__ __launch_bounds__(kPlanThreads) void head_fast_kernel(Launch L, Works
   uint32_t *plan = W.head_plan + (size_t)row * W.plan_stride;
   const tabby_row_params P = L.params[row];
   const RowState rs = W.row_state[row];
-  // Every slice's head count is requested with them (one slice per thread).
+  // Every slice's head count is requested with them (one slice per thread), and so are, by
+  // wave 0, the fast finish's inputs: the merge's top list (its first kWaveKcap slots, of
+  // which the row state then says how many hold it) and head_kernel's ulp counts, slice by
+  // slice -- one round trip for all.
   const int ns = L.h_splits;
   const uint32_t c = (int)threadIdx.x < ns ? W.head_slice_count[(size_t)row * W.acc_stride + threadIdx.x] : 0u;
+  constexpr int kTopRegs = kWaveKcap / kWaveSize;
+  uint64_t top[kTopRegs];
+  double r = 0.0, ties = 0.0, outside = 0.0;
+  if (wave_id() == 0) {
+    const uint64_t *list = W.head_sorted + (size_t)row * W.head_stride;
+#pragma unroll
+    for (int q = 0; q < kTopRegs; ++q) {
+      const int i = q * kWaveSize + wave_lane();
+      top[q] = i < W.head_stride ? list[i] : 0ull;
+    }
+    const double *acc = W.head_acc + (size_t)row * W.acc_stride * 3;
+    for (int i = wave_lane(); i < ns; i += kWaveSize) {
+      r += acc[3 * i];
+      ties += acc[3 * i + 1];
+      outside += acc[3 * i + 2];
+    }
+  }
   if (!is_head_row(P, L) || rs.status != TABBY_OK) {
     if (threadIdx.x == 0) plan[0] = 0u;
     return;
   }
-  // Wave 0 starts the fast finish's loads -- the top list and head_kernel's counts, slice by
-  // slice -- before the scan below.
   const int N = (int)(rs.handoff >> 16);
-  double r = 0.0, ties = 0.0, outside = 0.0;
-  if (wave_id() == 0 && N > 0 && N <= kWaveKcap) {
-    const uint64_t *list = W.head_sorted + (size_t)row * W.head_stride;
-    for (int i = wave_lane(); i < N; i += kWaveSize) sm.top[i] = list[i];
-    if (!greedy_temp(P.temperature)) {
-      const double *acc = W.head_acc + (size_t)row * W.acc_stride * 3;
-      for (int i = wave_lane(); i < L.h_splits; i += kWaveSize) {
-        r += acc[3 * i];
-        ties += acc[3 * i + 1];
-        outside += acc[3 * i + 2];
+  if (wave_id() == 0) {
+    if (N > 0 && N <= kWaveKcap) {
+#pragma unroll
+      for (int q = 0; q < kTopRegs; ++q) {
+        const int i = q * kWaveSize + wave_lane();
+        if (i < N) sm.top[i] = top[q];
       }
     }
+    if (!(N > 0 && N <= kWaveKcap) || greedy_temp(P.temperature)) r = ties = outside = 0.0;
   }
   // The head's size and where each slice's entries start (every thread holds one slice).
   const uint32_t inc = wave_inclusive_scan_u32(c);
