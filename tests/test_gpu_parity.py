@@ -7,7 +7,7 @@ import pytest
 from tabby_amd import sampler as S
 from tabby_amd import synth
 
-from parity import compare, params_of, run_gpu, run_oracle
+from parity import REL_TOL, compare, params_of, rel, run_gpu, run_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -109,6 +109,48 @@ def test_pool_row_kernel_rows_outside_contract(oracle):
             o = oracle.sample_row(logits[r], int(p[r]["top_k"]), float(p[r]["temperature"]),
                                   float(p[r]["top_p"]), float(p[r]["uniform"]))
             assert (int(res["id"][r]), int(res["considered"][r])) == (o["id"], o["considered"]), f"row {r}"
+
+
+def test_pool_row_kernel_batch_with_head_pass(oracle):
+    # 256 rows with k_max 1024 and TABBY_FLAG_FULL_VOCAB: pool_row_kernel samples the pools
+    # (k 50, 300, 1000) and writes the statuses itself, and hands the whole-vocabulary rows
+    # (k 0) to merge_kernel and the head kernels, which skip the rows it ended.
+    import torch
+    w = synth.random_workload(rows=256, vocab=4000, seed=31, k_choices=(0, 50, 300, 1000), ties=True,
+                              neg_inf_frac=0.05)
+    w.logits[17] = -np.inf
+    w.logits[140, 7] = np.nan
+    params = np.zeros(w.rows, dtype=S.PARAMS_DTYPE)
+    params["temperature"], params["top_p"], params["uniform"], params["top_k"] = (
+        w.temperature, w.top_p, w.uniform, w.top_k)
+    params["top_k"][99] = 2000  # above k_max: EINVAL
+    x = torch.from_numpy(np.ascontiguousarray(w.logits)).cuda()
+    pd = torch.from_numpy(params.view(np.uint8).copy()).cuda()
+    rd = torch.zeros(w.rows * S.RESULT_DTYPE.itemsize, dtype=torch.uint8, device="cuda")
+    with S.GpuSampler(vocab_max=w.vocab, rows_max=w.rows, k_max=1024) as g:
+        g.sample_device(x, pd, rd, flags=S.TABBY_FLAG_FULL_VOCAB)
+        res = rd.cpu().numpy().view(S.RESULT_DTYPE).copy()
+    logits = w.logits_f32()
+    sampled = 0
+    for r in range(w.rows):
+        if r in (17, 140):
+            assert int(res["status"][r]) == S.TABBY_EDOMAIN, f"row {r}"
+            continue
+        if r == 99:
+            assert int(res["status"][r]) == S.TABBY_EINVAL, f"row {r}"
+            continue
+        k, T, p, u = (int(params[r]["top_k"]), float(params[r]["temperature"]), float(params[r]["top_p"]),
+                      float(params[r]["uniform"]))
+        o = oracle.sample_row(logits[r], k, T, p, u)
+        c = f"row {r}: k={k} T={T} p={p} u={u!r}"
+        assert int(res["status"][r]) == o["status"] == 0, c
+        assert (int(res["id"][r]), int(res["considered"][r])) == (o["id"], o["considered"]), c
+        assert np.float32(res["max_logit"][r]) == np.float32(o["max_logit"]), c
+        for f in ("probability", "pool_mass", "sum_exp"):
+            assert rel(float(res[f][r]), o[f]) < REL_TOL, (c, f)
+        sampled += 1
+    assert sampled == w.rows - 3
+    _log("pool rows with a head pass", {"rows": sampled})
 
 
 def test_f16_input_finite_k(oracle):
