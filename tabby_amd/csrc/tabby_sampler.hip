@@ -4070,31 +4070,37 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       for (int e = 0; e < kWChunkPerLane; ++e)
         if (wave_local<VEC>(c, e) >= n) cur[e] = __builtin_nanf("");
     }
-    // The chunk's candidates: counted first, then one reservation for the wave, then the
-    // same ballots again for the appends (keeping sixteen 64-bit masks live spilled registers).
-    uint32_t total = 0;
+    // The chunk's candidates: each lane counts its own, a wave scan places the lanes' runs
+    // one after another behind one reservation for the wave, and each lane writes its
+    // candidates to its run in element order (a compare, the entry and its store per
+    // element; placing every element's takers by a ballot and a lane count cost four
+    // instructions more per element).
+    uint32_t mine = 0u;
 #pragma unroll
-    for (int e = 0; e < kWChunkPerLane; ++e) total += (uint32_t)__popcll(__ballot(cur[e] >= theta));
+    for (int e = 0; e < kWChunkPerLane; ++e) mine += cur[e] >= theta ? 1u : 0u;
+    const uint32_t inc = wave_inclusive_scan_u32(mine);
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)inc, kWaveSize - 1);
     if (total == 0u) return;
     uint32_t at = 0u;
     if (lane == 0) at = atomicAdd(&sm.count, total);
     at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
+    uint32_t pos = at + inc - mine;
     auto append = [&](auto &&store) {
 #pragma unroll
       for (int e = 0; e < kWChunkPerLane; ++e) {
-        const bool take = cur[e] >= theta;
-        const uint64_t mask = __ballot(take);
-        if (take) store(at + lanes_below(mask), composite(key_of(cur[e]), (uint32_t)wave_local<VEC>(c, e)));
-        at += (uint32_t)__popcll(mask);
+        if (cur[e] >= theta) {
+          store(pos, composite(key_of(cur[e]), (uint32_t)wave_local<VEC>(c, e)));
+          ++pos;
+        }
       }
     };
     // A reservation inside the LDS list (all but the rarest) stores with no per-element test
     // of where the entry goes.
     if (at + total <= (uint32_t)kPoolListCap) {
-      append([&](uint32_t pos, uint64_t v) { sm.u.list[pos] = v; });
+      append([&](uint32_t q, uint64_t v) { sm.u.list[q] = v; });
     } else {
-      append([&](uint32_t pos, uint64_t v) {
-        if (pos < (uint32_t)kPoolListCap) sm.u.list[pos] = v; else region[pos] = v;
+      append([&](uint32_t q, uint64_t v) {
+        if (q < (uint32_t)kPoolListCap) sm.u.list[q] = v; else region[q] = v;
       });
     }
   };
