@@ -4085,23 +4085,23 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     if (lane == 0) at = atomicAdd(&sm.count, total);
     at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
     uint32_t pos = at + inc - mine;
-    auto append = [&](auto &&store) {
+    // A reservation inside the LDS list (all but the rarest) stores through a pointer that
+    // steps by one entry, with no per-element test of where the entry goes.
+    if (at + total <= (uint32_t)kPoolListCap) {
+      uint64_t *dst = sm.u.list + pos;
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e) {
+        if (cur[e] >= theta) *dst++ = composite(key_of(cur[e]), (uint32_t)wave_local<VEC>(c, e));
+      }
+    } else {
 #pragma unroll
       for (int e = 0; e < kWChunkPerLane; ++e) {
         if (cur[e] >= theta) {
-          store(pos, composite(key_of(cur[e]), (uint32_t)wave_local<VEC>(c, e)));
+          const uint64_t v = composite(key_of(cur[e]), (uint32_t)wave_local<VEC>(c, e));
+          if (pos < (uint32_t)kPoolListCap) sm.u.list[pos] = v; else region[pos] = v;
           ++pos;
         }
       }
-    };
-    // A reservation inside the LDS list (all but the rarest) stores with no per-element test
-    // of where the entry goes.
-    if (at + total <= (uint32_t)kPoolListCap) {
-      append([&](uint32_t q, uint64_t v) { sm.u.list[q] = v; });
-    } else {
-      append([&](uint32_t q, uint64_t v) {
-        if (q < (uint32_t)kPoolListCap) sm.u.list[q] = v; else region[q] = v;
-      });
     }
   };
   if (a < nchunks) step(a, x);  // chunk b is already in flight
