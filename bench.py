@@ -429,6 +429,9 @@ def timeline(args) -> int:
             "unit": "us", "rows": w.rows, "vocab": w.vocab, "shader_clock_mhz": round(rate, 1),
             "phases": phases,
             "candidates_per_row": {p: int(v) for p, v in pct(tl[:, 31]).items()},
+            # Rows whose guessed first bound left fewer than k candidates (taken again at the
+            # certain bound).
+            "rows_taken_again": int(np.count_nonzero(tl[:, 29] == 1)),
             "key_passes_per_row": {p: int(v) for p, v in pct(tl[:, 26]).items()},
             "stream_end_by_wave": [round(float(x), 2) for x in waves.mean(0)],
             # The two workgroups on each CU (slot 30: XCC and CU): the earlier and the later

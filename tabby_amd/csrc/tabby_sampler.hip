@@ -60,7 +60,8 @@
 // time). pool_row_kernel (pools above 256) uses slots 0-15, 16/24, 22 and 21/25 the same way,
 // 17 for the barrier after the stream, 23 for the selection's key passes done, 18 for the
 // selection done, 19 for the pool gathered, 20 for the pool sorted, and records its candidate
-// count in slot 31, its key passes in slot 26 and where it ran in slot 30 (TABBY_RECORD).
+// count in slot 31, its key passes in slot 26, where it ran in slot 30 and whether it took
+// its candidates again at the floor of its first bound in slot 29 (TABBY_RECORD).
 #ifdef TABBY_TIMELINE
 namespace tabby {
 constexpr int kTimelineSlots = 32;
@@ -3707,6 +3708,18 @@ constexpr int kPoolWaves = 16;
 constexpr int kPoolThreads = kPoolWaves * kWaveSize;
 constexpr int kPoolListCap = 8192;
 constexpr int kPoolBoundKeys = 4 * kPoolThreads;
+// Rows of at least this many chunks (the sample then at most a quarter of the row) stream at a
+// guessed first bound (pool_row_kernel).
+constexpr int kPoolGuessChunks = 128;
+static_assert((kPoolWaves & (kPoolWaves - 1)) == 0, "pool_row_kernel's claim order takes v mod kPoolWaves by a mask");
+
+// The spacing of pool_row_kernel's sample chunks: the largest power of two s with
+// kPoolWaves * s <= nchunks (1 for rows of fewer than 2 * kPoolWaves chunks).
+__device__ __forceinline__ int pool_sample_stride(int nchunks) {
+  int s = 1;
+  while (2 * s * kPoolWaves <= nchunks) s *= 2;
+  return s;
+}
 
 constexpr int kPoolHistPad = kBins + kBins / 32;  // one pad word per 32 bins (pool_pass)
 
@@ -3840,13 +3853,13 @@ __device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Batches &batches, Bin
 // The composite T with exactly `need` entries >= T (1 <= need <= entries), given that every
 // entry's key lies in [lo, hi]: key passes over the live key range, 2,048 bins each, until one
 // key remains (a quantized row resolves in one), then the ~index digits of that key's
-// entries (bits 20..10, 9..0; bits 31..21 of ~index are ones below 2^21 indices). A pass
-// that leaves its bin exactly taken ends early.
+// entries, from bit index_bits - 1 down (every index is below 2^index_bits, so the ~index
+// bits above are ones). A pass that leaves its bin exactly taken ends early.
 // The rest of pool_select from a key range [lo, hi] that holds the `need`-th entry: narrower
 // key passes until one key remains, then that key's ties by their indices' digits.
 template <class Batches>
 __device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Batches &batches, uint32_t need, uint32_t lo,
-                                                     uint32_t hi, int key_passes) {
+                                                     uint32_t hi, int key_passes, int index_bits) {
   while (lo != hi) {
     ++key_passes;
     const uint32_t range = hi - lo;
@@ -3875,12 +3888,15 @@ __device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Batches &batc
     TABBY_RECORD(26, key_passes);
     TABBY_STAMP(23);
   }
-  uint64_t prefix = ((uint64_t)lo << 32) | 0xffe00000ull;
-  int done = 21;
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int sh = p == 0 ? 10 : 0;
-    const uint32_t mask = p == 0 ? 0x7ffu : 0x3ffu;
+  // The index digits from the top of the row's index width (11 bits, then the rest): above it
+  // every ~index bit is one. (At vocab 151,936 the first pass bins 128 indices each, so the few
+  // hundred entries of a tied key rarely share the chosen bin and one pass usually ends it.)
+  int done = index_bits;
+  uint64_t prefix = ((uint64_t)lo << 32) | (uint64_t)(done >= 32 ? 0u : ~0u << done);
+  while (done > 0) {
+    const int width = min(done, 11);
+    const int sh = done - width;
+    const uint32_t mask = (1u << width) - 1u;
     const uint64_t want = prefix >> done;
     const int d = done;
     const PoolBin r = pool_pass(sm, batches, [&](uint64_t v) {
@@ -3901,12 +3917,13 @@ __device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Batches &batc
 // until one key remains -- a quantized row resolves in one), then over the tied key's index
 // digits. After the first pass only the chosen bin's entries matter: they are copied behind
 // the candidates (B entries at list[C ..), when C + B fits the LDS list) and `batches` is moved
-// onto them, so the later passes visit those B alone instead of all C (config 5: ~6,300
+// onto them, so the later passes visit those B alone instead of all C (config 5: ~2,800
 // candidates, a tied bin of a few hundred; the later passes had re-read every candidate).
+// Indices are below 2^index_bits.
 template <class Batches>
 __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Batches &batches, uint32_t need, uint32_t lo, uint32_t hi,
-                                                uint32_t C, uint32_t &sel_begin, uint32_t &sel_end) {
-  if (lo == hi) return pool_select_from(sm, batches, need, lo, hi, 0);
+                                                uint32_t C, uint32_t &sel_begin, uint32_t &sel_end, int index_bits) {
+  if (lo == hi) return pool_select_from(sm, batches, need, lo, hi, 0, index_bits);
   const uint32_t range = hi - lo;
   const int bits = 32 - __builtin_clz(range);
   const int shift = bits > 11 ? bits - 11 : 0;
@@ -3924,7 +3941,8 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Batches &batches, 
     }
     return (uint64_t)bin_low << 32;
   }
-  if (shift == 0 || C + r.count > (uint32_t)kPoolListCap) return pool_select_from(sm, batches, need, bin_low, bin_top, 1);
+  if (shift == 0 || C + r.count > (uint32_t)kPoolListCap)
+    return pool_select_from(sm, batches, need, bin_low, bin_top, 1, index_bits);
   // The chosen bin's entries, copied to list[C, C + B), and their smallest and largest key
   // (the later passes bin [smallest, largest]; one key -- a tie -- goes straight to the index
   // digits).
@@ -3965,7 +3983,7 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Batches &batches, 
   sel_end = C + sm.bs.slot2;  // the bin's r.count entries
   const uint32_t lo2 = sm.bs.u[0], hi2 = sm.bs.u[1];
   __syncthreads();  // sm.bs is reused
-  return pool_select_from(sm, batches, need, lo2, hi2, 1);
+  return pool_select_from(sm, batches, need, lo2, hi2, 1, index_bits);
 }
 
 // Two workgroups per CU (74 KB of LDS and at most 64 VGPRs each): 512 rows run in one round,
@@ -3976,7 +3994,7 @@ template <typename In, int VEC>
 __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Workspace W) {
   __shared__ PoolSmem sm;
   const int row = (int)blockIdx.x;
-  const int w = wave_id(), lane = wave_lane();
+  const int w = __builtin_amdgcn_readfirstlane(wave_id()), lane = wave_lane();  // w: scalar
   const tabby_row_params P = L.params[row];
   const int n = L.vocab;
   const int nchunks = (n + kWChunk - 1) / kWChunk;
@@ -3993,8 +4011,16 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     TABBY_RECORD(30, ((__builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xfu) << 16) |
                          ((__builtin_amdgcn_s_getreg((31 << 11) | 4) >> 8) & 0xffu));
   }
+  // Claim order: claim v takes chunk (v mod 16) s + v / 16 while v < 16 s (s the largest power
+  // of two with 16 s <= the row's chunks), then chunk v. Claims w and 16 + w, wave w's first
+  // two chunks (s w and s w + 1 when s >= 2), are the first bound's sample, spread over the row
+  // so that it stands for the whole row; each chunk is still 4 KB of consecutive elements.
+  const int s_log = __builtin_ctz(pool_sample_stride(nchunks));
+  auto chunk_of = [&](int v) {
+    return v < (kPoolWaves << s_log) ? ((v & (kPoolWaves - 1)) << s_log) + v / kPoolWaves : v;
+  };
   if (threadIdx.x == 0) {
-    sm.next_chunk = kPoolWaves;
+    sm.next_chunk = 2 * kPoolWaves;
     sm.count = 0u;
   }
   __syncthreads();
@@ -4003,7 +4029,7 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
   auto claim = [&]() {
     int c = 0;
     if (lane == 0) c = atomicAdd(&sm.next_chunk, 1);
-    return __builtin_amdgcn_readfirstlane(c);
+    return chunk_of(__builtin_amdgcn_readfirstlane(c));
   };
   // Elements past the row's end (or a chunk past its last) become -inf for the statistics.
   auto mask_tail = [&](int c, float(&v)[kWChunkPerLane]) {
@@ -4014,14 +4040,16 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     }
   };
   float x[kWChunkPerLane], y[kWChunkPerLane];
-  const int a = w;
+  const int a = chunk_of(w);
+  int b = chunk_of(kPoolWaves + w);
   load(a, x);
-  int b = claim();
   load(b, y);
   mask_tail(a, x);
   mask_tail(b, y);
-  float theta = -INFINITY;
-  if (kk > 0 && kk < n) {
+  // A bound from the sample: the top 22 key bits of the need-th largest of its 4,096 group
+  // maxima (four elements of a lane's first chunk and the same four of its second), so that
+  // `need` distinct elements of the row lie at or above it.
+  auto sample_bound = [&](uint32_t need) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float gm = -INFINITY;
@@ -4033,36 +4061,27 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     auto keys = [&](auto &&f) {
       for (int i = threadIdx.x; i < kPoolBoundKeys; i += kPoolThreads) f((uint64_t)sm.u.keys[i] << 32);
     };
-    theta = theta_of(radix_select(keys, (uint32_t)kk, sm.hist, sm.bs, 2).prefix);
+    const float t = theta_of(radix_select(keys, need, sm.hist, sm.bs, 2).prefix);
     __syncthreads();  // the keys are read before the list overwrites them
+    return t;
+  };
+  // The first bound. At kk the bound is certain to leave kk candidates, but the sample is a
+  // fifth of a 151,936 row, so it leaves ~6 kk there; rows of at least kPoolGuessChunks
+  // chunks (a sample of at most a quarter) stream at the (kk/2)-th largest group maximum
+  // instead -- ~2.5 kk candidates when the sample stands for the row -- and take their
+  // candidates again at the certain bound if the guess leaves fewer than kk.
+  const bool guess = kk > 1 && kk < n && nchunks >= kPoolGuessChunks;
+  float theta = -INFINITY;
+  if (kk > 0 && kk < n) {
+    theta = sample_bound(guess ? (uint32_t)kk / 2u : (uint32_t)kk);
     if (w == 0) TABBY_STAMP(22);
   }
 
   float lane_max = -INFINITY;
   float lane_ml = 0.0f;   // the reference of lane_sum's terms (as in wave_slice)
   double lane_sum = 0.0;
-  auto step = [&](int c, float(&cur)[kWChunkPerLane]) __attribute__((always_inline)) {
-    mask_tail(c, cur);
-    float cm = cur[0];
-#pragma unroll
-    for (int e = 1; e < kWChunkPerLane; ++e) cm = fmaxf(cm, cur[e]);
-    const float nm = fmaxf(lane_max, cm);
-    if (nm != -INFINITY) {
-      const float ml = nm * kLog2e;
-      float t[kWChunkPerLane];
-#pragma unroll
-      for (int e = 0; e < kWChunkPerLane; ++e) t[e] = __builtin_amdgcn_exp2f(fmaf(cur[e], kLog2e, -ml));
-#pragma unroll
-      for (int h = kWChunkPerLane / 2; h > 0; h >>= 1) {
-#pragma unroll
-        for (int e = 0; e < h; ++e) t[e] += t[e + h];
-      }
-      const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f(lane_ml - ml);
-      lane_sum = lane_sum * rescale + (double)t[0];
-      lane_max = nm;
-      lane_ml = ml;
-    }
-    if (kk == 0 || !__ballot(cm >= theta)) return;
+  // Appends chunk c's elements at or above theta to the list.
+  auto append = [&](int c, float(&cur)[kWChunkPerLane]) __attribute__((always_inline)) {
     // Past the row's end the elements become NaN, which fails x >= theta for every theta
     // (-inf included), so that one compare decides each element below.
     if (c >= full_chunks) {
@@ -4104,6 +4123,30 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       }
     }
   };
+  auto step = [&](int c, float(&cur)[kWChunkPerLane]) __attribute__((always_inline)) {
+    mask_tail(c, cur);
+    float cm = cur[0];
+#pragma unroll
+    for (int e = 1; e < kWChunkPerLane; ++e) cm = fmaxf(cm, cur[e]);
+    const float nm = fmaxf(lane_max, cm);
+    if (nm != -INFINITY) {
+      const float ml = nm * kLog2e;
+      float t[kWChunkPerLane];
+#pragma unroll
+      for (int e = 0; e < kWChunkPerLane; ++e) t[e] = __builtin_amdgcn_exp2f(fmaf(cur[e], kLog2e, -ml));
+#pragma unroll
+      for (int h = kWChunkPerLane / 2; h > 0; h >>= 1) {
+#pragma unroll
+        for (int e = 0; e < h; ++e) t[e] += t[e + h];
+      }
+      const double rescale = lane_max == -INFINITY ? 0.0 : (double)__builtin_amdgcn_exp2f(lane_ml - ml);
+      lane_sum = lane_sum * rescale + (double)t[0];
+      lane_max = nm;
+      lane_ml = ml;
+    }
+    if (kk == 0 || !__ballot(cm >= theta)) return;
+    append(c, cur);
+  };
   if (a < nchunks) step(a, x);  // chunk b is already in flight
   while (b < nchunks) {
     const int c = claim();
@@ -4125,20 +4168,54 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     sm.stats[w] = st;
   }
   __syncthreads();
+  uint32_t C = sm.count;
+  // A guessed bound that left fewer than kk candidates (a sample unlike the rest of its row):
+  // the certain bound from the sample, read again, and the row's candidates at it, an
+  // element per lane and step (a rare path, kept apart from the stream's code).
+  const bool rescan = guess && C < (uint32_t)kk;
+  if (rescan) {
+    __syncthreads();  // every wave has read the count (the sample's keys overwrite the list)
+    load(chunk_of(w), x);
+    load(chunk_of(kPoolWaves + w), y);
+    mask_tail(chunk_of(w), x);
+    mask_tail(chunk_of(kPoolWaves + w), y);
+    theta = sample_bound((uint32_t)kk);
+    if (threadIdx.x == 0) sm.count = 0u;
+    __syncthreads();
+    for (int base = 0; base < n; base += kPoolThreads) {
+      const int i = base + (int)threadIdx.x;
+      const float v = i < n ? load_one(src + i) : __builtin_nanf("");
+      const bool take = v >= theta;
+      const uint64_t m = __ballot(take);
+      if (m) {
+        uint32_t at = 0u;
+        if (lane == 0) at = atomicAdd(&sm.count, (uint32_t)__popcll(m));
+        at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
+        if (take) {
+          const uint32_t pos = at + (uint32_t)lanes_below(m);
+          const uint64_t e = composite(key_of(v), (uint32_t)i);
+          if (pos < (uint32_t)kPoolListCap) sm.u.list[pos] = e; else region[pos] = e;
+        }
+      }
+    }
+    __syncthreads();
+    C = sm.count;
+  }
   // The row's exact top kk of the candidates, unsorted: to `sorted` in LDS for a row this
   // workgroup samples itself (valid parameters, a pool of at most kcap, finite statistics:
   // every row that merge_kernel would sample from the pool), else to region[0 .. kept) for
   // merge_kernel (statuses and whole-vocabulary rows).
-  const uint32_t C = sm.count;
   if (w == 0) {
     TABBY_STAMP(17);
     TABBY_RECORD(31, C);
+    TABBY_RECORD(29, rescan ? 1 : 0);
   }
   const RowStats rs = row_stats(sm.stats, kPoolWaves);
   // The row's outcome, as merge_kernel decides it: a status (parameters outside the contract,
   // statistics outside the domain, a whole-vocabulary row with no head pass), a pool this
   // workgroup samples (`here`), or a whole-vocabulary row for merge_kernel and the head
-  // kernels. (C >= kk >= 1 for a pool in the domain: theta has kk elements at or above it.)
+  // kernels. (C >= kk >= 1 for a pool in the domain: theta has kk elements at or above it --
+  // the floor always, a guessed bound once the count above has shown it.)
   const bool in_domain = rs.max > -INFINITY && rs.max < INFINITY && rs.sum_exp > 0.0 && rs.sum_exp < INFINITY;
   const bool pool = keff <= L.kcap;
   int32_t status = TABBY_OK;
@@ -4167,7 +4244,8 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       }
     };
     // Every candidate's key lies between theta's and the row max's.
-    const uint64_t thr = pool_select(sm, batches, (uint32_t)kk, key_of(theta), key_of(rs.max), C, sel_begin, sel_end);
+    const uint64_t thr = pool_select(sm, batches, (uint32_t)kk, key_of(theta), key_of(rs.max), C, sel_begin, sel_end,
+                                     n > 1 ? 32 - __builtin_clz((unsigned)(n - 1)) : 1);
     sel_begin = 0u;  // the gather below visits every candidate
     sel_end = C;
     if (threadIdx.x == 0) sm.bs.slot = 0u;

@@ -153,6 +153,71 @@ def test_pool_row_kernel_batch_with_head_pass(oracle):
     _log("pool rows with a head pass", {"rows": sampled})
 
 
+def _f32_keys(x):
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return np.where(b >> 31 == 1, (~b) & 0xFFFFFFFF, b | 0x80000000)
+
+
+def _pool_guess_candidates(row, kk):
+    """The candidates pool_row_kernel's guessed first bound leaves in a row (f32, at least 128
+    chunks of 1,024): its sample is each wave's first two claims -- claim v takes chunk
+    (v mod 16) s + v // 16 below 16 s, s the largest power of two with 16 s <= chunks -- and the
+    bound is the top 22 key bits of the (kk/2)-th largest of the sample's 4,096 group maxima
+    (four elements of a lane's first chunk and the same four of its second)."""
+    n = row.size
+    nch = -(-n // 1024)
+    s = 1
+    while 32 * s <= nch:
+        s *= 2
+    chunk = lambda v: (v % 16) * s + v // 16 if v < 16 * s else v
+    gm = []
+    for w in range(16):
+        a, b = chunk(w), chunk(16 + w)
+        xa = row[a * 1024:(a + 1) * 1024].reshape(4, 64, 4)
+        xb = row[b * 1024:(b + 1) * 1024].reshape(4, 64, 4)
+        gm.append(np.maximum(xa.max(2), xb.max(2)).ravel())
+    keys = np.clip(_f32_keys(np.concatenate(gm)), 0x007FFFFF, 0xFF800000)
+    t = np.sort(keys)[::-1][kk // 2 - 1] & ~np.uint64(0x3FF)
+    return int(np.count_nonzero(_f32_keys(row) >= t))
+
+
+def test_pool_row_kernel_guessed_bound(oracle):
+    # Rows of 151,936 (149 chunks) take pool_row_kernel's guessed first bound: the (k/2)-th
+    # largest group maximum of a sample of 32 chunks spread over the row. Rows 0-3 put their
+    # largest values in exactly those chunks, so the guess leaves fewer than k candidates and
+    # the row's candidates are taken again at the certain bound (rows 0-2: the sampled chunks
+    # drawn around 10, the rest around 0; row 3: one value near 20 in every group of the
+    # sample, the rest around 0). Rows 4-5 are sorted ascending and descending, row 6 has a
+    # sample of -inf (no guess: every element is a candidate), row 7 a sample of one value;
+    # the other rows are config-5-like (ties, -inf) with k from 1 to 1,024.
+    V, rows = 151936, 256
+    w = synth.random_workload(rows=rows, vocab=V, seed=5150, ties=True, neg_inf_frac=0.3,
+                              k_choices=(1, 64, 300, 1024), temperatures=(0.7, 1.0), top_ps=(0.5, 0.98, 1.0),
+                              sigma=2.0)
+    rng = np.random.default_rng(5150)
+    sample = np.zeros(V, dtype=bool)
+    for v in range(32):
+        c = (v % 16) * 8 + v // 16
+        sample[c * 1024:(c + 1) * 1024] = True
+    for r, k in ((0, 1024), (1, 300), (2, 1000), (3, 1024), (4, 1024), (5, 1024), (6, 1024), (7, 1024)):
+        w.top_k[r] = k
+        w.logits[r] = rng.standard_normal(V).astype(np.float32)
+    for r in range(3):
+        w.logits[r, sample] += 10.0
+    big = np.zeros(V, dtype=bool)
+    big[np.flatnonzero(sample)[::8]] = True  # element 0 of every lane's four in chunk a or b
+    w.logits[3, big] = 20.0 + rng.random(int(big.sum())).astype(np.float32)
+    w.logits[4] = np.sort(w.logits[4])
+    w.logits[5] = np.sort(w.logits[5])[::-1]
+    w.logits[6, sample] = -np.inf
+    w.logits[7, sample] = 5.0
+    w.top_p[:4] = (0.98, 0.5, 0.98, 0.9)
+    for r in range(4):  # the premise: the guess leaves fewer than k candidates
+        assert _pool_guess_candidates(w.logits[r], int(w.top_k[r])) < int(w.top_k[r]), f"row {r}"
+    res, ids, vals = run_gpu(w, k_max=1024, topk_cap=64)
+    _log("pool kernel guessed bound", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
 def test_f16_input_finite_k(oracle):
     w = synth.config(4, rows=16)
     w.top_k[:] = np.array([1, 20, 50, 100] * 4, np.int32)
