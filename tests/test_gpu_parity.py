@@ -158,30 +158,36 @@ def _f32_keys(x):
     return np.where(b >> 31 == 1, (~b) & 0xFFFFFFFF, b | 0x80000000)
 
 
-def _pool_guess_candidates(row, kk):
-    """The candidates pool_row_kernel's guessed first bound leaves in a row (f32, at least 128
-    chunks of 1,024): its sample is each wave's first two claims -- claim v takes chunk
-    (v mod 16) s + v // 16 below 16 s, s the largest power of two with 16 s <= chunks -- and the
-    bound is the top 22 key bits of the (kk/2)-th largest of the sample's 4,096 group maxima
-    (four elements of a lane's first chunk and the same four of its second)."""
+def _pool_guess_candidates(row, kk, vec):
+    """The candidates pool_row_kernel's guessed first bound leaves in a row (at least 128 chunks
+    of 1,024; vec: elements per lane per load, 4 for f32 and 8 for f16): its sample is each
+    wave's first two claims -- claim v takes chunk (v mod 16) s + v // 16 below 16 s, s the
+    largest power of two with 16 s <= chunks -- and the bound is the top 22 key bits of the
+    (kk/2)-th largest of the sample's 4,096 group maxima (a lane's elements 4g .. 4g + 3 of its
+    first chunk and of its second; element e of lane l sits at (e // vec) 64 vec + l vec +
+    e % vec in its chunk)."""
+    row = row.astype(np.float32)
     n = row.size
     nch = -(-n // 1024)
     s = 1
     while 32 * s <= nch:
         s *= 2
     chunk = lambda v: (v % 16) * s + v // 16 if v < 16 * s else v
+    e = np.arange(16).reshape(4, 1, 4)
+    lanes = np.arange(64).reshape(1, 64, 1)
+    at = (e // vec) * 64 * vec + lanes * vec + e % vec  # [group, lane, element of the group]
     gm = []
     for w in range(16):
-        a, b = chunk(w), chunk(16 + w)
-        xa = row[a * 1024:(a + 1) * 1024].reshape(4, 64, 4)
-        xb = row[b * 1024:(b + 1) * 1024].reshape(4, 64, 4)
+        xa = row[chunk(w) * 1024 + at]
+        xb = row[chunk(16 + w) * 1024 + at]
         gm.append(np.maximum(xa.max(2), xb.max(2)).ravel())
     keys = np.clip(_f32_keys(np.concatenate(gm)), 0x007FFFFF, 0xFF800000)
     t = np.sort(keys)[::-1][kk // 2 - 1] & ~np.uint64(0x3FF)
     return int(np.count_nonzero(_f32_keys(row) >= t))
 
 
-def test_pool_row_kernel_guessed_bound(oracle):
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_pool_row_kernel_guessed_bound(oracle, dtype):
     # Rows of 151,936 (149 chunks) take pool_row_kernel's guessed first bound: the (k/2)-th
     # largest group maximum of a sample of 32 chunks spread over the row. Rows 0-3 put their
     # largest values in exactly those chunks, so the guess leaves fewer than k candidates and
@@ -189,8 +195,10 @@ def test_pool_row_kernel_guessed_bound(oracle):
     # drawn around 10, the rest around 0; row 3: one value near 20 in every group of the
     # sample, the rest around 0). Rows 4-5 are sorted ascending and descending, row 6 has a
     # sample of -inf (no guess: every element is a candidate), row 7 a sample of one value;
-    # the other rows are config-5-like (ties, -inf) with k from 1 to 1,024.
+    # the other rows are config-5-like (ties, -inf) with k from 1 to 1,024. f16 rows load
+    # eight elements per lane at a time, which changes the groups (and row 3's layout).
     V, rows = 151936, 256
+    vec = 4 if dtype == np.float32 else 8
     w = synth.random_workload(rows=rows, vocab=V, seed=5150, ties=True, neg_inf_frac=0.3,
                               k_choices=(1, 64, 300, 1024), temperatures=(0.7, 1.0), top_ps=(0.5, 0.98, 1.0),
                               sigma=2.0)
@@ -204,18 +212,24 @@ def test_pool_row_kernel_guessed_bound(oracle):
         w.logits[r] = rng.standard_normal(V).astype(np.float32)
     for r in range(3):
         w.logits[r, sample] += 10.0
+    # Row 3: element 0 of lane l's elements 4g .. 4g + 3, for even lanes, in every sampled chunk.
     big = np.zeros(V, dtype=bool)
-    big[np.flatnonzero(sample)[::8]] = True  # element 0 of every lane's four in chunk a or b
+    at = np.flatnonzero(sample)
+    off = at % 1024
+    big[at[(off % (2 * vec) == 0) if vec == 4 else (off % vec == 0) & ((off // vec) % 2 == 0)]] = True
     w.logits[3, big] = 20.0 + rng.random(int(big.sum())).astype(np.float32)
     w.logits[4] = np.sort(w.logits[4])
     w.logits[5] = np.sort(w.logits[5])[::-1]
     w.logits[6, sample] = -np.inf
     w.logits[7, sample] = 5.0
     w.top_p[:4] = (0.98, 0.5, 0.98, 0.9)
+    if dtype == np.float16:
+        w.logits = w.logits.astype(np.float16)
     for r in range(4):  # the premise: the guess leaves fewer than k candidates
-        assert _pool_guess_candidates(w.logits[r], int(w.top_k[r])) < int(w.top_k[r]), f"row {r}"
+        assert _pool_guess_candidates(w.logits[r], int(w.top_k[r]), vec) < int(w.top_k[r]), f"row {r}"
     res, ids, vals = run_gpu(w, k_max=1024, topk_cap=64)
-    _log("pool kernel guessed bound", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+    _log(f"pool kernel guessed bound {dtype.__name__}",
+         compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
 
 
 def test_f16_input_finite_k(oracle):
