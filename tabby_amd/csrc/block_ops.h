@@ -226,17 +226,47 @@ __device__ __forceinline__ void block_sort_desc(uint64_t *a, int n) {
   }
 }
 
-// In-place descending sort of a[0..n), n a power of two and at most NW * 64, by the whole
-// workgroup of NW waves, through tmp[0..n) in LDS: each wave sorts 64 entries in registers,
-// then log2(n / 64) merge rounds, each a barrier: an entry's place in the merged pair of runs
-// is its place in its own run plus the entries of the other run ahead of it, found by binary
-// search (an equal entry of the left run counts as ahead of the right run's, so that equal
-// entries -- the zero padding -- still take distinct places). Against the bitonic network
-// above that is one barrier per doubling instead of one per stride, and a dependent LDS read
-// per halving instead of a compare-exchange stage.
+// One merge round of block_merge_sort_desc: runs of L = 32 R sorted descending are merged in
+// pairs by wave w, which writes register r = w mod R (sorted places 64 r .. 64 r + 63) of pair
+// p = w / R. The pair's first run followed by its second reversed is a bitonic sequence X of
+// 2L; the bitonic merge's stages of stride 64 and above compare X[i] with X[i + stride] at the
+// same lane, and of each of them the wave keeps only the half its register falls in: the
+// maxima above, the minima below, one compare and select per pair, R - 1 in all. What is left
+// is the bitonic 64 of register r, sorted by the stages below 64 through lane exchanges. The
+// loads and the store are 64 consecutive entries each.
+template <int R>
+__device__ __forceinline__ void bitonic_merge_round(const uint64_t *src, uint64_t *dst, int w) {
+  constexpr int L = 32 * R;
+  const int lane = lane_id(), p = w / R, r = w - p * R;
+  const uint64_t *A = src + 2 * p * L, *B = A + L;
+  uint64_t v[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) v[q] = q < R / 2 ? A[64 * q + lane] : B[2 * L - 1 - 64 * q - lane];
+#pragma unroll
+  for (int half = R / 2; half >= 1; half >>= 1) {
+    const bool low = (r & half) != 0;  // the minima's half
+#pragma unroll
+    for (int k = 0; k < half; ++k) v[k] = cmpx(v[k], v[k + half], !low);
+  }
+#pragma unroll
+  for (int stride = 32; stride > 0; stride >>= 1) v[0] = cmpx(v[0], xor_lane_by(v[0], stride), (lane & stride) == 0);
+  dst[2 * p * L + 64 * r + lane] = v[0];
+}
+
+// In-place descending sort of a[0..n), n a power of two and at most NW * 64 <= 1,024, by the
+// whole workgroup of NW waves, through tmp[0..n) in LDS: each wave sorts 64 entries in
+// registers, then log2(n / 64) merge rounds, one barrier each. Up to runs of 256 a round is
+// bitonic_merge_round: each of the n / 64 waves computes 64 entries of the merged runs from 2,
+// 4 or 8 loads (0.9, 0.7 and 0.8 us of config 5's tail against 1.05, 0.97 and 1.08 for the
+// binary search below). The round of runs of 512 places each entry by binary search in the
+// other run -- an equal entry of the left run counts as ahead of the right run's, so that
+// equal entries, the zero padding among them, take distinct places -- which beat the bitonic
+// form's 16 loads and 15 selects per lane there (1.17 against 1.25 us).
 template <int NW>
 __device__ __forceinline__ void block_merge_sort_desc(uint64_t *a, uint64_t *tmp, int n) {
+  static_assert(NW <= 16, "n <= 1,024: the last round is the binary search's");
   const int t = (int)threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   if (n <= 64) {
     if (t < 64) {
       uint64_t v[1] = {lane < n ? a[lane] : 0ull};
@@ -254,17 +284,27 @@ __device__ __forceinline__ void block_merge_sort_desc(uint64_t *a, uint64_t *tmp
   __syncthreads();
   uint64_t *src = a, *dst = tmp;
   for (int len = 64; len < n; len <<= 1) {
-    if (t < n) {
-      const uint64_t x = src[t];
-      const int run = t / len, i = t - run * len;
-      const bool left = (run & 1) == 0;
-      const uint64_t *other = src + (run ^ 1) * len;
-      auto ahead = [&](uint64_t y) { return left ? y > x : y >= x; };
-      int pos = 0;  // entries of `other` ahead of x: a prefix of it
-      for (int step = len >> 1; step > 0; step >>= 1)
-        if (ahead(other[pos + step - 1])) pos += step;
-      pos += ahead(other[pos]) ? 1 : 0;  // only at pos == len - 1 can other[pos] be ahead
-      dst[(run & ~1) * len + i + pos] = x;
+    if (len == 512) {
+      // The last round by binary search: each entry's place in the other run (16 loads per
+      // lane and 15 selects made the bitonic form slower here).
+      if (t < n) {
+        const uint64_t x = src[t];
+        const int run = t / len, i = t - run * len;
+        const bool left = (run & 1) == 0;
+        const uint64_t *other = src + (run ^ 1) * len;
+        auto ahead = [&](uint64_t y) { return left ? y > x : y >= x; };
+        int pos = 0;  // entries of `other` ahead of x: a prefix of it
+        for (int step = len >> 1; step > 0; step >>= 1)
+          if (ahead(other[pos + step - 1])) pos += step;
+        pos += ahead(other[pos]) ? 1 : 0;  // only at pos == len - 1 can other[pos] be ahead
+        dst[(run & ~1) * len + i + pos] = x;
+      }
+    } else if (w < n / 64) {
+      switch (len) {
+        case 64: bitonic_merge_round<2>(src, dst, w); break;
+        case 128: bitonic_merge_round<4>(src, dst, w); break;
+        default: bitonic_merge_round<8>(src, dst, w); break;
+      }
     }
     __syncthreads();
     uint64_t *const s2 = src;
