@@ -267,13 +267,14 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
   if (greedy_temp(T)) return false;
   const int lane = lane_id(), wave = wave_id();
   double *run = sm.u.tail.w;  // running sums, by index
-  double c[PER], e_sum = 0.0, acc = 0.0;
+  double c[PER], ex[PER], e_sum = 0.0, acc = 0.0;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int i = (int)threadIdx.x * PER + j;
     const bool in = i < count;
     const double d = in ? (double)value_of(composite_key(sm.sorted[i])) - (double)max_logit : 0.0;
     const double e = in ? exp_nonpos(d) : 0.0;
+    ex[j] = e;  // the exact term: the probability if this entry is drawn
     e_sum += e;
     acc += !in ? 0.0 : T == 1.0 ? e : exp_nonpos(d / T);
     c[j] = acc;  // the thread's running sum of the scaled terms
@@ -349,8 +350,12 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
     __syncthreads();  // finish_row reuses the arrays
     return false;
   }
-  const uint64_t cv = sm.sorted[chosen];
-  if (threadIdx.x == 0) {
+  // The thread that holds the drawn entry writes the result with its own term.
+  if ((int)threadIdx.x == chosen / PER) {
+    double e = ex[0];
+#pragma unroll
+    for (int j = 1; j < PER; ++j)
+      if (j == chosen % PER) e = ex[j];
     tabby_row_result res;
     res.max_logit = max_logit;
     res.sum_exp = sum_exp;
@@ -359,8 +364,8 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
     res.topk_count = min(count, L.topk_cap);
     res.considered = (uint32_t)cut;
     res.pool_exhausted = (top_p < 1.0 && pool < top_p) ? 1 : 0;
-    res.id = (int32_t)composite_index(cv);
-    res.probability = exp_nonpos((double)value_of(composite_key(cv)) - (double)max_logit) / sum_exp;
+    res.id = (int32_t)composite_index(sm.sorted[chosen]);
+    res.probability = e / sum_exp;
     L.results[row] = res;
   }
   if (L.topk_cap > 0) {
