@@ -186,8 +186,8 @@ def _pool_guess_candidates(row, kk, vec):
     return int(np.count_nonzero(_f32_keys(row) >= t))
 
 
-@pytest.mark.parametrize("dtype", [np.float32, np.float16])
-def test_pool_row_kernel_guessed_bound(oracle, dtype):
+@pytest.mark.parametrize("dtype,V", [(np.float32, 151936), (np.float16, 151936), (np.float32, 151937)])
+def test_pool_row_kernel_guessed_bound(oracle, dtype, V):
     # Rows of 151,936 (149 chunks) take pool_row_kernel's guessed first bound: the (k/2)-th
     # largest group maximum of a sample of 32 chunks spread over the row. Rows 0-3 put their
     # largest values in exactly those chunks, so the guess leaves fewer than k candidates and
@@ -196,9 +196,10 @@ def test_pool_row_kernel_guessed_bound(oracle, dtype):
     # sample, the rest around 0). Rows 4-5 are sorted ascending and descending, row 6 has a
     # sample of -inf (no guess: every element is a candidate), row 7 a sample of one value;
     # the other rows are config-5-like (ties, -inf) with k from 1 to 1,024. f16 rows load
-    # eight elements per lane at a time, which changes the groups (and row 3's layout).
-    V, rows = 151936, 256
-    vec = 4 if dtype == np.float32 else 8
+    # eight elements per lane at a time and an odd vocabulary one, which changes the groups
+    # (and row 3's layout).
+    rows = 256
+    vec = 1 if V % 8 else 4 if dtype == np.float32 else 8
     w = synth.random_workload(rows=rows, vocab=V, seed=5150, ties=True, neg_inf_frac=0.3,
                               k_choices=(1, 64, 300, 1024), temperatures=(0.7, 1.0), top_ps=(0.5, 0.98, 1.0),
                               sigma=2.0)
@@ -212,11 +213,13 @@ def test_pool_row_kernel_guessed_bound(oracle, dtype):
         w.logits[r] = rng.standard_normal(V).astype(np.float32)
     for r in range(3):
         w.logits[r, sample] += 10.0
-    # Row 3: element 0 of lane l's elements 4g .. 4g + 3, for even lanes, in every sampled chunk.
+    # Row 3: the first of lane l's elements 4g .. 4g + 3, for even lanes, in every sampled chunk
+    # (element e of lane l sits at (e // vec) 64 vec + l vec + e % vec in its chunk).
     big = np.zeros(V, dtype=bool)
-    at = np.flatnonzero(sample)
-    off = at % 1024
-    big[at[(off % (2 * vec) == 0) if vec == 4 else (off % vec == 0) & ((off // vec) % 2 == 0)]] = True
+    e, lane = np.meshgrid(np.arange(0, 16, 4), np.arange(0, 64, 2))
+    first = ((e // vec) * 64 * vec + lane * vec + e % vec).ravel()
+    for v in range(32):
+        big[((v % 16) * 8 + v // 16) * 1024 + first] = True
     w.logits[3, big] = 20.0 + rng.random(int(big.sum())).astype(np.float32)
     w.logits[4] = np.sort(w.logits[4])
     w.logits[5] = np.sort(w.logits[5])[::-1]
