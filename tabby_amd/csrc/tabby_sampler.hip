@@ -3800,11 +3800,16 @@ __device__ __forceinline__ void wave_slots(const bool (&take)[B], uint32_t *slot
   }
 }
 
-template <class Batches, class BinOf>
-__device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Batches &batches, BinOf bin_of, uint32_t need) {
+// Zeroes the pool histogram (no barrier).
+__device__ __forceinline__ void pool_hist_clear(PoolSmem &sm) {
   static_assert(kPoolHistPad % 4 == 0 && kPoolHistPad <= 4 * kPoolThreads, "one 16-byte store per thread");
   if ((int)threadIdx.x < kPoolHistPad / 4) reinterpret_cast<u32x4 *>(sm.hist)[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
-  __syncthreads();
+}
+
+// The histogram is zero on entry (cleared after the first bound's select) and again on return:
+// wave 0 zeroes the bins as it searches them, so a pass takes two barriers.
+template <class Batches, class BinOf>
+__device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Batches &batches, BinOf bin_of, uint32_t need) {
   each_of(batches, [&](uint64_t v) {
     const int b = bin_of(v);
     // Lanes whose entries all fall in one bin (a tied key's entries do) add their count
@@ -3829,7 +3834,7 @@ __device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Batches &batches, Bin
     const int lane = wave_lane();
     uint32_t sum = 0u;
     static_assert(PER == 32, "pool_hist_at pads one word per 32 bins: a lane's bins are lane * 33 + q");
-    const uint32_t *mine = sm.hist + lane * (PER + 1);
+    uint32_t *mine = sm.hist + lane * (PER + 1);
 #pragma unroll 8
     for (int q = 0; q < PER; ++q) sum += mine[q];
     const uint32_t inc = wave_inclusive_scan_u32(sum);
@@ -3839,6 +3844,9 @@ __device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Batches &batches, Bin
     const int owner = got ? __ffsll((unsigned long long)got) - 1 : kWaveSize - 1;
     const uint32_t before = (uint32_t)__builtin_amdgcn_readlane((int)(inc - sum), owner);
     const uint32_t c = lane < PER ? sm.hist[owner * (PER + 1) + lane] : 0u;
+    // Zero for the next pass (after the reads above: a wave's LDS operations complete in order).
+#pragma unroll 8
+    for (int q = 0; q < PER; ++q) mine[q] = 0u;
     const uint32_t cum = before + wave_inclusive_scan_u32(c);
     // The owner's last bin holds it if none before does.
     const uint64_t reach = __ballot(lane < PER - 1 && cum >= need);
@@ -3850,9 +3858,9 @@ __device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Batches &batches, Bin
     }
   }
   __syncthreads();
-  const PoolBin r{sm.bs.bin, sm.bs.above, sm.bs.count};
-  __syncthreads();  // sm.bs and sm.hist are reused
-  return r;
+  // (No barrier after the read: the next pass's search writes sm.bs only after its visit's
+  // barrier, and the histogram is already zero.)
+  return PoolBin{sm.bs.bin, sm.bs.above, sm.bs.count};
 }
 
 // The composite T with exactly `need` entries >= T (1 <= need <= entries), given that every
@@ -4054,6 +4062,7 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
   // A bound from the sample: the top 22 key bits of the need-th largest of its 4,096 group
   // maxima (four elements of a lane's first chunk and the same four of its second), so that
   // `need` distinct elements of the row lie at or above it.
+  // The select leaves the histogram zeroed for the selection's passes (pool_pass).
   auto sample_bound = [&](uint32_t need) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -4067,6 +4076,7 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       for (int i = threadIdx.x; i < kPoolBoundKeys; i += kPoolThreads) f((uint64_t)sm.u.keys[i] << 32);
     };
     const float t = theta_of(radix_select(keys, need, sm.hist, sm.bs, 2).prefix);
+    pool_hist_clear(sm);
     __syncthreads();  // the keys are read before the list overwrites them
     return t;
   };
