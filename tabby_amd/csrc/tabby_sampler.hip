@@ -3933,6 +3933,8 @@ __device__ __forceinline__ uint64_t pool_select_from(PoolSmem &sm, Batches &batc
 // onto them, so the later passes visit those B alone instead of all C (config 5: ~2,800
 // candidates, a tied bin of a few hundred; the later passes had re-read every candidate).
 // Indices are below 2^index_bits.
+// The caller has set sm.bs.slot2 = 0, sm.bs.u[0] = ~0 and sm.bs.u[1] = 0 (the compaction's
+// counters) before the call; the passes' barriers publish them.
 template <class Batches>
 __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Batches &batches, uint32_t need, uint32_t lo, uint32_t hi,
                                                 uint32_t C, uint32_t &sel_begin, uint32_t &sel_end, int index_bits) {
@@ -3958,13 +3960,7 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Batches &batches, 
     return pool_select_from(sm, batches, need, bin_low, bin_top, 1, index_bits);
   // The chosen bin's entries, copied to list[C, C + B), and their smallest and largest key
   // (the later passes bin [smallest, largest]; one key -- a tie -- goes straight to the index
-  // digits).
-  if (threadIdx.x == 0) {
-    sm.bs.slot2 = 0u;
-    sm.bs.u[0] = ~0u;
-    sm.bs.u[1] = 0u;
-  }
-  __syncthreads();
+  // digits). Their counters were set before the first pass.
   uint32_t kmin = ~0u, kmax = 0u;
   batches([&](const uint64_t (&v)[kPoolBatch], const bool (&ok)[kPoolBatch]) {
     bool in[kPoolBatch];
@@ -3994,8 +3990,7 @@ __device__ __forceinline__ uint64_t pool_select(PoolSmem &sm, Batches &batches, 
   __syncthreads();
   sel_begin = C;
   sel_end = C + sm.bs.slot2;  // the bin's r.count entries
-  const uint32_t lo2 = sm.bs.u[0], hi2 = sm.bs.u[1];
-  __syncthreads();  // sm.bs is reused
+  const uint32_t lo2 = sm.bs.u[0], hi2 = sm.bs.u[1];  // (nothing writes them again)
   return pool_select_from(sm, batches, need, lo2, hi2, 1, index_bits);
 }
 
@@ -4259,12 +4254,19 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
       }
     };
     // Every candidate's key lies between theta's and the row max's.
+    // The compaction's and the gather's slot counters, published by the passes' barriers.
+    if (threadIdx.x == 0) {
+      sm.bs.slot = 0u;
+      sm.bs.slot2 = 0u;
+      sm.bs.u[0] = ~0u;
+      sm.bs.u[1] = 0u;
+    }
     const uint64_t thr = pool_select(sm, batches, (uint32_t)kk, key_of(theta), key_of(rs.max), C, sel_begin, sel_end,
                                      n > 1 ? 32 - __builtin_clz((unsigned)(n - 1)) : 1);
     sel_begin = 0u;  // the gather below visits every candidate
     sel_end = C;
-    if (threadIdx.x == 0) sm.bs.slot = 0u;
-    __syncthreads();  // (also: the selection's last histogram reads are done, `sorted` is free)
+    // (No barrier: the last pass's search, which read the histogram that `sorted` overlays,
+    // ended with one.)
     // region[0 .. kk) lies below the overflow entries (kk <= 1,024 < kPoolListCap).
     if (w == 0) TABBY_STAMP(18);
     batches([&](const uint64_t (&v)[kPoolBatch], const bool (&ok)[kPoolBatch]) {
