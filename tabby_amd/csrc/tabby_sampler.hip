@@ -3694,14 +3694,16 @@ __global__ void exp_kernel(const double *x, double *y, int64_t n) {
 
 // ---------------------------------------------------------------------------------------
 // Pools of 257..1024 (k_max > 256) in batches of at least as many rows as CUs: one 16-wave
-// workgroup per row streams it as row_kernel does (each wave's first chunk, then chunks
+// workgroup per row streams it as row_kernel does (each wave's first two chunks, then chunks
 // claimed from an LDS counter) with the lane max and sum-exp, and appends every element at
 // or above the row's first bound to one LDS list shared by its waves: a wave reserves room
 // for a chunk's candidates with one LDS atomic, with no barrier, and past kPoolListCap
 // entries they go to the row's region of global memory. The first bound: the maxima of four
-// groups of eight elements of each lane's first two chunks are 4,096 distinct elements; the
-// kk-th largest of their keys (its top 22 bits: a lower bound) has kk elements at or above
-// it, so it never exceeds the row's kk-th largest. (The 4-wave slice kernel started from
+// groups of eight elements of each lane's first two chunks (spread over the row) are 4,096
+// distinct elements; the kk-th largest of their keys (its top 22 bits: a lower bound) has kk
+// elements at or above it, so it never exceeds the row's kk-th largest -- and long rows
+// stream at the (kk/2)-th instead, checked at the end (the rows whose count falls short take
+// their candidates again at the certain bound). (The 4-wave slice kernel started from
 // the first chunk's kk-th largest -- a quarter of that chunk at kk = 1,024 -- and pruned its
 // list with two workgroup barriers per chunk: config 5 took 135 us there.) At the end the
 // workgroup selects the row's exact top kk from the list (pool_select), gathers it into LDS,
