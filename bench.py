@@ -43,6 +43,11 @@ def parse_args():
     ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5], default=None,
                     help="run BASELINE.json's configs[N-1] exactly as generated (parameters, "
                          "dtype and shape) instead of the headline; a secondary measurement")
+    ap.add_argument("--guess-fails", action="store_true",
+                    help="with --config 5: raise every row's finite logits in the chunks its "
+                         "first bound samples by 20, so that pool_row_kernel's guessed bound "
+                         "leaves too few candidates on every row and each row is taken again at "
+                         "the certain bound; a diagnostic of that path's cost")
     ap.add_argument("--host-params", action="store_true",
                     help="time the host-parameter entry (tabby_sampler_sample: parameters uploaded "
                          "and results read back every call, synchronously) instead of the "
@@ -506,6 +511,22 @@ def main() -> int:
     # host once; params per row from config 3, with k/p overridden to the headline's.
     if args.config is not None:
         w = synth.config(args.config)
+        if args.guess_fails:
+            if args.config != 5:
+                print("bench: --guess-fails applies to --config 5", file=sys.stderr)
+                return 2
+            # The sample: claims v < 32 take chunk (v mod 16) s + v // 16, s the largest power of
+            # two with 16 s <= the row's chunks (pool_row_kernel's claim order).
+            nch = -(-w.vocab // 1024)
+            s = 1
+            while 32 * s <= nch:
+                s *= 2
+            sampled = np.zeros(w.vocab, dtype=bool)
+            for v in range(32):
+                c = (v % 16) * s + v // 16
+                sampled[c * 1024:(c + 1) * 1024] = True
+            block = w.logits[:, sampled]
+            w.logits[:, sampled] = np.where(np.isfinite(block), block + 20.0, block)
     else:
         w = synth.config(3, rows=args.rows, vocab=args.vocab)
         if not args.mixed_params:
@@ -626,7 +647,8 @@ def main() -> int:
         metric = (f"sampled rows/sec + achieved HBM GB/s, BASELINE configs[{args.config - 1}] "
                   f"({w.rows}x{w.vocab} {dtype_name})")
         ks = sorted(set(int(k) for k in w.top_k))
-        config = {"workload": f"config{args.config}", "rows": w.rows, "vocab": w.vocab,
+        config = {"workload": f"config{args.config}" + ("-guess-fails" if args.guess_fails else ""),
+                  "rows": w.rows, "vocab": w.vocab,
                   "top_k": ks if len(ks) > 1 else ks[0],
                   "top_p": sorted(set(float(p) for p in w.top_p)),
                   "temperature": sorted(set(float(t) for t in w.temperature)),

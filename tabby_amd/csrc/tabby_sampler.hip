@@ -61,7 +61,7 @@
 // 17 for the barrier after the stream, 23 for the selection's key passes done, 18 for the
 // selection done, 19 for the pool gathered, 20 for the pool sorted, and records its candidate
 // count in slot 31, its key passes in slot 26, where it ran in slot 30 and whether it took
-// its candidates again at the floor of its first bound in slot 29 (TABBY_RECORD).
+// its candidates again at the certain first bound in slot 29 (TABBY_RECORD).
 #ifdef TABBY_TIMELINE
 namespace tabby {
 constexpr int kTimelineSlots = 32;
@@ -4194,19 +4194,27 @@ __global__ __launch_bounds__(kPoolThreads, 8) void pool_row_kernel(Launch L, Wor
     theta = sample_bound((uint32_t)kk);
     if (threadIdx.x == 0) sm.count = 0u;
     __syncthreads();
-    for (int base = 0; base < n; base += kPoolThreads) {
-      const int i = base + (int)threadIdx.x;
-      const float v = i < n ? load_one(src + i) : __builtin_nanf("");
-      const bool take = v >= theta;
-      const uint64_t m = __ballot(take);
-      if (m) {
-        uint32_t at = 0u;
-        if (lane == 0) at = atomicAdd(&sm.count, (uint32_t)__popcll(m));
-        at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
-        if (take) {
-          const uint32_t pos = at + (uint32_t)lanes_below(m);
-          const uint64_t e = composite(key_of(v), (uint32_t)i);
-          if (pos < (uint32_t)kPoolListCap) sm.u.list[pos] = e; else region[pos] = e;
+    constexpr int kAhead = 8;  // loads in flight per lane
+    for (int base = 0; base < n; base += kAhead * kPoolThreads) {
+      float v[kAhead];
+#pragma unroll
+      for (int u = 0; u < kAhead; ++u) {
+        const int i = base + u * kPoolThreads + (int)threadIdx.x;
+        v[u] = i < n ? load_one(src + i) : __builtin_nanf("");
+      }
+#pragma unroll
+      for (int u = 0; u < kAhead; ++u) {
+        const bool take = v[u] >= theta;
+        const uint64_t m = __ballot(take);
+        if (m) {
+          uint32_t at = 0u;
+          if (lane == 0) at = atomicAdd(&sm.count, (uint32_t)__popcll(m));
+          at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
+          if (take) {
+            const uint32_t pos = at + (uint32_t)lanes_below(m);
+            const uint64_t e = composite(key_of(v[u]), (uint32_t)(base + u * kPoolThreads + (int)threadIdx.x));
+            if (pos < (uint32_t)kPoolListCap) sm.u.list[pos] = e; else region[pos] = e;
+          }
         }
       }
     }
