@@ -235,6 +235,25 @@ def test_pool_row_kernel_guessed_bound(oracle, dtype, V):
          compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
 
 
+def test_pool_row_kernel_guessed_bound_k_sweep(oracle):
+    # 256 rows of 131,072 (exactly the 128 chunks from which pool_row_kernel guesses its first
+    # bound), k from 2 to 1,024 in steps of 4 with ties and -inf; every fourth row has its
+    # sampled chunks raised by 3, so that some guesses fall short (those rows are taken again)
+    # and others only just hold.
+    V, rows = 131072, 256
+    w = synth.random_workload(rows=rows, vocab=V, seed=7331, ties=True, neg_inf_frac=0.2,
+                              k_choices=tuple(range(2, 1025, 4)), temperatures=(0.0, 0.7, 1.0),
+                              top_ps=(0.5, 0.95, 1.0), sigma=2.0)
+    sample = np.zeros(V, dtype=bool)
+    for v in range(32):
+        c = (v % 16) * 8 + v // 16
+        sample[c * 1024:(c + 1) * 1024] = True
+    for r in range(0, rows, 4):
+        w.logits[r, sample] += 3.0
+    res, ids, vals = run_gpu(w, k_max=1024, topk_cap=64)
+    _log("pool kernel guessed bound, k sweep", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
+
+
 def test_f16_input_finite_k(oracle):
     w = synth.config(4, rows=16)
     w.top_k[:] = np.array([1, 20, 50, 100] * 4, np.int32)
