@@ -254,6 +254,40 @@ def test_pool_row_kernel_guessed_bound_k_sweep(oracle):
     _log("pool kernel guessed bound, k sweep", compare(w, res, ids, vals, run_oracle(oracle, w, 64), 64))
 
 
+@pytest.mark.parametrize("it", range(8))
+def test_pool_row_kernel_random_batches(oracle, it):
+    # Seeded random batches for the large-pool kernel: k from 257 to 1,024, vocabularies of
+    # 131,072 to 262,144 (odd ones too), ties or not, -inf, f16 or f32, and rows whose
+    # first-bound sample is raised or lowered against the rest of the row.
+    rng = np.random.default_rng(4242 + it)
+    V = int(rng.choice([131072, 131075, 151936, 152064, 200000, 262144]))
+    rows = int(rng.choice([256, 300, 512]))
+    w = synth.random_workload(rows=rows, vocab=V, seed=int(rng.integers(1, 1 << 30)),
+                              ties=bool(rng.integers(0, 2)), neg_inf_frac=float(rng.choice([0.0, 0.1, 0.5])),
+                              k_choices=tuple(int(x) for x in rng.integers(257, 1025, 8)),
+                              temperatures=(0.0, 0.5, 1.0, 2.0), top_ps=(0.5, 0.9, 0.98, 1.0),
+                              sigma=float(rng.choice([1.0, 2.0, 3.0])))
+    nch = -(-V // 1024)
+    s = 1
+    while 32 * s <= nch:
+        s *= 2
+    sample = np.zeros(V, dtype=bool)
+    for v in range(32):
+        c = (v % 16) * s + v // 16
+        sample[c * 1024:min((c + 1) * 1024, V)] = True
+    for r in range(rows):
+        u = rng.random()
+        if u < 0.15:
+            w.logits[r, sample] += float(rng.uniform(0.5, 6.0))
+        elif u < 0.25:
+            w.logits[r, sample] -= float(rng.uniform(0.5, 6.0))
+    if rng.random() < 0.3:
+        w.logits = w.logits.astype(np.float16)
+    res, ids, vals = run_gpu(w, k_max=1024, topk_cap=32)
+    _log(f"pool kernel random batch {it} (V={V}, rows={rows}, {w.logits.dtype})",
+         compare(w, res, ids, vals, run_oracle(oracle, w, 32), 32))
+
+
 def test_f16_input_finite_k(oracle):
     w = synth.config(4, rows=16)
     w.top_k[:] = np.array([1, 20, 50, 100] * 4, np.int32)
