@@ -279,10 +279,15 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
     acc += !in ? 0.0 : T == 1.0 ? e : exp_nonpos(d / T);
     c[j] = acc;  // the thread's running sum of the scaled terms
   }
+  // At T = 1 the scaled terms are the exact ones: their total serves poolMass too (a different
+  // summation order, within poolMass's 1e-5), and the exact terms need no reduction of their own.
+  const bool t1 = T == 1.0;
   const double incl = wave_inclusive_scan(acc);
-  const double e_wave = wave_sum(e_sum);
   if (lane == kWaveSize - 1) sm.bs.d[wave] = incl;
-  if (lane == 0) sm.bs.d2[wave] = e_wave;
+  if (!t1) {
+    const double e_wave = wave_sum(e_sum);
+    if (lane == 0) sm.bs.d2[wave] = e_wave;
+  }
   if (threadIdx.x == 0) {
     sm.bs.slot = (uint32_t)count;
     sm.bs.slot2 = (uint32_t)count;
@@ -293,7 +298,7 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
 #pragma unroll
     for (int k = 0; k < NW; ++k) {
       scaled += sm.bs.d[k];
-      e_total += sm.bs.d2[k];
+      if (!t1) e_total += sm.bs.d2[k];
       if (k < wave) base += sm.bs.d[k];
     }
   } else {
@@ -301,9 +306,10 @@ __device__ __forceinline__ bool finish_row_fast(Smem &sm, const Launch &L, int r
     // unrolled loop above held too many of them in registers).
     const double waves_incl = wave_inclusive_scan(lane < NW ? sm.bs.d[lane] : 0.0);
     scaled = readlane_f64(waves_incl, NW - 1);
-    e_total = wave_sum(lane < NW ? sm.bs.d2[lane] : 0.0);
+    if (!t1) e_total = wave_sum(lane < NW ? sm.bs.d2[lane] : 0.0);
     if (wave > 0) base += readlane_f64(waves_incl, wave - 1);
   }
+  if (t1) e_total = scaled;
   const double pool = e_total / sum_exp;
   double r[PER];
 #pragma unroll
