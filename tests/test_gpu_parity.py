@@ -288,6 +288,31 @@ def test_pool_row_kernel_random_batches(oracle, it):
          compare(w, res, ids, vals, run_oracle(oracle, w, 32), 32))
 
 
+@pytest.mark.parametrize("it", range(16))
+def test_random_batches_every_launch_shape(oracle, it):
+    # Seeded random batches over every launch shape the plan picks: 1 to 600 rows, vocabularies
+    # of 1 to 200,000 (odd ones too), k_max 64 to 1,024 with k up to it and whole-vocabulary
+    # rows, ties, -inf, greedy and sampled rows, f16 or f32.
+    rng = np.random.default_rng(9000 + it)
+    rows = int(rng.choice([1, 2, 3, 7, 16, 64, 100, 129, 200, 256, 300, 512, 600]))
+    V = int(rng.choice([1, 5, 64, 1000, 4097, 16385, 49152, 100003, 131072, 151936, 200000]))
+    if rows * V > 600 * 151936:
+        V = 151936
+    kmax = int(rng.choice([64, 128, 256, 1024]))
+    kc = [int(k) for k in rng.integers(1, kmax + 1, 4)] + ([0] if rng.random() < 0.3 else [])
+    w = synth.random_workload(rows=rows, vocab=V, seed=int(rng.integers(1, 1 << 30)), ties=bool(rng.integers(0, 2)),
+                              neg_inf_frac=float(rng.choice([0.0, 0.05, 0.3])), k_choices=tuple(kc),
+                              temperatures=(0.0, 0.3, 0.7, 1.0, 2.0), top_ps=(0.5, 0.9, 0.98, 1.0),
+                              sigma=float(rng.choice([1.0, 3.0])))
+    w.logits[~np.isfinite(w.logits).any(axis=1), 0] = 0.0  # no row of only -inf (outside the contract)
+    if rng.random() < 0.3:
+        w.logits = w.logits.astype(np.float16)
+    cap = min(kmax, 32)
+    res, ids, vals = run_gpu(w, k_max=kmax, topk_cap=cap)
+    _log(f"random batch {it} (rows={rows}, V={V}, k_max={kmax}, {w.logits.dtype})",
+         compare(w, res, ids, vals, run_oracle(oracle, w, cap), cap))
+
+
 def test_f16_input_finite_k(oracle):
     w = synth.config(4, rows=16)
     w.top_k[:] = np.array([1, 20, 50, 100] * 4, np.int32)
