@@ -3734,7 +3734,7 @@ __device__ __forceinline__ int pool_sample_stride(int nchunks) {
   return s;
 }
 
-constexpr int kPoolHistPad = kBins + kBins / 32;  // one pad word per 32 bins (pool_pass)
+constexpr int kPoolHistPad = kBins + kBins / 8;  // four pad words per 32 bins (pool_pass)
 
 struct PoolSmem {
   union {
@@ -3746,7 +3746,7 @@ struct PoolSmem {
     } tail;  // finish_row's terms, once the pool is in `sorted`
     uint64_t merge[kKcapLarge];  // the sort's second buffer, before those
   } u;
-  union {
+  union alignas(16) {  // (pool_pass reads and clears the histogram 16 bytes at a time)
     uint32_t hist[kPoolHistPad];
     uint64_t sorted[kKcapLarge];  // the row's pool, gathered after the last selection pass
   };
@@ -3762,14 +3762,15 @@ static_assert(kKcapLarge <= kPoolThreads, "block_merge_sort_desc sorts one entry
 
 // One histogram pass of the pool kernel's selections, by the whole workgroup: the entries
 // that bin_of admits (bin >= 0; bin 0 holds the largest) are counted, and wave 0 finds the
-// bin where the count from the top reaches `need` (each lane scans 32 consecutive bins,
-// stored one pad word per 32 so that the lanes' reads fall in different banks). Returns the
-// bin, the entries in the bins above it and the entries in it.
+// bin where the count from the top reaches `need` (each lane reads its 32 consecutive bins as
+// eight 16-byte words, stored four pad words per 32 so that every lane's bins start 16-byte
+// aligned and eight lanes' reads cover the 32 banks). Returns the bin, the entries in the bins
+// above it and the entries in it.
 struct PoolBin {
   uint32_t bin, above, count;
 };
 
-__device__ __forceinline__ int pool_hist_at(int b) { return b + (b >> 5); }
+__device__ __forceinline__ int pool_hist_at(int b) { return b + ((b >> 5) << 2); }
 
 // The selection visits the candidate list in batches: `batches(g)` loads kPoolBatch entries
 // per lane (all in flight before the first is used) and calls g(v, ok) with them; each_of
@@ -3839,22 +3840,26 @@ __device__ __forceinline__ PoolBin pool_pass(PoolSmem &sm, Batches &batches, Bin
     // that lane's 32 bins each and a second scan finds the bin (a walk of the owner's bins by
     // the owner alone was a chain of up to 31 dependent LDS reads).
     constexpr int PER = kBins / kWaveSize;
+    constexpr int kStride = PER + 4;  // a lane's bins and their pad, in words
     const int lane = wave_lane();
     uint32_t sum = 0u;
-    static_assert(PER == 32, "pool_hist_at pads one word per 32 bins: a lane's bins are lane * 33 + q");
-    uint32_t *mine = sm.hist + lane * (PER + 1);
-#pragma unroll 8
-    for (int q = 0; q < PER; ++q) sum += mine[q];
+    static_assert(PER == 32 && kStride % 4 == 0, "pool_hist_at: a lane's bins are lane * 36 + q, 16-byte aligned");
+    u32x4 *mine = reinterpret_cast<u32x4 *>(sm.hist + lane * kStride);
+    u32x4 h[PER / 4];
+#pragma unroll
+    for (int q = 0; q < PER / 4; ++q) h[q] = mine[q];
+#pragma unroll
+    for (int q = 0; q < PER / 4; ++q) sum += h[q].x + h[q].y + h[q].z + h[q].w;
     const uint32_t inc = wave_inclusive_scan_u32(sum);
     // need <= the total: some lane's running sum reaches it (else the last lane, whose
     // reads stay inside the histogram).
     const uint64_t got = __ballot(inc >= need);
     const int owner = got ? __ffsll((unsigned long long)got) - 1 : kWaveSize - 1;
     const uint32_t before = (uint32_t)__builtin_amdgcn_readlane((int)(inc - sum), owner);
-    const uint32_t c = lane < PER ? sm.hist[owner * (PER + 1) + lane] : 0u;
+    const uint32_t c = lane < PER ? sm.hist[owner * kStride + lane] : 0u;
     // Zero for the next pass (after the reads above: a wave's LDS operations complete in order).
-#pragma unroll 8
-    for (int q = 0; q < PER; ++q) mine[q] = 0u;
+#pragma unroll
+    for (int q = 0; q < PER / 4; ++q) mine[q] = u32x4{0u, 0u, 0u, 0u};
     const uint32_t cum = before + wave_inclusive_scan_u32(c);
     // The owner's last bin holds it if none before does.
     const uint64_t reach = __ballot(lane < PER - 1 && cum >= need);
